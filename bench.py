@@ -1,0 +1,249 @@
+#!/usr/bin/env python3
+"""Benchmark of the frozen-weight matmul path on one MI355X.
+
+Headline (BASELINE.json metric "q4_K dequant-matmul GB/s (M=1) & TFLOPS
+(M=512)"): a step is one decode GEMV (tiermm_qgemv) of the north-star q4_K
+weight 13824x5120 (W ~N(0,0.02) quantized by the host quantizer, x ~N(0,1)),
+inputs resident in HBM.  The weight is rotated over enough copies (> 256 MiB in
+total) that the 256 MiB Infinity Cache cannot hold them, so each step streams
+its weight from HBM.  ``value`` is the whole-run rate: algorithmic bytes of K
+steps / wall time between HIP events recorded around them on the stream the
+kernels run on.  ``roofline.achieved`` uses the kernel's own average duration
+(an event pair around each launch).
+
+Secondary measurements in the same JSON line (``secondary``): the other config
+shapes at M=1, q8_0 4096x4096 (config 1), the fused-path quantized GEMM at
+M=512 (config 3, TFLOPS against fp16 peak/3) and the x3-2x2 GEMM at M=4096
+(config 2).
+
+``cpu_baseline``: the reference's own q_val GEMV (oracle/_ref, compiled from
+quant.h) on the host's threads, on the same weight (timed over a bounded number
+of repetitions).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2516.6          # dense MFMA, 256 CU x 2.4 GHz x 4096 FLOP/clk
+X3_PEAK_TFLOPS = FP16_PEAK_TFLOPS / 3
+MALL_BYTES = 256 << 20
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def gemv_bytes(N: int, K: int, rb: int) -> int:
+    return N * rb + 4 * K + 4 * N
+
+
+class GemvCase:
+    """A quantized weight rotated over `copies` device buffers, plus x and y."""
+
+    def __init__(self, tier_amd, hip, qtype: int, N: int, K: int, seed: int):
+        rng = np.random.default_rng(seed)
+        w = (rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
+        self.blocks = tier_amd.q_row(qtype, w)
+        del w
+        self.qtype, self.N, self.K = qtype, N, K
+        self.rb = tier_amd.q_row_bytes(qtype, K)
+        nbytes = N * self.rb
+        self.copies = max(2, -(-(MALL_BYTES * 5 // 4) // nbytes))
+        self.W = [hip.to_device(self.blocks)]
+        for _ in range(self.copies - 1):
+            b = hip.DeviceBuffer(nbytes)
+            hip.copy_d2d(b.ptr, self.W[0].ptr, nbytes)
+            self.W.append(b)
+        self.x = rng.standard_normal(K).astype(np.float32)
+        self.X = hip.to_device(self.x)
+        self.Y = hip.DeviceBuffer(N * 4)
+        self.bytes = gemv_bytes(N, K, self.rb)
+
+    def launch(self, tier_amd, i: int, stream) -> None:
+        tier_amd.gemv_q(self.W[i % self.copies].ptr, self.qtype, self.rb, self.X.ptr, self.Y.ptr, self.N, self.K,
+                        stream)
+
+
+def time_launches(hip, stream, launch, steps: int, warmup: int):
+    """Returns (wall_ms over `steps` back-to-back launches, mean per-launch kernel ms from event pairs)."""
+    for i in range(warmup):
+        launch(i)
+    stream.synchronize()
+    # whole-run timing: back-to-back launches between two events
+    t0, t1 = hip.Event(), hip.Event()
+    t0.record(stream)
+    for i in range(steps):
+        launch(warmup + i)
+    t1.record(stream)
+    t1.synchronize()
+    wall = t0.elapsed_ms(t1)
+    # per-launch kernel time: an event pair around each launch
+    pairs = [(hip.Event(), hip.Event()) for _ in range(steps)]
+    for i, (a, b) in enumerate(pairs):
+        a.record(stream)
+        launch(warmup + steps + i)
+        b.record(stream)
+    pairs[-1][1].synchronize()
+    per = [a.elapsed_ms(b) for a, b in pairs]
+    for e in (t0, t1):
+        e.destroy()
+    for a, b in pairs:
+        a.destroy()
+        b.destroy()
+    return wall, float(np.mean(per)), float(np.median(per))
+
+
+def cpu_baseline(case: GemvCase, budget_s: float):
+    """The reference q_val GEMV (oracle/_ref, built from quant.h) on every host thread; bounded repetitions."""
+    import oracle
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    W = np.ascontiguousarray(case.blocks)
+    if oracle.ref_available():
+        kind = "reference"
+        run = lambda: oracle.ref_gemv_threads(W, case.qtype, case.x, case.N, case.K, threads)  # noqa: E731
+    else:  # the C restatement, single thread (lane order of gemv_q)
+        kind, threads = "port", 1
+        run = lambda: oracle.gemv_lanes(W, case.qtype, case.x, case.N, case.K, 64)  # noqa: E731
+    run()
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        run()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= 200:
+            break
+    gbs = case.bytes * reps / el / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+            "sample": f"{reps} full {case.N}x{case.K} q4_K GEMVs ({el:.1f} s wall, {el * threads:.0f} thread-s)"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the host baseline")
+    ap.add_argument("--no-secondary", action="store_true", help="headline only")
+    ap.add_argument("--cpu-seconds", type=float, default=3.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
+              file=sys.stderr)
+        return 2
+
+    import tier_amd
+    from tier_amd import hip
+
+    hip.set_device(0)
+    tier_amd.init(0)
+    cus = hip.attribute(hip.ATTR_MULTIPROCESSORS)
+    clk_mhz = hip.attribute(hip.ATTR_CLOCK_RATE_KHZ) / 1000.0
+    stream = hip.Stream()
+
+    # ---------------------------------------------------------------- headline
+    log("bench: preparing q4_K 13824x5120 GEMV inputs")
+    head = GemvCase(tier_amd, hip, tier_amd.Q4_K, 13824, 5120, seed=3)
+    wall, kmean, kmed = time_launches(hip, stream, lambda i: head.launch(tier_amd, i, stream), args.steps, args.warmup)
+    value = head.bytes * args.steps / (wall * 1e-3) / 1e9
+    achieved = head.bytes / (kmean * 1e-3) / 1e9
+    log(f"bench: q4_K GEMV {wall / args.steps * 1e3:.2f} us/step wall, {kmean * 1e3:.2f} us/launch kernel")
+
+    secondary = {}
+    if not args.no_secondary:
+        reps, warm = max(20, args.steps // 4), 5
+        for name, qt, N, K in (("q4_K_5120x5120_m1", tier_amd.Q4_K, 5120, 5120),
+                               ("q4_K_14336x5120_m1", tier_amd.Q4_K, 14336, 5120),
+                               ("q4_K_5120x14336_m1", tier_amd.Q4_K, 5120, 14336),
+                               ("q8_0_4096x4096_m1", tier_amd.Q8_0, 4096, 4096)):
+            log(f"bench: {name}")
+            c = GemvCase(tier_amd, hip, qt, N, K, seed=N + K)
+            w, km, _ = time_launches(hip, stream, lambda i: c.launch(tier_amd, i, stream), reps, warm)
+            secondary[name] = {"GB/s": round(c.bytes / (km * 1e-3) / 1e9, 1),
+                               "frac_hbm": round(c.bytes / (km * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                               "us_kernel": round(km * 1e3, 2), "us_wall_per_step": round(w / reps * 1e3, 2)}
+            del c
+        # quantized GEMM at M=512 (config 3), x3-ref semantics
+        for name, N, K in (("q4_K_5120x5120_m512", 5120, 5120), ("q4_K_14336x5120_m512", 14336, 5120),
+                           ("q4_K_5120x14336_m512", 5120, 14336)):
+            log(f"bench: {name}")
+            M = 512
+            rng = np.random.default_rng(N * 7 + K)
+            blocks = tier_amd.q_row(tier_amd.Q4_K, rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
+            Wd = hip.to_device(blocks)
+            X = hip.to_device(rng.standard_normal((M, K), dtype=np.float32))
+            Y = hip.DeviceBuffer(M * N * 4)
+            wsb = tier_amd.qgemm_ws_bytes(tier_amd.Q4_K, M, N, K)
+            WS = hip.DeviceBuffer(wsb)
+            rb = tier_amd.q_row_bytes(tier_amd.Q4_K, K)
+            f = lambda i: tier_amd.qgemm(Wd.ptr, tier_amd.Q4_K, rb, X.ptr, Y.ptr, M, N, K, N,  # noqa: E731
+                                         tier_amd.MODE_X3REF, 0.0, WS.ptr, wsb, stream)
+            w, km, _ = time_launches(hip, stream, f, 10, 3)
+            tf = 2.0 * M * N * K / (km * 1e-3) / 1e12
+            secondary[name] = {"TFLOPS": round(tf, 2), "frac_x3_peak": round(tf / X3_PEAK_TFLOPS, 4),
+                               "us_per_call": round(km * 1e3, 1)}
+            del Wd, X, Y, WS
+        # x3-2x2 GEMM, config 2
+        log("bench: x3s_4096x5120x5120")
+        M, N, K = 4096, 5120, 5120
+        rng = np.random.default_rng(8)
+        Wf = hip.to_device(rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
+        Xf = hip.to_device(rng.standard_normal((M, K), dtype=np.float32))
+        bufs = [hip.DeviceBuffer(n) for n in (M * K * 2, M * K * 2, M * 4, N * K * 2, N * K * 2, N * 4, M * N * 4)]
+        xh, xl, xe, wh, wl, we, Y = bufs
+        tier_amd.x3s_split(Wf.ptr, wh.ptr, wl.ptr, we.ptr, N, K, stream)
+        f = lambda i: (tier_amd.x3s_split(Xf.ptr, xh.ptr, xl.ptr, xe.ptr, M, K, stream),  # noqa: E731
+                       tier_amd.x3s_gemm(xh.ptr, xl.ptr, xe.ptr, wh.ptr, wl.ptr, we.ptr, Y.ptr, M, N, K, N, stream))
+        w, km, _ = time_launches(hip, stream, f, 10, 3)
+        tf = 2.0 * M * N * K / (km * 1e-3) / 1e12
+        secondary["x3s_4096x5120x5120"] = {"TFLOPS": round(tf, 2), "frac_x3_peak": round(tf / X3_PEAK_TFLOPS, 4),
+                                           "us_per_call": round(km * 1e3, 1), "includes": "X split + GEMM"}
+        del bufs, Wf, Xf
+
+    cpu = None
+    if not args.no_cpu:
+        log("bench: cpu baseline")
+        try:
+            cpu = cpu_baseline(head, args.cpu_seconds)
+        except Exception as e:  # the baseline is reported, not required
+            log(f"bench: cpu baseline unavailable: {e}")
+
+    out = {
+        "metric": "q4_K dequant-matmul GB/s (M=1) & TFLOPS (M=512), % of MI355X roofline",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_K/fp32",
+        "data": "synthetic: W ~N(0,0.02) quantized to q4_K by the host quantizer, x ~N(0,1); "
+                f"weight rotated over {head.copies} HBM copies",
+        "config": {"workload": "q4_K decode GEMV 13824x5120 (M=1), tiermm_qgemv", "N": 13824, "K": 5120, "M": 1,
+                   "bytes_per_step": head.bytes},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel_us_mean": round(kmean * 1e3, 3), "kernel_us_median": round(kmed * 1e3, 3)},
+        "cpu_baseline": cpu,
+        "device": {"cus": cus, "clock_mhz": clk_mhz},
+        "secondary": secondary,
+    }
+    print(json.dumps(out), flush=True)
+    stream.destroy()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,179 @@
+/*
+ * tiermm.h -- C ABI of libtiermm.so, the MI355X (gfx950) frozen-weight matmul
+ * path of tierlm: GGUF block dequantization fused into GEMV/GEMM, and the
+ * "x3" split-precision fp16 GEMM.
+ *
+ * The reference engine (tier/tier.cpp) has no shared library: these entry
+ * points replace the engine-internal functions cited on each one, keeping their
+ * argument meaning so a tier.cpp-like engine can call them in place of the
+ * originals.
+ *
+ * Conventions
+ *  - Matrices are row-major.  A weight is W[N][K] (N = out_features rows,
+ *    K = in_features cols); a quantized row is rb = K/blk*blk_bytes bytes,
+ *    rows contiguous (quant.h:33, tier.cpp:288).  Activations X[M][K] fp32,
+ *    outputs Y[M][ldy] fp32.
+ *  - Every tensor argument is a DEVICE pointer allocated by the caller, except
+ *    for tiermm_quantize (host memory).  Nothing here frees caller memory.
+ *  - Calls are stream-ordered and asynchronous: no host synchronisation, no
+ *    device allocation on the hot path.  A NULL stream is the null stream.
+ *  - Status: TIERMM_OK (0); TIERMM_UNSUPPORTED (1) when a shape/type/layout is
+ *    not handled (the caller falls back, as the engine does when
+ *    tw::launch() returns false, tier_wmma.h:81, or chat_fp3() returns false,
+ *    tier.cpp:2368); TIERMM_EINVAL (2) for a bad argument; a negative value is
+ *    -(hipError_t) of a failed HIP call.  No call exits the process (the
+ *    reference's HIP_CHECK does, tier.cpp:63-64); tiermm_last_error() gives the
+ *    text of the last failure on the calling thread.
+ *  - Workspace (ws, ws_bytes): entry points that need scratch take it
+ *    explicitly; *_ws_bytes() returns the size.  ws == NULL selects a pool the
+ *    library grows per device (allocation happens on that call, outside any
+ *    graph capture) and frees in tiermm_shutdown(); calls that share the pool
+ *    must be ordered on one stream.
+ */
+#ifndef TIERMM_H
+#define TIERMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* tiermm_stream_t; /* a hipStream_t */
+
+enum {
+  TIERMM_OK = 0,
+  TIERMM_UNSUPPORTED = 1,
+  TIERMM_EINVAL = 2
+};
+
+/* ggml type ids, as quant.h:21-24 numbers them. */
+enum {
+  TIERMM_F32 = 0,
+  TIERMM_F16 = 1,
+  TIERMM_Q5_0 = 6,
+  TIERMM_Q8_0 = 8,
+  TIERMM_Q4_K = 12,
+  TIERMM_Q5_K = 13,
+  TIERMM_Q6_K = 14,
+  TIERMM_BF16 = 30
+};
+
+/* element type of a dequantized output (dq_k<T>, tier.cpp:294: float, tier_fp16, hip_bfloat16) */
+enum { TIERMM_OUT_F32 = 0, TIERMM_OUT_F16 = 1, TIERMM_OUT_BF16 = 2 };
+
+/* split layouts: TIERMM_HML = planes hi,mid,lo at 0, s, 2s (fp3gemm, tier.cpp:925);
+ * TIERMM_LMH = lo,mid,hi (split3s_fp16, tier.cpp:2193-2194) */
+enum { TIERMM_HML = 0, TIERMM_LMH = 1 };
+
+/* BLAS operation of the weight operand in tiermm_x3_gemm (hipblasOperation_t values) */
+enum { TIERMM_OP_N = 111, TIERMM_OP_T = 112 };
+
+/* quantized-GEMM semantics: X3REF = fp16 dequant then x3 (training path,
+ * tier.cpp:515 + 922); F32 = fp32 dequant then fp32 GEMM (chat prefill path,
+ * tier.cpp:2358-2359). */
+enum { TIERMM_MODE_X3REF = 0, TIERMM_MODE_F32 = 1 };
+
+/* ------------------------------------------------------------------ library */
+/* Select `device` (hipSetDevice) and set up per-device state.  Replaces the
+ * engine's lazy global set-up (g_lt/g_lt_ws/g_own_tmp, tier.cpp:923-924). */
+int tiermm_init(int device);
+/* Free the library's pools on every device it used. */
+void tiermm_shutdown(void);
+/* Text of the last error raised on the calling thread ("" if none). */
+const char* tiermm_last_error(void);
+const char* tiermm_version(void);
+
+/* ---------------------------------------------------- block-format registry */
+/* quant.h:25-31 q_info: elements and bytes per block of `qtype`.
+ * TIERMM_UNSUPPORTED for an unknown id. */
+int tiermm_q_info(int qtype, int* blk_elems, int* blk_bytes);
+/* quant.h:33-34 q_row_bytes + q_cols_ok: *rb = cols/blk*blk_bytes.
+ * TIERMM_UNSUPPORTED if cols is not a whole number of blocks. */
+int tiermm_q_row_bytes(int qtype, int cols, size_t* rb);
+
+/* ----------------------------------------------------------------- dequant */
+/* dq_k<T> / dq_launch (tier.cpp:293-298): for i < nrows*cols,
+ * out[i] = T(q_val(W + (r0 + i/cols)*rb, qtype, i%cols)), T = fp32, fp16
+ * (round to nearest even, subnormals kept, as tier_fp16) or bf16 (RNE, as
+ * hip_bfloat16).  qtype in {Q8_0, Q5_0, Q4_K, Q5_K, Q6_K}.  Bit-exact with
+ * the reference's q_val for finite block scales. */
+int tiermm_dequant(const void* W, int qtype, size_t rb, int cols, size_t r0, size_t nrows,
+                   void* out, int out_dtype, tiermm_stream_t stream);
+
+/* --------------------------------------------------------------- decode GEMV */
+/* gemv_q (tier.cpp:299-306, launched at 2357): y[r] = sum_k q_val(W_r, k) * x[k]
+ * for r < N, fp32 accumulation.  W: N rows of rb bytes; x: K fp32; y: N fp32.
+ * qtype in {Q8_0, Q5_0, Q4_K, Q5_K, Q6_K}. */
+int tiermm_qgemv(const void* W, int qtype, size_t rb, const float* x, float* y, int N, int K,
+                 tiermm_stream_t stream);
+
+/* --------------------------------------------------------------- x3 splits */
+/* split3_fp_k (tier.cpp:869-870) / split3s_fp16 (tier.cpp:2192-2194):
+ * h = fp16(v); m = fp16(v - h); l = fp16(v - h - m) (fp32 subtractions), for
+ * i < n; written as planes at parts + {0, part_stride, 2*part_stride} in the
+ * given order (TIERMM_HML or TIERMM_LMH).  part_stride >= n. */
+int tiermm_split3_f16(const float* x, uint16_t* parts, size_t n, size_t part_stride, int order,
+                      tiermm_stream_t stream);
+
+/* ------------------------------------------------------------ x3-ref GEMM */
+/* fp3gemm (tier.cpp:922-943) in its BLAS column-major contract:
+ * C(m x n) = op(A)(m x k) * B(k x n) + beta * C, A fp16 (the frozen weight,
+ * exact), B fp32 split into three fp16 parts; the three products run on fp16
+ * MFMA with fp32 accumulation.  With opA = TIERMM_OP_T and lda = k this is the
+ * forward linear out[n][m] = x[n][k] * W[m][k]^T (low3_linear, tier.cpp:1212);
+ * ldc >= m.  opA = TIERMM_OP_N (the dX layout, tier.cpp:1226) returns
+ * TIERMM_UNSUPPORTED in this version.  Accuracy: rel. Frobenius error <= 2^-20
+ * against fp64(A * B). */
+int tiermm_x3_gemm(int opA, int m, int n, int k, const uint16_t* A, int lda, const float* B,
+                   float beta, float* C, int ldc, void* ws, size_t ws_bytes,
+                   tiermm_stream_t stream);
+size_t tiermm_x3_gemm_ws_bytes(int m, int n, int k);
+
+/* chat_fp3 (tier.cpp:2195-2219): y[M][ldo] = x[M][K] * W[N][K]^T with x split
+ * into three fp16 parts and W fp16, fp32 accumulation (the reference sums the
+ * parts as (lo + mid) + hi, add3ld tier.cpp:2162-2164). ldo >= N. */
+int tiermm_x3_rows(const uint16_t* W, const float* x, float* y, int M, int K, int N, int ldo,
+                   void* ws, size_t ws_bytes, tiermm_stream_t stream);
+size_t tiermm_x3_rows_ws_bytes(int M, int K, int N);
+
+/* ------------------------------------------------------------ x3-2x2 GEMM */
+/* Two-part split with a power-of-two exponent per row (the storage of the 2x2
+ * x3 GEMM; README.md:21 describes it, no reference function exists):
+ * e_r = 14 - floor(log2(max_k |src[r][k]|)) (0 for an all-zero row, clamped
+ * to [-100, 100]); hi = fp16(src * 2^e_r); lo = fp16(src * 2^e_r - hi).
+ * exps[r] = e_r.  Scaling keeps lo out of the fp16 subnormal range. */
+int tiermm_x3s_split(const float* src, uint16_t* hi, uint16_t* lo, int32_t* exps, int rows,
+                     int cols, tiermm_stream_t stream);
+/* Y[M][ldy] = 2^-(xexp[m] + wexp[n]) * (Xhi*Whi^T + Xhi*Wlo^T + Xlo*Whi^T), the
+ * three products on fp16 MFMA accumulated in fp32.  X*: [M][K], W*: [N][K].
+ * Accuracy: rel. Frobenius error <= 2^-20 against fp64(X * W^T). */
+int tiermm_x3s_gemm(const uint16_t* Xhi, const uint16_t* Xlo, const int32_t* xexp,
+                    const uint16_t* Whi, const uint16_t* Wlo, const int32_t* wexp, float* Y,
+                    int M, int N, int K, int ldy, tiermm_stream_t stream);
+
+/* -------------------------------------------------------- quantized GEMM */
+/* The M > 1 quantized linear: Y[M][ldy] = X[M][K] * dequant(W)^T + beta * Y.
+ * mode TIERMM_MODE_X3REF: W is dequantized to fp16 (bit-exact with dq_k<tier_fp16>,
+ * tier.cpp:515) inside the kernel and multiplied with x split in three fp16
+ * parts (fp3gemm semantics, tier.cpp:922): rel. Frobenius error <= 2^-20
+ * against fp64(fp16deq(W) * X).  TIERMM_MODE_F32 is reserved (returns
+ * TIERMM_UNSUPPORTED).  qtype in {Q8_0, Q5_0, Q4_K, Q5_K, Q6_K}. */
+int tiermm_qgemm(const void* W, int qtype, size_t rb, const float* X, float* Y, int M, int N,
+                 int K, int ldy, int mode, float beta, void* ws, size_t ws_bytes,
+                 tiermm_stream_t stream);
+size_t tiermm_qgemm_ws_bytes(int qtype, int M, int N, int K, int mode);
+
+/* ------------------------------------------------------ host quantizer */
+/* q_row (quant.h:201-204) over `rows` rows of `cols` host floats, writing
+ * rows*rb bytes of blocks to host memory `out`: Q8_0 (quant.h:134-136),
+ * Q4_K/Q5_K (qk_minmax_row, quant.h:138-173), Q6_K (q6_k_row, quant.h:175-199);
+ * byte-identical with the reference.  Rows are split over `nthreads` host
+ * threads (<= 0: all hardware threads). */
+int tiermm_quantize(int qtype, const float* x, void* out, size_t rows, int cols, int nthreads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TIERMM_H */

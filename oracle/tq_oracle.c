@@ -1,0 +1,256 @@
+/*
+ * tq_oracle.c -- CPU restatement of the reference's frozen-weight matmul path.
+ *
+ * TEST INFRASTRUCTURE ONLY: loaded by tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py as the checker; never by the product.
+ * Built with -ffp-contract=off so every fp32 expression rounds exactly where
+ * the written C rounds.  See tq_oracle.h for what pins each function.
+ */
+#include "tq_oracle.h"
+
+#include <math.h>
+#include <string.h>
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+static inline uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+static inline uint32_t rd32(const uint8_t* p) {
+  return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+/* (type, elements per block, bytes per block): the table of quant.h:26-30. */
+static const int QTAB[][3] = {
+  {0, 1, 4}, {1, 1, 2}, {30, 1, 2}, {2, 32, 18}, {3, 32, 20}, {6, 32, 22}, {7, 32, 24},
+  {8, 32, 34}, {10, 256, 84}, {11, 256, 110}, {12, 256, 144}, {13, 256, 176},
+  {14, 256, 210}, {16, 256, 66}, {17, 256, 74}, {22, 256, 82}, {18, 256, 98},
+  {21, 256, 110}, {19, 256, 50}, {29, 256, 56}, {20, 32, 18}, {23, 256, 136},
+  {34, 256, 54}, {35, 256, 66}, {39, 32, 17}, {200, 64, 36}, {201, 64, 36},
+};
+
+int orc_q_block(int type, int* blk_elems, int* blk_bytes) {
+  for (size_t i = 0; i < sizeof(QTAB) / sizeof(QTAB[0]); ++i)
+    if (QTAB[i][0] == type) {
+      if (blk_elems) *blk_elems = QTAB[i][1];
+      if (blk_bytes) *blk_bytes = QTAB[i][2];
+      return 1;
+    }
+  return 0;
+}
+
+/* quant.h:33 q_row_bytes: cols/blk*bytes (integer division), 0 for unknown types. */
+size_t orc_q_row_bytes(int type, int cols) {
+  int be, bb;
+  if (!orc_q_block(type, &be, &bb)) return 0;
+  return (size_t)cols / (size_t)be * (size_t)bb;
+}
+
+/* binary16 -> binary32, exact (quant.h:37-42, gpu_compat.h:175-190).
+ * Normal: (1024+m) * 2^(e-25); subnormal: m * 2^-24; inf/NaN keep the payload. */
+float orc_h2f(uint16_t h) {
+  const uint32_t sgn = (uint32_t)(h >> 15), e = (h >> 10) & 31u, m = h & 1023u;
+  if (e == 31u) return u2f((sgn << 31) | 0x7f800000u | (m << 13));
+  float v = (e == 0u) ? ldexpf((float)m, -24) : ldexpf((float)(m | 1024u), (int)e - 25);
+  return sgn ? -v : v;
+}
+
+/* binary32 -> binary16, round to nearest even (gpu_compat.h:151-174). */
+uint16_t orc_f2h(float f) {
+  const uint32_t u = f2u(f), sgn = (u >> 16) & 0x8000u, a = u & 0x7fffffffu;
+  if (a >= 0x7f800000u) return (uint16_t)(sgn | (a > 0x7f800000u ? 0x7e00u : 0x7c00u));
+  if (a >= 0x477ff000u) return (uint16_t)(sgn | 0x7c00u); /* >= 65520 rounds to inf */
+  if (a >= 0x38800000u) {                                  /* fp16 normal range */
+    uint32_t h = ((((a >> 23) - 112u)) << 10) | ((a >> 13) & 1023u);
+    const uint32_t rem = a & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h; /* carry may bump exponent */
+    return (uint16_t)(sgn | h);
+  }
+  if (a <= 0x33000000u) return (uint16_t)sgn; /* <= 2^-25: rounds to zero (tie to even) */
+  /* fp16 subnormal: count units of 2^-24 */
+  const uint32_t mant = (a & 0x7fffffu) | 0x800000u;
+  const int sh = 126 - (int)(a >> 23); /* value = mant * 2^(E-23), E=(a>>23)-127 */
+  uint32_t q = mant >> sh;
+  const uint32_t rem = mant & ((1u << sh) - 1u), half = 1u << (sh - 1);
+  if (rem > half || (rem == half && (q & 1u))) ++q;
+  return (uint16_t)(sgn | q);
+}
+
+/* hip_bfloat16(float): keep the top 16 bits, round to nearest even; NaN stays NaN. */
+uint16_t orc_f2bf(float f) {
+  const uint32_t u = f2u(f);
+  uint32_t hi = u >> 16;
+  if ((u & 0x7f800000u) == 0x7f800000u) return (uint16_t)((u & 0xffffu) ? (hi | 1u) : hi);
+  const uint32_t rem = u & 0xffffu;
+  if (rem > 0x8000u || (rem == 0x8000u && (hi & 1u))) ++hi;
+  return (uint16_t)hi;
+}
+
+void orc_f2h_n(const float* x, uint16_t* h, size_t n) {
+  for (size_t i = 0; i < n; ++i) h[i] = orc_f2h(x[i]);
+}
+void orc_h2f_n(const uint16_t* h, float* x, size_t n) {
+  for (size_t i = 0; i < n; ++i) x[i] = orc_h2f(h[i]);
+}
+void orc_f2bf_n(const float* x, uint16_t* b, size_t n) {
+  for (size_t i = 0; i < n; ++i) b[i] = orc_f2bf(x[i]);
+}
+
+static inline float fp16_at(const uint8_t* p) { return orc_h2f(rd16(p)); }
+
+/* 6-bit scale/min pair s (0..7) of a q4_K/q5_K super-block (quant.h:47-48). */
+static void kq_scale_min(int s, const uint8_t* q, int* sc, int* mn) {
+  if (s < 4) {
+    *sc = q[s] & 63;
+    *mn = q[s + 4] & 63;
+  } else {
+    *sc = (q[s + 4] & 15) | ((q[s - 4] >> 6) << 4);
+    *mn = (q[s + 4] >> 4) | ((q[s] >> 6) << 4);
+  }
+}
+
+/* One element of a quantized row (quant.h:59-121, the types this path uses). */
+float orc_q_val(const uint8_t* row, int type, int col) {
+  switch (type) {
+    case ORC_F32: return u2f(rd32(row + (size_t)col * 4));
+    case ORC_F16: return orc_h2f(rd16(row + (size_t)col * 2));
+    case ORC_BF16: return u2f((uint32_t)rd16(row + (size_t)col * 2) << 16);
+    case ORC_Q8_0: { /* quant.h:68: d fp16 @0, int8 q[32] @2 */
+      const uint8_t* b = row + (size_t)(col / 32) * 34;
+      return fp16_at(b) * (float)(int8_t)b[2 + col % 32];
+    }
+    case ORC_Q4_0: { /* quant.h:64: d @0, qs[16] @2; element i<16 low nibble, else high */
+      const uint8_t* b = row + (size_t)(col / 32) * 18;
+      const int i = col % 32, v = (b[2 + i % 16] >> (i < 16 ? 0 : 4)) & 15;
+      return fp16_at(b) * (float)(v - 8);
+    }
+    case ORC_Q4_1: { /* quant.h:65: d @0, m @2, qs @4 */
+      const uint8_t* b = row + (size_t)(col / 32) * 20;
+      const int i = col % 32, v = (b[4 + i % 16] >> (i < 16 ? 0 : 4)) & 15;
+      return fp16_at(b) * (float)v + fp16_at(b + 2);
+    }
+    case ORC_Q5_0: { /* quant.h:66: d @0, qh u32 @2, qs @6; bit 4 = qh bit i */
+      const uint8_t* b = row + (size_t)(col / 32) * 22;
+      const int i = col % 32;
+      const int v = ((b[6 + i % 16] >> (i < 16 ? 0 : 4)) & 15) | (int)(((rd32(b + 2) >> i) & 1u) << 4);
+      return fp16_at(b) * (float)(v - 16);
+    }
+    case ORC_Q5_1: { /* quant.h:67: d @0, m @2, qh @4, qs @8 */
+      const uint8_t* b = row + (size_t)(col / 32) * 24;
+      const int i = col % 32;
+      const int v = ((b[8 + i % 16] >> (i < 16 ? 0 : 4)) & 15) | (int)(((rd32(b + 4) >> i) & 1u) << 4);
+      return fp16_at(b) * (float)v + fp16_at(b + 2);
+    }
+    default: break;
+  }
+  const int i = col % 256; /* position inside a 256-element super-block */
+  switch (type) {
+    case ORC_Q4_K: { /* quant.h:83-84: d @0, dmin @2, scales[12] @4, qs[128] @16 */
+      const uint8_t* b = row + (size_t)(col / 256) * 144;
+      const int grp = i / 64, l = i % 64;
+      int sc, mn;
+      kq_scale_min(2 * grp + (l >= 32), b + 4, &sc, &mn);
+      const uint8_t byte = b[16 + 32 * grp + l % 32];
+      const int v = (l < 32) ? (byte & 15) : (byte >> 4);
+      return (fp16_at(b) * (float)sc) * (float)v - fp16_at(b + 2) * (float)mn;
+    }
+    case ORC_Q5_K: { /* quant.h:85-87: as Q4_K, qh[32] @16, qs[128] @48 */
+      const uint8_t* b = row + (size_t)(col / 256) * 176;
+      const int grp = i / 64, l = i % 64;
+      int sc, mn;
+      kq_scale_min(2 * grp + (l >= 32), b + 4, &sc, &mn);
+      const uint8_t byte = b[48 + 32 * grp + l % 32];
+      const int hbit = (b[16 + i % 32] >> (i / 32)) & 1;
+      const int v = ((l < 32) ? (byte & 15) : (byte >> 4)) | (hbit << 4);
+      return (fp16_at(b) * (float)sc) * (float)v - fp16_at(b + 2) * (float)mn;
+    }
+    case ORC_Q6_K: { /* quant.h:88-90: ql[128] @0, qh[64] @128, int8 sc[16] @192, d @208 */
+      const uint8_t* b = row + (size_t)(col / 256) * 210;
+      const int half128 = i / 128, r = i % 128;
+      const int lo4 = (b[64 * half128 + r % 64] >> (4 * (r / 64))) & 15;
+      const int hi2 = (b[128 + 32 * half128 + r % 32] >> (2 * (r / 32))) & 3;
+      const int q = (lo4 | (hi2 << 4)) - 32;
+      return (fp16_at(b + 208) * (float)(int8_t)b[192 + i / 16]) * (float)q;
+    }
+    default: return 0.f;
+  }
+}
+
+void orc_dequant(const uint8_t* W, int type, size_t rb, int cols, size_t r0, size_t nrows,
+                 void* out, int out_dtype) {
+  const size_t n = nrows * (size_t)cols;
+  for (size_t i = 0; i < n; ++i) {
+    const float v = orc_q_val(W + (r0 + i / (size_t)cols) * rb, type, (int)(i % (size_t)cols));
+    if (out_dtype == ORC_OUT_F32) ((float*)out)[i] = v;
+    else if (out_dtype == ORC_OUT_F16) ((uint16_t*)out)[i] = orc_f2h(v);
+    else ((uint16_t*)out)[i] = orc_f2bf(v);
+  }
+}
+
+void orc_gemv_f64(const uint8_t* W, int type, size_t rb, const float* x, double* y, int N, int K) {
+  for (int r = 0; r < N; ++r) {
+    const uint8_t* w = W + (size_t)r * rb;
+    double acc = 0.0;
+    for (int k = 0; k < K; ++k) acc += (double)orc_q_val(w, type, k) * (double)x[k];
+    y[r] = acc;
+  }
+}
+
+void orc_gemv_lanes(const uint8_t* W, int type, size_t rb, const float* x, float* y, int N, int K,
+                    int wave) {
+  float acc[128];
+  if (wave < 1 || wave > 128) return;
+  for (int r = 0; r < N; ++r) {
+    const uint8_t* w = W + (size_t)r * rb;
+    for (int l = 0; l < wave; ++l) {
+      float a = 0.f;
+      for (int k = l; k < K; k += wave) a = fmaf(orc_q_val(w, type, k), x[k], a);
+      acc[l] = a;
+    }
+    for (int o = wave / 2; o > 0; o /= 2)
+      for (int l = 0; l < o; ++l) acc[l] = acc[l] + acc[l + o];
+    y[r] = acc[0];
+  }
+}
+
+void orc_split3_f16(const float* x, uint16_t* parts, size_t n, size_t stride, int order) {
+  for (size_t i = 0; i < n; ++i) {
+    const float v = x[i];
+    const uint16_t h = orc_f2h(v);
+    const float r = v - orc_h2f(h);
+    const uint16_t m = orc_f2h(r);
+    const uint16_t l = orc_f2h(r - orc_h2f(m));
+    if (order == 0) {
+      parts[i] = h; parts[i + stride] = m; parts[i + 2 * stride] = l;
+    } else {
+      parts[i] = l; parts[i + stride] = m; parts[i + 2 * stride] = h;
+    }
+  }
+}
+
+int32_t orc_x3s_row_exp(const float* v, int cols) {
+  float amax = 0.f;
+  for (int k = 0; k < cols; ++k) {
+    const float a = fabsf(v[k]);
+    if (a > amax) amax = a;
+  }
+  if (!(amax > 0.f) || !isfinite(amax)) return 0;
+  int ex;
+  frexpf(amax, &ex); /* amax = f * 2^ex, f in [0.5,1): floor(log2 amax) = ex-1 */
+  int e = 15 - ex;
+  if (e < -100) e = -100;
+  if (e > 100) e = 100;
+  return e;
+}
+
+void orc_x3s_split(const float* v, uint16_t* hi, uint16_t* lo, int32_t* exps, int rows, int cols) {
+  for (int r = 0; r < rows; ++r) {
+    const float* row = v + (size_t)r * cols;
+    const int32_t e = orc_x3s_row_exp(row, cols);
+    exps[r] = e;
+    for (int k = 0; k < cols; ++k) {
+      const float s = ldexpf(row[k], e);
+      const uint16_t h = orc_f2h(s);
+      hi[(size_t)r * cols + k] = h;
+      lo[(size_t)r * cols + k] = orc_f2h(s - orc_h2f(h));
+    }
+  }
+}

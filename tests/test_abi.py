@@ -1,0 +1,101 @@
+"""The C ABI library on the CPU: it loads, exports every declared symbol, and its
+host-side code (registry, quantizer, argument checks) behaves like the reference.
+No kernel is launched here."""
+import os
+import re
+
+import numpy as np
+import pytest
+
+import oracle
+import tier_amd
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    text = open(os.path.join(ROOT, "include", "tiermm.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tiermm_\w+)\s*\(", text)))
+
+
+def test_exports_every_declared_symbol():
+    names = _declared()
+    assert len(names) >= 18
+    lib = tier_amd.lib()
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    assert sorted(tier_amd.EXPORTS) == names
+
+
+def test_registry_matches_oracle_table():
+    for t in (0, 1, 2, 3, 6, 7, 8, 10, 11, 12, 13, 14, 16, 17, 18, 19, 20, 21, 22, 23, 29, 30, 34, 35, 39, 200, 201):
+        assert tier_amd.q_info(t) == oracle.block(t)
+        be, _ = oracle.block(t)
+        for cols in (0, be, 256 * be, 5120 if 5120 % be == 0 else be * 3):
+            assert tier_amd.q_row_bytes(t, cols) == oracle.row_bytes(t, cols)
+    with pytest.raises(tier_amd.TiermmUnsupported):
+        tier_amd.q_info(99)
+    assert not tier_amd.q_cols_ok(tier_amd.Q4_K, 1408)  # F4: 1408 % 256 != 0
+    assert tier_amd.q_cols_ok(tier_amd.Q8_0, 1408)
+
+
+@pytest.mark.parametrize("name", ["q8_0", "q4_K", "q5_K", "q6_K"])
+def test_quantizer_bytes_match_reference_golden(golden, name):
+    g = golden["quant"]
+    t = {"q8_0": tier_amd.Q8_0, "q4_K": tier_amd.Q4_K, "q5_K": tier_amd.Q5_K, "q6_K": tier_amd.Q6_K}[name]
+    got = tier_amd.q_row(t, g["x"], nthreads=3)
+    assert np.array_equal(got, g[name])
+
+
+@pytest.mark.skipif(not oracle.ref_available(), reason="oracle/_ref not built (no reference checkout)")
+@pytest.mark.parametrize("t", [tier_amd.Q8_0, tier_amd.Q4_K, tier_amd.Q5_K, tier_amd.Q6_K])
+def test_quantizer_bytes_match_reference_build(t):
+    rng = np.random.default_rng(100 + t)
+    x = np.concatenate([rng.standard_normal((24, 2048)) * 0.02,
+                        rng.standard_normal((4, 2048)) * 30,       # large values
+                        np.zeros((2, 2048)),                       # all-zero rows
+                        rng.standard_normal((2, 2048)) * 1e-9]).astype(np.float32)
+    x[0, :256] = 0.0
+    x[1, 5] = 1e3  # an outlier inside one block
+    assert np.array_equal(tier_amd.q_row(t, x), oracle.ref_quantize(x, t))
+
+
+@pytest.mark.parametrize("t,lim", [(tier_amd.Q8_0, 0.007), (tier_amd.Q6_K, 0.022), (tier_amd.Q5_K, 0.042),
+                                   (tier_amd.Q4_K, 0.08)])
+def test_quantizer_error_bounds(t, lim):
+    """check_quant.py:105-120: rel. Frobenius error of quantize->dequant on N(0,0.02) rows."""
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal((32, 4096)) * 0.02).astype(np.float32)
+    back = oracle.dequant(tier_amd.q_row(t, x), t, 4096)
+    assert oracle.rel_fro(back, x) <= lim
+
+
+def test_argument_checks_return_before_device_work():
+    L = tier_amd.lib()
+    # unknown / unhandled type
+    assert L.tiermm_dequant(16, 16, 66, 256, 0, 1, 16, tier_amd.OUT_F16, None) == tier_amd.UNSUPPORTED
+    # rb inconsistent with cols
+    assert L.tiermm_dequant(16, tier_amd.Q4_K, 100, 256, 0, 1, 16, tier_amd.OUT_F16, None) == tier_amd.EINVAL
+    # misaligned Q4_K rows
+    assert L.tiermm_qgemv(18, tier_amd.Q4_K, 144, 16, 16, 1, 256, None) == tier_amd.EINVAL
+    # columns not whole blocks (F4: down_proj K=1408 cannot be Q4_K)
+    assert L.tiermm_qgemv(16, tier_amd.Q4_K, 792, 16, 16, 1, 1408, None) == tier_amd.UNSUPPORTED
+    # K beyond the staged-x limit
+    assert L.tiermm_qgemv(16, tier_amd.Q8_0, 34 * 1024, 16, 16, 1, 32768, None) == tier_amd.UNSUPPORTED
+    # dX layout not built yet; reserved fp32 mode
+    assert L.tiermm_x3_gemm(tier_amd.OP_N, 64, 64, 64, 16, 64, 16, 0.0, 16, 64, None, 0, None) == tier_amd.UNSUPPORTED
+    assert L.tiermm_qgemm(16, tier_amd.Q4_K, 144, 16, 16, 2, 4, 256, 4, tier_amd.MODE_F32, 0.0, None, 0,
+                          None) == tier_amd.UNSUPPORTED
+    # K not a multiple of the 32-element K step
+    assert L.tiermm_x3s_gemm(16, 16, 16, 16, 16, 16, 16, 4, 4, 48, 4, None) == tier_amd.UNSUPPORTED
+    assert L.tiermm_split3_f16(16, 16, 10, 5, 0, None) == tier_amd.EINVAL
+    assert "part_stride" in tier_amd.last_error()
+    # chat_fp3 mirror: unsupported shape -> False, not an exception
+    assert tier_amd.chat_fp3(16, 16, 16, 4, 48, 4, 4) is False
+
+
+def test_workspace_sizes():
+    assert tier_amd.x3_gemm_ws_bytes(5120, 4096, 5120) == 3 * 4096 * 5120 * 2
+    assert tier_amd.x3_rows_ws_bytes(256, 5120, 14336) == 3 * 256 * 5120 * 2
+    assert tier_amd.qgemm_ws_bytes(tier_amd.Q4_K, 512, 5120, 5120) >= 5120 * 5120 * 2

@@ -1,0 +1,100 @@
+"""GPU parity of tiermm_dequant (dq_k<T>, tier.cpp:293-298): bit-exact with the oracle."""
+import numpy as np
+import pytest
+
+import oracle
+import tier_amd
+from helpers import quantized_weight
+from tier_amd import hip
+
+pytestmark = pytest.mark.gpu
+
+TYPES = {"q8_0": tier_amd.Q8_0, "q5_0": tier_amd.Q5_0, "q4_K": tier_amd.Q4_K, "q5_K": tier_amd.Q5_K,
+         "q6_K": tier_amd.Q6_K}
+OUTS = {"f32": (tier_amd.OUT_F32, np.uint32), "f16": (tier_amd.OUT_F16, np.uint16),
+        "bf16": (tier_amd.OUT_BF16, np.uint16)}
+
+
+def _expect(blocks, t, cols, out, r0=0, nrows=None):
+    f = oracle.dequant(blocks, t, cols, oracle.OUT_F32, r0, nrows)
+    if out == tier_amd.OUT_F32:
+        return f.view(np.uint32).ravel()
+    if out == tier_amd.OUT_F16:
+        return oracle.f2h(f)
+    return oracle.f2bf(f)
+
+
+def _run(gpu, blocks, t, cols, out, r0=0, nrows=None):
+    rb = tier_amd.q_row_bytes(t, cols)
+    rows = blocks.size // rb
+    nrows = rows - r0 if nrows is None else nrows
+    esz = 4 if out == tier_amd.OUT_F32 else 2
+    W = hip.to_device(blocks)
+    O = hip.DeviceBuffer(max(nrows * cols * esz, 16))
+    tier_amd.dq_launch(W.ptr, t, rb, cols, r0, nrows, O.ptr, out)
+    hip.synchronize()
+    return O.download(np.uint32 if esz == 4 else np.uint16, nrows * cols)
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+@pytest.mark.parametrize("outname", list(OUTS))
+def test_dequant_golden_blocks(gpu, golden, name, outname):
+    """Random blocks of every type (check_quant.py's construction) against the reference's own values."""
+    t = TYPES[name]
+    out = OUTS[outname][0]
+    if name == "q5_0":
+        rng = np.random.default_rng(9)
+        blocks = oracle.random_blocks(rng, t, 512 // 32 * 8)
+    else:
+        blocks = golden["dequant"][f"{name}_blocks"]
+    cols = 512
+    got = _run(gpu, blocks, t, cols, out)
+    want = _expect(blocks, t, cols, out)
+    if name != "q5_0" and out == tier_amd.OUT_F32:
+        assert np.array_equal(want, golden["dequant"][f"{name}_f32bits"].ravel())
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+def test_dequant_quantized_weights_rows_subset(gpu, name):
+    """N(0,0.02) weights quantized by the host quantizer; rows r0..r0+nrows only (chat prefill chunks)."""
+    t = TYPES[name]
+    N, K = 40, 5120
+    blocks = quantized_weight(t, N, K, seed=30 + t)
+    for out in (tier_amd.OUT_F16, tier_amd.OUT_F32):
+        got = _run(gpu, blocks, t, K, out, r0=7, nrows=29)
+        assert np.array_equal(got, _expect(blocks, t, K, out, 7, 29))
+
+
+def test_dequant_special_blocks(gpu):
+    """fp16 subnormal and zero scales, extreme 6-bit scales, all nibble values (bit-exact incl. fp16 subnormal outputs)."""
+    rng = np.random.default_rng(77)
+    cases = []
+    for d in (0.0, 2.0 ** -24, 3 * 2.0 ** -24, 6.1e-5, 1.0, -2.0, 65504.0 / 1024):
+        b = rng.integers(0, 256, size=(4, 144), dtype=np.uint8)
+        b[:, 0:2] = np.array([d], np.float16).view(np.uint8)
+        b[:, 2:4] = np.array([abs(d) / 3], np.float16).view(np.uint8)
+        b[1, 4:16] = 0xff
+        b[2, 4:16] = 0
+        cases.append(b)
+    blocks = np.concatenate(cases)
+    for out in OUTS.values():
+        got = _run(gpu, blocks, tier_amd.Q4_K, 256, out[0])
+        assert np.array_equal(got, _expect(blocks, tier_amd.Q4_K, 256, out[0]))
+    q6 = rng.integers(0, 256, size=(6, 210), dtype=np.uint8)
+    q6[0, 192:208] = 0x80  # int8 scales -128
+    q6[1, 192:208] = 0x7f
+    q6[:, 208:210] = np.array([2.0 ** -20], np.float16).view(np.uint8)
+    got = _run(gpu, q6, tier_amd.Q6_K, 256, tier_amd.OUT_F16)
+    assert np.array_equal(got, _expect(q6, tier_amd.Q6_K, 256, tier_amd.OUT_F16))
+
+
+def test_dequant_full_layer_shape(gpu):
+    """A whole 14336x5120 Q4_K matrix to fp16 (the training path's dq_launch, tier.cpp:515), checked by hash of rows."""
+    t, N, K = tier_amd.Q4_K, 14336, 5120
+    blocks = quantized_weight(t, N, K, seed=41)
+    got = _run(gpu, blocks, t, K, tier_amd.OUT_F16).reshape(N, K)
+    rows = np.random.default_rng(0).choice(N, 300, replace=False)
+    rows = np.concatenate([rows, [0, N - 1]])
+    for r in rows:
+        assert np.array_equal(got[r], _expect(blocks[r:r + 1], t, K, tier_amd.OUT_F16)), r

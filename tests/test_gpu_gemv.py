@@ -1,0 +1,88 @@
+"""GPU parity of tiermm_qgemv (gemv_q, tier.cpp:299-306).
+
+Bar: relative Frobenius error <= 1e-5 against the fp64 product of the oracle's
+fp32 dequantization with x (BASELINE config 1 states y rel-err <= 1e-5; the
+reference's own lane-strided fp32 GEMV sits near 1e-7 of fp64).
+"""
+import numpy as np
+import pytest
+
+import oracle
+import tier_amd
+from helpers import activations, quantized_weight
+from tier_amd import hip
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+def _gemv(blocks, t, x, N, K):
+    rb = tier_amd.q_row_bytes(t, K)
+    W = hip.to_device(blocks)
+    X = hip.to_device(x)
+    Y = hip.DeviceBuffer(N * 4)
+    Y.fill_bytes(0xff)
+    tier_amd.gemv_q(W.ptr, t, rb, X.ptr, Y.ptr, N, K)
+    hip.synchronize()
+    return Y.download(np.float32, N)
+
+
+CASES = [
+    ("q8_0", tier_amd.Q8_0, 4096, 4096),      # config 1
+    ("q4_K", tier_amd.Q4_K, 13824, 5120),     # north-star GEMV
+    ("q4_K", tier_amd.Q4_K, 5120, 5120),      # config 3 shapes
+    ("q4_K", tier_amd.Q4_K, 14336, 5120),
+    ("q4_K", tier_amd.Q4_K, 5120, 14336),
+    ("q5_K", tier_amd.Q5_K, 1024, 5120),      # config 4 v_proj / down_proj types
+    ("q5_K", tier_amd.Q5_K, 5120, 14336),
+    ("q6_K", tier_amd.Q6_K, 1024, 5120),
+    ("q6_K", tier_amd.Q6_K, 5120, 14336),
+    ("q5_0", tier_amd.Q5_0, 2048, 1408),      # MoE down_proj fallback type
+]
+
+
+@pytest.mark.parametrize("name,t,N,K", CASES, ids=[f"{c[0]}-{c[2]}x{c[3]}" for c in CASES])
+def test_gemv_config_shapes(gpu, name, t, N, K):
+    blocks = quantized_weight(t, N, K, seed=N + K + t)
+    x = activations(1, K, seed=2)[0]
+    y = _gemv(blocks, t, x, N, K)
+    want = oracle.gemv_f64(blocks, t, x, N, K)
+    assert np.all(np.isfinite(y))
+    assert oracle.rel_fro(y, want) <= TOL
+
+
+@pytest.mark.parametrize("t", [tier_amd.Q8_0, tier_amd.Q5_0, tier_amd.Q4_K, tier_amd.Q5_K, tier_amd.Q6_K])
+@pytest.mark.parametrize("N,K", [(1, 256), (13, 512), (7, 768), (65, 2304)])
+def test_gemv_ragged_shapes(gpu, t, N, K):
+    """Row counts that do not fill a wave or a block; one super-block rows; K not a multiple of 512."""
+    rng = np.random.default_rng(N * 1000 + K + t)
+    be, _ = oracle.block(t)
+    blocks = oracle.random_blocks(rng, t, N * (K // be)).reshape(N, -1)
+    x = rng.standard_normal(K).astype(np.float32)
+    y = _gemv(blocks, t, x, N, K)
+    assert oracle.rel_fro(y, oracle.gemv_f64(blocks, t, x, N, K)) <= TOL
+
+
+def test_gemv_zero_and_extreme_inputs(gpu):
+    t, N, K = tier_amd.Q4_K, 64, 1024
+    blocks = quantized_weight(t, N, K, seed=5)
+    y = _gemv(blocks, t, np.zeros(K, np.float32), N, K)
+    assert np.all(y == 0)
+    x = activations(1, K, seed=6)[0] * np.float32(1e4)
+    x[::97] = np.float32(3e4)
+    y = _gemv(blocks, t, x, N, K)
+    assert oracle.rel_fro(y, oracle.gemv_f64(blocks, t, x, N, K)) <= TOL
+
+
+def test_gemv_on_a_stream(gpu):
+    """Stream-ordered: the call returns before the result is ready; a stream sync makes it visible."""
+    t, N, K = tier_amd.Q6_K, 300, 4096
+    blocks = quantized_weight(t, N, K, seed=8)
+    x = activations(1, K, seed=9)[0]
+    W, X, Y = hip.to_device(blocks), hip.to_device(x), hip.DeviceBuffer(N * 4)
+    s = hip.Stream()
+    tier_amd.gemv_q(W.ptr, t, tier_amd.q_row_bytes(t, K), X.ptr, Y.ptr, N, K, stream=s)
+    s.synchronize()
+    y = Y.download(np.float32, N)
+    s.destroy()
+    assert oracle.rel_fro(y, oracle.gemv_f64(blocks, t, x, N, K)) <= TOL

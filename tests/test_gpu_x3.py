@@ -1,0 +1,152 @@
+"""GPU parity of the split kernels and the x3 GEMMs.
+
+Splits are bit-exact with the oracle.  GEMMs: relative Frobenius error <= 2^-20
+against fp64 -- of X*W^T for the 2x2 variant, of
+fp16(W)*X for x3-ref (fp3gemm / chat_fp3 / the quantized GEMM, whose weight is
+the bit-exact fp16 dequantization).
+"""
+import numpy as np
+import pytest
+
+import oracle
+import tier_amd
+from helpers import activations, quantized_weight
+from tier_amd import hip
+
+pytestmark = pytest.mark.gpu
+BAR = 2.0 ** -20
+
+
+def test_split3_bit_exact(gpu):
+    rng = np.random.default_rng(11)
+    x = np.concatenate([rng.uniform(-60000, 60000, 50000),
+                        np.ldexp(rng.uniform(-1, 1, 20000), rng.integers(-40, 10, 20000)),
+                        [0.0, -0.0, 65504.0, 65520.0, 1e-30]]).astype(np.float32)
+    n = x.size
+    X = hip.to_device(x)
+    for order, stride in ((tier_amd.HML, n), (tier_amd.LMH, n + 40)):
+        P = hip.DeviceBuffer((2 * stride + n) * 2)
+        P.fill_bytes(0)
+        tier_amd.split3(X.ptr, P.ptr, n, stride, order)
+        hip.synchronize()
+        got = P.download(np.uint16, 2 * stride + n)
+        want = oracle.split3(x, order, stride)
+        for i in range(3):
+            assert np.array_equal(got[i * stride:i * stride + n], want[i * stride:i * stride + n]), (order, i)
+
+
+def test_x3s_split_bit_exact(gpu):
+    rng = np.random.default_rng(12)
+    v = (rng.standard_normal((9, 1000)) * np.array([0.02, 1, 1e-6, 300, 0, 1e4, 2e-5, 5, 1e-30])[:, None])
+    v = v.astype(np.float32)
+    rows, cols = v.shape
+    S = hip.to_device(v)
+    H, L, E = hip.DeviceBuffer(v.size * 2), hip.DeviceBuffer(v.size * 2), hip.DeviceBuffer(rows * 4)
+    tier_amd.x3s_split(S.ptr, H.ptr, L.ptr, E.ptr, rows, cols)
+    hip.synchronize()
+    hi, lo, ex = oracle.x3s_split(v)
+    assert np.array_equal(E.download(np.int32, rows), ex)
+    assert np.array_equal(H.download(np.uint16, v.size), hi.ravel())
+    assert np.array_equal(L.download(np.uint16, v.size), lo.ravel())
+
+
+def _x3s_gemm(X, W):
+    M, K = X.shape
+    N = W.shape[0]
+    dX, dW = hip.to_device(X), hip.to_device(W)
+    xh, xl, wh, wl = (hip.DeviceBuffer(a * K * 2) for a in (M, M, N, N))
+    xe, we = hip.DeviceBuffer(M * 4), hip.DeviceBuffer(N * 4)
+    Y = hip.DeviceBuffer(M * N * 4)
+    tier_amd.x3s_split(dX.ptr, xh.ptr, xl.ptr, xe.ptr, M, K)
+    tier_amd.x3s_split(dW.ptr, wh.ptr, wl.ptr, we.ptr, N, K)
+    tier_amd.x3s_gemm(xh.ptr, xl.ptr, xe.ptr, wh.ptr, wl.ptr, we.ptr, Y.ptr, M, N, K)
+    hip.synchronize()
+    return Y.download(np.float32, M * N).reshape(M, N)
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 384, 1024), (130, 70, 320), (1, 5, 32), (512, 640, 5120)])
+def test_x3s_gemm_vs_fp64(gpu, M, N, K):
+    W = (np.random.default_rng(8).standard_normal((N, K)) * 0.02).astype(np.float32)
+    X = activations(M, K, seed=9)
+    Y = _x3s_gemm(X, W)
+    ref = X.astype(np.float64) @ W.astype(np.float64).T
+    assert oracle.rel_fro(Y, ref) <= BAR
+
+
+def test_x3s_gemm_config2_sampled(gpu):
+    """BASELINE config 2 at full size: W 5120x5120 ~N(0,0.02), X 4096x5120 ~N(0,1); fp64 on 192 sampled rows."""
+    M, N, K = 4096, 5120, 5120
+    W = (np.random.default_rng(8).standard_normal((N, K), dtype=np.float32) * 0.02).astype(np.float32)
+    X = activations(M, K, seed=9)
+    Y = _x3s_gemm(X, W)
+    rows = np.random.default_rng(1).choice(M, 192, replace=False)
+    ref = X[rows].astype(np.float64) @ W.astype(np.float64).T
+    assert np.all(np.isfinite(Y))
+    assert oracle.rel_fro(Y[rows], ref) <= BAR
+
+
+def _fp16(w):
+    return oracle.h2f(oracle.f2h(w)).reshape(w.shape)
+
+
+@pytest.mark.parametrize("beta", [0.0, 1.0])
+def test_fp3gemm_forward_contract(gpu, beta):
+    """fp3gemm(OP_T, m=N, n=M, k=K, W16, lda=K, x, beta, C, ldc): out[M][ldc] = x W^T (+ beta*out)."""
+    rng = np.random.default_rng(13)
+    M, N, K, ldc = 192, 320, 768, 336
+    w16 = oracle.f2h((rng.standard_normal((N, K)) * 0.02).astype(np.float32)).reshape(N, K)
+    x = activations(M, K, seed=14)
+    c0 = rng.standard_normal((M, ldc)).astype(np.float32)
+    A, B, C = hip.to_device(w16), hip.to_device(x), hip.to_device(c0)
+    tier_amd.fp3gemm(tier_amd.OP_T, N, M, K, A.ptr, K, B.ptr, beta, C.ptr, ldc)
+    hip.synchronize()
+    got = C.download(np.float32, M * ldc).reshape(M, ldc)
+    ref = x.astype(np.float64) @ oracle.h2f(w16).reshape(N, K).astype(np.float64).T + beta * c0[:, :N]
+    assert oracle.rel_fro(got[:, :N], ref) <= BAR
+    assert np.array_equal(got[:, N:], c0[:, N:])  # columns past m untouched
+
+
+def test_chat_fp3_rows(gpu):
+    rng = np.random.default_rng(15)
+    M, N, K, ldo = 100, 200, 1024, 256
+    w16 = oracle.f2h((rng.standard_normal((N, K)) * 0.02).astype(np.float32)).reshape(N, K)
+    x = activations(M, K, seed=16)
+    A, B, Y = hip.to_device(w16), hip.to_device(x), hip.DeviceBuffer(M * ldo * 4)
+    assert tier_amd.chat_fp3(A.ptr, B.ptr, Y.ptr, M, K, N, ldo)
+    hip.synchronize()
+    got = Y.download(np.float32, M * ldo).reshape(M, ldo)[:, :N]
+    ref = x.astype(np.float64) @ oracle.h2f(w16).reshape(N, K).astype(np.float64).T
+    assert oracle.rel_fro(got, ref) <= BAR
+
+
+QG = [("q4_K", tier_amd.Q4_K, 96, 640, 1024), ("q8_0", tier_amd.Q8_0, 64, 256, 512),
+      ("q5_K", tier_amd.Q5_K, 64, 128, 768), ("q6_K", tier_amd.Q6_K, 33, 100, 512),
+      ("q5_0", tier_amd.Q5_0, 40, 64, 1408)]
+
+
+@pytest.mark.parametrize("name,t,M,N,K", QG, ids=[c[0] for c in QG])
+def test_qgemm_x3ref(gpu, name, t, M, N, K):
+    blocks = quantized_weight(t, N, K, seed=20 + t)
+    x = activations(M, K, seed=21)
+    W, X, Y = hip.to_device(blocks), hip.to_device(x), hip.DeviceBuffer(M * N * 4)
+    tier_amd.qgemm(W.ptr, t, tier_amd.q_row_bytes(t, K), X.ptr, Y.ptr, M, N, K)
+    hip.synchronize()
+    got = Y.download(np.float32, M * N).reshape(M, N)
+    w16 = oracle.h2f(oracle.dequant(blocks, t, K, oracle.OUT_F16)).reshape(N, K)
+    ref = x.astype(np.float64) @ w16.astype(np.float64).T
+    assert oracle.rel_fro(got, ref) <= BAR
+
+
+def test_qgemm_config3_m512_sampled(gpu):
+    """Config 3 prefill: q4_K 14336x5120 at M=512; fp64 check on sampled output rows."""
+    t, M, N, K = tier_amd.Q4_K, 512, 14336, 5120
+    blocks = quantized_weight(t, N, K, seed=33)
+    x = activations(M, K, seed=34)
+    W, X, Y = hip.to_device(blocks), hip.to_device(x), hip.DeviceBuffer(M * N * 4)
+    tier_amd.qgemm(W.ptr, t, tier_amd.q_row_bytes(t, K), X.ptr, Y.ptr, M, N, K)
+    hip.synchronize()
+    got = Y.download(np.float32, M * N).reshape(M, N)
+    rows = np.random.default_rng(2).choice(M, 48, replace=False)
+    w16 = oracle.h2f(oracle.dequant(blocks, t, K, oracle.OUT_F16)).reshape(N, K)
+    ref = x[rows].astype(np.float64) @ w16.astype(np.float64).T
+    assert oracle.rel_fro(got[rows], ref) <= BAR

@@ -1,0 +1,226 @@
+"""tier_amd -- MI355X (gfx950) frozen-weight matmul path of tierlm, behind a C ABI.
+
+``libtiermm.so`` (built in-tree by ``tier_amd.build``) holds hand-written HIP
+kernels for gfx950 and exports the C ABI declared in ``include/tiermm.h``.
+This module binds that ABI with ctypes and mirrors, under the reference's own
+names, the engine functions the ABI replaces:
+
+=====================  ====================================  ==============================
+reference function     meaning                               here
+=====================  ====================================  ==============================
+q_row_bytes/q_cols_ok  quant.h:31-34                         ``q_row_bytes``
+dq_launch / dq_k<T>    tier.cpp:293-298                      ``dq_launch``
+gemv_q                 tier.cpp:299-306                      ``gemv_q``
+split3_fp_k/split3s    tier.cpp:869-870, 2192-2194           ``split3``
+fp3gemm                tier.cpp:922-943                      ``fp3gemm``
+chat_fp3               tier.cpp:2195-2219                    ``chat_fp3`` (returns False when unsupported)
+chat_lin (quantized)   tier.cpp:2351-2378                    ``qlinear``
+q_row                  quant.h:201-204                       ``q_row`` (host)
+=====================  ====================================  ==============================
+
+Device tensors are passed as integer device addresses (``tier_amd.hip`` gives
+them).  There is no CPU fallback: if the library is missing, importing this
+package raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libtiermm.so")
+
+OK, UNSUPPORTED, EINVAL = 0, 1, 2
+F32, F16, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K, BF16 = 0, 1, 6, 8, 12, 13, 14, 30
+OUT_F32, OUT_F16, OUT_BF16 = 0, 1, 2
+HML, LMH = 0, 1
+OP_N, OP_T = 111, 112
+MODE_X3REF, MODE_F32 = 0, 1
+GPU_TYPES = (Q8_0, Q5_0, Q4_K, Q5_K, Q6_K)
+TYPE_NAMES = {Q8_0: "q8_0", Q5_0: "q5_0", Q4_K: "q4_K", Q5_K: "q5_K", Q6_K: "q6_K"}
+
+# every symbol include/tiermm.h declares
+EXPORTS = (
+    "tiermm_init", "tiermm_shutdown", "tiermm_last_error", "tiermm_version", "tiermm_q_info",
+    "tiermm_q_row_bytes", "tiermm_dequant", "tiermm_qgemv", "tiermm_split3_f16", "tiermm_x3_gemm",
+    "tiermm_x3_gemm_ws_bytes", "tiermm_x3_rows", "tiermm_x3_rows_ws_bytes", "tiermm_x3s_split",
+    "tiermm_x3s_gemm", "tiermm_qgemm", "tiermm_qgemm_ws_bytes", "tiermm_quantize",
+)
+
+
+class TiermmError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+class TiermmUnsupported(TiermmError):
+    pass
+
+
+if not os.path.isfile(LIB_PATH):
+    raise ImportError(f"{LIB_PATH} is not built: run `python -m tier_amd.build` (no CPU fallback exists)")
+
+_L = ctypes.CDLL(LIB_PATH)
+_vp, _sz, _i, _f = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_float
+
+
+def _sig(name, args, res=ctypes.c_int):
+    fn = getattr(_L, name)
+    fn.argtypes = args
+    fn.restype = res
+    return fn
+
+
+_sig("tiermm_init", [_i])
+_sig("tiermm_shutdown", [], None)
+_sig("tiermm_last_error", [], ctypes.c_char_p)
+_sig("tiermm_version", [], ctypes.c_char_p)
+_sig("tiermm_q_info", [_i, ctypes.POINTER(_i), ctypes.POINTER(_i)])
+_sig("tiermm_q_row_bytes", [_i, _i, ctypes.POINTER(_sz)])
+_sig("tiermm_dequant", [_vp, _i, _sz, _i, _sz, _sz, _vp, _i, _vp])
+_sig("tiermm_qgemv", [_vp, _i, _sz, _vp, _vp, _i, _i, _vp])
+_sig("tiermm_split3_f16", [_vp, _vp, _sz, _sz, _i, _vp])
+_sig("tiermm_x3_gemm", [_i, _i, _i, _i, _vp, _i, _vp, _f, _vp, _i, _vp, _sz, _vp])
+_sig("tiermm_x3_gemm_ws_bytes", [_i, _i, _i], _sz)
+_sig("tiermm_x3_rows", [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp])
+_sig("tiermm_x3_rows_ws_bytes", [_i, _i, _i], _sz)
+_sig("tiermm_x3s_split", [_vp, _vp, _vp, _vp, _i, _i, _vp])
+_sig("tiermm_x3s_gemm", [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp])
+_sig("tiermm_qgemm", [_vp, _i, _sz, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp, _sz, _vp])
+_sig("tiermm_qgemm_ws_bytes", [_i, _i, _i, _i, _i], _sz)
+_sig("tiermm_quantize", [_i, _vp, _vp, _sz, _i, _i])
+
+
+def lib():
+    return _L
+
+
+def last_error() -> str:
+    return (_L.tiermm_last_error() or b"").decode()
+
+
+def _check(code: int) -> None:
+    if code == OK:
+        return
+    cls = TiermmUnsupported if code == UNSUPPORTED else TiermmError
+    raise cls(code, last_error())
+
+
+def _s(stream) -> int | None:
+    if stream is None:
+        return None
+    return getattr(stream, "handle", stream)
+
+
+def init(device: int = 0) -> None:
+    _check(_L.tiermm_init(device))
+
+
+def shutdown() -> None:
+    _L.tiermm_shutdown()
+
+
+def version() -> str:
+    return _L.tiermm_version().decode()
+
+
+# ---------------------------------------------------------------- registry
+def q_info(qtype: int) -> tuple[int, int]:
+    be, bb = _i(), _i()
+    _check(_L.tiermm_q_info(qtype, ctypes.byref(be), ctypes.byref(bb)))
+    return be.value, bb.value
+
+
+def q_row_bytes(qtype: int, cols: int) -> int:
+    rb = _sz()
+    _check(_L.tiermm_q_row_bytes(qtype, cols, ctypes.byref(rb)))
+    return rb.value
+
+
+def q_cols_ok(qtype: int, cols: int) -> bool:
+    rb = _sz()
+    return _L.tiermm_q_row_bytes(qtype, cols, ctypes.byref(rb)) == OK
+
+
+# ------------------------------------------------------------- host quantizer
+def q_row(qtype: int, x: np.ndarray, nthreads: int = 0) -> np.ndarray:
+    """Quantize rows of a host fp32 matrix [rows][cols] (quant.h:201-204); returns [rows][rb] bytes."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    if x.ndim == 1:
+        x = x[None, :]
+    rows, cols = x.shape
+    out = np.empty((rows, q_row_bytes(qtype, cols)), dtype=np.uint8)
+    _check(_L.tiermm_quantize(qtype, x.ctypes.data_as(_vp), out.ctypes.data_as(_vp), rows, cols, nthreads))
+    return out
+
+
+# ------------------------------------------------------------- device entry points
+def dq_launch(W: int, qtype: int, rb: int, cols: int, r0: int, nrows: int, out: int, out_dtype: int = OUT_F16,
+              stream=None) -> None:
+    """dq_launch (tier.cpp:297): dequantize rows r0..r0+nrows of W into out."""
+    _check(_L.tiermm_dequant(W, qtype, rb, cols, r0, nrows, out, out_dtype, _s(stream)))
+
+
+def gemv_q(W: int, qtype: int, rb: int, x: int, y: int, N: int, K: int, stream=None) -> None:
+    """gemv_q (tier.cpp:300): y[N] = dequant(W)[N][K] * x[K]."""
+    _check(_L.tiermm_qgemv(W, qtype, rb, x, y, N, K, _s(stream)))
+
+
+def split3(x: int, parts: int, n: int, stride: int | None = None, order: int = HML, stream=None) -> None:
+    """split3_fp_k / split3s_fp16 (tier.cpp:869, 2192)."""
+    _check(_L.tiermm_split3_f16(x, parts, n, n if stride is None else stride, order, _s(stream)))
+
+
+def fp3gemm(opA: int, m: int, n: int, k: int, A: int, lda: int, B: int, beta: float, C: int, ldc: int,
+            ws: int | None = None, ws_bytes: int = 0, stream=None) -> None:
+    """fp3gemm (tier.cpp:922) in its BLAS column-major contract."""
+    _check(_L.tiermm_x3_gemm(opA, m, n, k, A, lda, B, beta, C, ldc, ws, ws_bytes, _s(stream)))
+
+
+def x3_gemm_ws_bytes(m: int, n: int, k: int) -> int:
+    return _L.tiermm_x3_gemm_ws_bytes(m, n, k)
+
+
+def chat_fp3(W: int, x: int, y: int, M: int, K: int, N: int, ldo: int, ws: int | None = None, ws_bytes: int = 0,
+             stream=None) -> bool:
+    """chat_fp3 (tier.cpp:2195): False when the shape is not handled (the caller falls back)."""
+    code = _L.tiermm_x3_rows(W, x, y, M, K, N, ldo, ws, ws_bytes, _s(stream))
+    if code == UNSUPPORTED:
+        return False
+    _check(code)
+    return True
+
+
+def x3_rows_ws_bytes(M: int, K: int, N: int) -> int:
+    return _L.tiermm_x3_rows_ws_bytes(M, K, N)
+
+
+def x3s_split(src: int, hi: int, lo: int, exps: int, rows: int, cols: int, stream=None) -> None:
+    _check(_L.tiermm_x3s_split(src, hi, lo, exps, rows, cols, _s(stream)))
+
+
+def x3s_gemm(Xhi: int, Xlo: int, xexp: int, Whi: int, Wlo: int, wexp: int, Y: int, M: int, N: int, K: int,
+             ldy: int | None = None, stream=None) -> None:
+    _check(_L.tiermm_x3s_gemm(Xhi, Xlo, xexp, Whi, Wlo, wexp, Y, M, N, K, N if ldy is None else ldy, _s(stream)))
+
+
+def qgemm(W: int, qtype: int, rb: int, X: int, Y: int, M: int, N: int, K: int, ldy: int | None = None,
+          mode: int = MODE_X3REF, beta: float = 0.0, ws: int | None = None, ws_bytes: int = 0, stream=None) -> None:
+    _check(_L.tiermm_qgemm(W, qtype, rb, X, Y, M, N, K, N if ldy is None else ldy, mode, beta, ws, ws_bytes,
+                           _s(stream)))
+
+
+def qgemm_ws_bytes(qtype: int, M: int, N: int, K: int, mode: int = MODE_X3REF) -> int:
+    return _L.tiermm_qgemm_ws_bytes(qtype, M, N, K, mode)
+
+
+def qlinear(W: int, qtype: int, rb: int, x: int, y: int, M: int, N: int, K: int, ws: int | None = None,
+            ws_bytes: int = 0, stream=None) -> None:
+    """The quantized branch of chat_lin (tier.cpp:2356-2359): GEMV at M=1, dequant-GEMM above."""
+    if M == 1:
+        gemv_q(W, qtype, rb, x, y, N, K, stream)
+    else:
+        qgemm(W, qtype, rb, x, y, M, N, K, N, MODE_X3REF, 0.0, ws, ws_bytes, stream)

@@ -1,0 +1,104 @@
+// dequant.hip -- tiermm_dequant: quantized rows -> fp32 / fp16 / bf16 (dq_k<T>, tier.cpp:293-298).
+//
+// One thread decodes 8 consecutive outputs of a row and writes them with one
+// 16-byte store (fp16/bf16) or two (fp32): the kernel is bound by the output
+// writes (2 B/element for fp16 against 0.56 B/element read for Q4_K).
+#include "tm_device.h"
+
+namespace tiermm {
+namespace {
+
+template <int QT, int OUT>
+__global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ W, size_t rb, int cols, size_t r0,
+                                                      size_t n8, void* __restrict__ out) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x; t < n8; t += stride) {
+    const size_t e = t * 8;
+    const size_t row = e / (size_t)cols;
+    const int col = (int)(e - row * (size_t)cols);
+    float v[8];
+    Dec<QT>::run(W + (r0 + row) * rb, col, v);
+    if (OUT == TIERMM_OUT_F32) {
+      float4* o = (float4*)((float*)out + e);
+      o[0] = make_float4(v[0], v[1], v[2], v[3]);
+      o[1] = make_float4(v[4], v[5], v[6], v[7]);
+    } else {
+      uint32_t p[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t lo = OUT == TIERMM_OUT_F16 ? f2h(v[2 * k]) : f2bf(v[2 * k]);
+        const uint32_t hi = OUT == TIERMM_OUT_F16 ? f2h(v[2 * k + 1]) : f2bf(v[2 * k + 1]);
+        p[k] = lo | (hi << 16);
+      }
+      *(uint4*)((uint16_t*)out + e) = make_uint4(p[0], p[1], p[2], p[3]);
+    }
+  }
+}
+
+template <int QT>
+int launch_dequant(const void* W, size_t rb, int cols, size_t r0, size_t nrows, void* out, int out_dtype,
+                   hipStream_t s) {
+  const size_t n8 = nrows * (size_t)cols / 8;
+  if (n8 == 0) return TIERMM_OK;
+  const size_t want = (n8 + 255) / 256;
+  const unsigned grid = (unsigned)(want < 65536 ? want : 65536);
+  const uint8_t* w = (const uint8_t*)W;
+  switch (out_dtype) {
+    case TIERMM_OUT_F32: dequant_kernel<QT, TIERMM_OUT_F32><<<grid, 256, 0, s>>>(w, rb, cols, r0, n8, out); break;
+    case TIERMM_OUT_F16: dequant_kernel<QT, TIERMM_OUT_F16><<<grid, 256, 0, s>>>(w, rb, cols, r0, n8, out); break;
+    default: dequant_kernel<QT, TIERMM_OUT_BF16><<<grid, 256, 0, s>>>(w, rb, cols, r0, n8, out); break;
+  }
+  TM_LAUNCH_CHECK("tiermm_dequant: launch");
+  return TIERMM_OK;
+}
+
+}  // namespace
+
+// Shared argument checks for a quantized weight: type handled, rb consistent,
+// alignment of the row bytes the decoders assume.
+int check_qweight(const char* who, const void* W, int qtype, size_t rb, int cols) {
+  const BlockInfo* bi = block_info(qtype);
+  if (!bi || (qtype != QT_Q8_0 && qtype != QT_Q5_0 && qtype != QT_Q4_K && qtype != QT_Q5_K && qtype != QT_Q6_K))
+    return set_error(TIERMM_UNSUPPORTED, "%s: type %d is not handled on the GPU", who, qtype);
+  if (cols <= 0 || cols % bi->elems)
+    return set_error(TIERMM_UNSUPPORTED, "%s: %d columns are not whole %s blocks", who, cols, bi->name);
+  if (rb != (size_t)cols / bi->elems * bi->bytes)
+    return set_error(TIERMM_EINVAL, "%s: rb %zu does not match %d %s columns", who, rb, cols, bi->name);
+  const size_t align = (qtype == QT_Q4_K || qtype == QT_Q5_K) ? 16 : 2;
+  if (!W || ((uintptr_t)W % align) || (rb % align))
+    return set_error(TIERMM_EINVAL, "%s: weight rows must be %zu-byte aligned", who, align);
+  return TIERMM_OK;
+}
+
+// Whole rows to fp16 for the quantized GEMM (dq_launch<tier_fp16>, tier.cpp:515).
+int dequant_f16_rows(const void* W, int qtype, size_t rb, int cols, size_t nrows, uint16_t* out, hipStream_t s) {
+  switch (qtype) {
+    case QT_Q8_0: return launch_dequant<QT_Q8_0>(W, rb, cols, 0, nrows, out, TIERMM_OUT_F16, s);
+    case QT_Q5_0: return launch_dequant<QT_Q5_0>(W, rb, cols, 0, nrows, out, TIERMM_OUT_F16, s);
+    case QT_Q4_K: return launch_dequant<QT_Q4_K>(W, rb, cols, 0, nrows, out, TIERMM_OUT_F16, s);
+    case QT_Q5_K: return launch_dequant<QT_Q5_K>(W, rb, cols, 0, nrows, out, TIERMM_OUT_F16, s);
+    default: return launch_dequant<QT_Q6_K>(W, rb, cols, 0, nrows, out, TIERMM_OUT_F16, s);
+  }
+}
+
+}  // namespace tiermm
+
+using namespace tiermm;
+
+extern "C" int tiermm_dequant(const void* W, int qtype, size_t rb, int cols, size_t r0, size_t nrows, void* out,
+                              int out_dtype, tiermm_stream_t stream) {
+  int st = check_qweight("tiermm_dequant", W, qtype, rb, cols);
+  if (st) return st;
+  if (out_dtype != TIERMM_OUT_F32 && out_dtype != TIERMM_OUT_F16 && out_dtype != TIERMM_OUT_BF16)
+    return set_error(TIERMM_EINVAL, "tiermm_dequant: unknown output dtype %d", out_dtype);
+  if (nrows && (!out || ((uintptr_t)out % 16)))
+    return set_error(TIERMM_EINVAL, "tiermm_dequant: output must be 16-byte aligned");
+  hipStream_t s = (hipStream_t)stream;
+  switch (qtype) {
+    case QT_Q8_0: return launch_dequant<QT_Q8_0>(W, rb, cols, r0, nrows, out, out_dtype, s);
+    case QT_Q5_0: return launch_dequant<QT_Q5_0>(W, rb, cols, r0, nrows, out, out_dtype, s);
+    case QT_Q4_K: return launch_dequant<QT_Q4_K>(W, rb, cols, r0, nrows, out, out_dtype, s);
+    case QT_Q5_K: return launch_dequant<QT_Q5_K>(W, rb, cols, r0, nrows, out, out_dtype, s);
+    default: return launch_dequant<QT_Q6_K>(W, rb, cols, r0, nrows, out, out_dtype, s);
+  }
+}

@@ -1,0 +1,155 @@
+// tm_device.h -- device helpers shared by the gfx950 kernels: fp16/bf16
+// conversion, aligned loads and the exact per-block decoders.
+//
+// Exactness: for Q8_0, Q5_0, Q4_K, Q5_K and Q6_K every product in q_val
+// (quant.h:59-121) is exact in fp32 (at most 11+7+5 significant bits), so the
+// only fp32 rounding is the final subtraction of the K-quants with a minimum.
+// The decoders below therefore give the reference's fp32 value bit for bit
+// whatever the compiler fuses.  fp32 -> fp16 uses v_cvt_f16_f32 (round to
+// nearest even, fp16 denormals kept by the default MODE), matching tier_fp16.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "tm_host.h"
+
+namespace tiermm {
+
+__device__ __forceinline__ float h2f(uint32_t h16) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h16);
+}
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+// hip_bfloat16(float): round to nearest even on the top 16 bits; NaN stays NaN.
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u) return (uint16_t)((u >> 16) | ((u & 0xffffu) ? 1u : 0u));
+  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) { return *(const uint16_t*)p; }
+// 4 bytes at a 2-byte aligned address
+__device__ __forceinline__ uint32_t ld_u32_a2(const uint8_t* p) {
+  return (uint32_t)*(const uint16_t*)p | ((uint32_t)*(const uint16_t*)(p + 2) << 16);
+}
+// 8 bytes at a 2-byte aligned address
+__device__ __forceinline__ uint2 ld_u64_a2(const uint8_t* p) { return make_uint2(ld_u32_a2(p), ld_u32_a2(p + 4)); }
+
+__device__ __forceinline__ uint32_t byte_at(uint2 v, int k) {
+  return ((k < 4 ? v.x : v.y) >> (8 * (k & 3))) & 255u;
+}
+
+// 6-bit (scale, min) of sub-block s of a Q4_K/Q5_K super-block (quant.h:47-48).
+// q0 = scale bytes 0..3, q1 = 4..7, q2 = 8..11 (block bytes 4..15).
+__device__ __forceinline__ void kq_scale_min(int s, uint32_t q0, uint32_t q1, uint32_t q2, int& sc, int& mn) {
+  const int sh = 8 * (s & 3);
+  if (s < 4) {
+    sc = (q0 >> sh) & 63;
+    mn = (q1 >> sh) & 63;
+  } else {
+    sc = ((q2 >> sh) & 15) | (((q0 >> (sh + 6)) & 3) << 4);
+    mn = ((q2 >> (sh + 4)) & 15) | (((q1 >> (sh + 6)) & 3) << 4);
+  }
+}
+
+// Decoders: 8 consecutive elements starting at column `c` (c % 8 == 0) of a
+// quantized row, exactly as q_val evaluates each of them.
+template <int QT>
+struct Dec;
+
+template <>
+struct Dec<QT_Q8_0> {  // quant.h:68 -- 34-byte blocks: d fp16, 32 x int8
+  static constexpr int BLK = 32, BYTES = 34;
+  __device__ static void run(const uint8_t* row, int c, float v[8]) {
+    const uint8_t* b = row + (size_t)(c >> 5) * 34;
+    const float d = h2f(ld_u16(b));
+    const uint2 q = ld_u64_a2(b + 2 + (c & 31));
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = d * (float)(int8_t)byte_at(q, k);
+  }
+};
+
+template <>
+struct Dec<QT_Q5_0> {  // quant.h:66 -- 22-byte blocks: d, qh u32, 16 bytes of nibbles
+  static constexpr int BLK = 32, BYTES = 22;
+  __device__ static void run(const uint8_t* row, int c, float v[8]) {
+    const uint8_t* b = row + (size_t)(c >> 5) * 22;
+    const int i0 = c & 31;
+    const float d = h2f(ld_u16(b));
+    const uint32_t qh = ld_u32_a2(b + 2);
+    const uint2 q = ld_u64_a2(b + 6 + (i0 & 15));
+    const int sh = i0 < 16 ? 0 : 4;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int nib = (int)((byte_at(q, k) >> sh) & 15u) | (int)(((qh >> (i0 + k)) & 1u) << 4);
+      v[k] = d * (float)(nib - 16);
+    }
+  }
+};
+
+template <>
+struct Dec<QT_Q4_K> {  // quant.h:83-84 -- 144-byte super-blocks
+  static constexpr int BLK = 256, BYTES = 144;
+  __device__ static void run(const uint8_t* row, int c, float v[8]) {
+    const uint8_t* b = row + (size_t)(c >> 8) * 144;
+    const int i0 = c & 255, j = i0 >> 6, l0 = i0 & 63;
+    const uint4 h = *(const uint4*)b;
+    int sc, mn;
+    kq_scale_min(2 * j + (l0 >= 32), h.y, h.z, h.w, sc, mn);
+    const float dsc = h2f(h.x & 0xffffu) * (float)sc, dm = h2f(h.x >> 16) * (float)mn;
+    const uint2 q = *(const uint2*)(b + 16 + 32 * j + (l0 & 31));
+    const int sh = l0 < 32 ? 0 : 4;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = dsc * (float)((byte_at(q, k) >> sh) & 15u) - dm;
+  }
+};
+
+template <>
+struct Dec<QT_Q5_K> {  // quant.h:85-87 -- 176-byte super-blocks
+  static constexpr int BLK = 256, BYTES = 176;
+  __device__ static void run(const uint8_t* row, int c, float v[8]) {
+    const uint8_t* b = row + (size_t)(c >> 8) * 176;
+    const int i0 = c & 255, j = i0 >> 6, l0 = i0 & 63;
+    const uint4 h = *(const uint4*)b;
+    int sc, mn;
+    kq_scale_min(2 * j + (l0 >= 32), h.y, h.z, h.w, sc, mn);
+    const float dsc = h2f(h.x & 0xffffu) * (float)sc, dm = h2f(h.x >> 16) * (float)mn;
+    const uint2 q = *(const uint2*)(b + 48 + 32 * j + (l0 & 31));
+    const uint2 qh = *(const uint2*)(b + 16 + (i0 & 31));
+    const int sh = l0 < 32 ? 0 : 4, hs = i0 >> 5;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t nib = ((byte_at(q, k) >> sh) & 15u) | (((byte_at(qh, k) >> hs) & 1u) << 4);
+      v[k] = dsc * (float)nib - dm;
+    }
+  }
+};
+
+template <>
+struct Dec<QT_Q6_K> {  // quant.h:88-90 -- 210-byte super-blocks (2-byte aligned)
+  static constexpr int BLK = 256, BYTES = 210;
+  __device__ static void run(const uint8_t* row, int c, float v[8]) {
+    const uint8_t* b = row + (size_t)(c >> 8) * 210;
+    const int i0 = c & 255, a = i0 >> 7, r = i0 & 127;
+    const uint2 ql = ld_u64_a2(b + 64 * a + (r & 63));
+    const uint2 qh = ld_u64_a2(b + 128 + 32 * a + (r & 31));
+    const float ds = h2f(ld_u16(b + 208)) * (float)(int8_t)b[192 + (i0 >> 4)];
+    const int s4 = 4 * (r >> 6), s2 = 2 * (r >> 5);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int q = (int)(((byte_at(ql, k) >> s4) & 15u) | (((byte_at(qh, k) >> s2) & 3u) << 4)) - 32;
+      v[k] = ds * (float)q;
+    }
+  }
+};
+
+// Launch-shape guard: kernels assume their block size; a mismatch is a host bug.
+#define TM_LAUNCH_CHECK(what)                                  \
+  do {                                                         \
+    hipError_t e_ = hipGetLastError();                         \
+    if (e_ != hipSuccess) return hip_fail(e_, what);           \
+  } while (0)
+
+}  // namespace tiermm

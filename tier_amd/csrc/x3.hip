@@ -1,0 +1,441 @@
+// x3.hip -- split-precision ("x3") fp16 MFMA GEMMs and the split kernels.
+//
+//  * split3_f16 (split3_fp_k tier.cpp:869-870, split3s_fp16 tier.cpp:2192-2194)
+//  * x3s_split: two-part split with a power-of-two exponent per row
+//  * gemm_x3 core: C[M][N] = scale * sum over products (p,q) of A_p[M][K] * B_q[N][K]^T,
+//    A_p/B_q fp16 row-major with K contiguous ("NT"), fp32 accumulation on
+//    v_mfma_f32_32x32x16_f16.  Used with
+//      - x3-ref (fp3gemm, chat_fp3): A = x split in hi/mid/lo, B = the fp16
+//        weight, products (lo,W) (mid,W) (hi,W) -- the reference's part order
+//        (tier.cpp:940);
+//      - x3-2x2: A = X hi/lo, B = W hi/lo, products (hi,hi) (hi,lo) (lo,hi),
+//        result scaled by 2^-(xexp[m]+wexp[n]).
+//
+// Tiling: a 256-thread workgroup (4 waves, 2x2) owns a BMxBN output tile; each
+// wave a (BM/2)x(BN/2) sub-tile of 32x32 MFMA blocks.  K advances by BK=32 per
+// stage through a double-buffered LDS copy of every part tile (one barrier per
+// stage; the next stage's global loads are issued before the MFMAs of the
+// current one).  LDS rows are 64 data bytes + 16 pad bytes so the 16-byte
+// fragment reads of 8 consecutive rows hit distinct banks.
+#include "tm_device.h"
+
+namespace tiermm {
+
+int check_qweight(const char* who, const void* W, int qtype, size_t rb, int cols);
+int dequant_f16_rows(const void* W, int qtype, size_t rb, int cols, size_t nrows, uint16_t* out, hipStream_t s);
+
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------------ splits
+__global__ __launch_bounds__(256) void split3_kernel(const float* __restrict__ x, uint16_t* __restrict__ parts,
+                                                     size_t n, size_t stride, int order) {
+  const size_t step = (size_t)gridDim.x * blockDim.x;
+  uint16_t* p0 = parts;
+  uint16_t* p1 = parts + stride;
+  uint16_t* p2 = parts + 2 * stride;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) {
+    const float v = x[i];
+    const uint16_t h = f2h(v);
+    const float r = v - h2f(h);
+    const uint16_t m = f2h(r);
+    const uint16_t l = f2h(r - h2f(m));
+    if (order == TIERMM_HML) {
+      p0[i] = h; p1[i] = m; p2[i] = l;
+    } else {
+      p0[i] = l; p1[i] = m; p2[i] = h;
+    }
+  }
+}
+
+__device__ __forceinline__ float block_max_256(float v, float* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  v = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  return v;
+}
+
+// Row exponent e = 14 - floor(log2(amax)) so that amax * 2^e lies in [2^14, 2^15).
+__device__ __forceinline__ int x3s_exp(float amax) {
+  if (!(amax > 0.f) || !isfinite(amax)) return 0;
+  int ex;
+  (void)frexpf(amax, &ex);
+  return min(100, max(-100, 15 - ex));
+}
+
+__global__ __launch_bounds__(256) void x3s_split_kernel(const float* __restrict__ src, uint16_t* __restrict__ hi,
+                                                        uint16_t* __restrict__ lo, int32_t* __restrict__ exps,
+                                                        int cols) {
+  __shared__ float red[4];
+  const size_t base = (size_t)blockIdx.x * cols;
+  float amax = 0.f;
+  for (int k = threadIdx.x; k < cols; k += 256) amax = fmaxf(amax, fabsf(src[base + k]));
+  amax = block_max_256(amax, red);
+  const int e = x3s_exp(amax);
+  const float sc = ldexpf(1.f, e);
+  for (int k = threadIdx.x; k < cols; k += 256) {
+    const float s = src[base + k] * sc;
+    const uint16_t h = f2h(s);
+    hi[base + k] = h;
+    lo[base + k] = f2h(s - h2f(h));
+  }
+  if (threadIdx.x == 0) exps[blockIdx.x] = e;
+}
+
+// ------------------------------------------------------------- GEMM core
+constexpr int BK = 32;            // K per LDS stage (two 32x32x16 MFMA steps)
+constexpr int LDS_ROW = 40;       // halfs per LDS row: 32 data + 8 pad
+
+// Operand parts per GEMM flavour (the products are spelled out in the kernel).
+enum { X3_REF = 0, X3_2X2 = 1 };
+template <int MODE>
+struct X3Mode;
+template <>
+struct X3Mode<X3_REF> {  // A = x hi/mid/lo, B = the fp16 weight
+  static constexpr int NA = 3, NB = 1;
+};
+template <>
+struct X3Mode<X3_2X2> {  // A = X hi/lo, B = W hi/lo
+  static constexpr int NA = 2, NB = 2;
+};
+
+struct X3Args {
+  const uint16_t* A[3];  // [M][lda]
+  const uint16_t* B[2];  // [N][ldb]
+  int lda, ldb;
+  float* C;
+  int ldc;
+  int M, N, K;
+  const int32_t* aexp;  // per-row exponent of A (x3-2x2) or null
+  const int32_t* bexp;  // per-row exponent of B or null
+  float beta;
+};
+
+template <int BM, int BN, int MODE>
+__global__ __launch_bounds__(256) void gemm_x3_kernel(const X3Args p) {
+  using Md = X3Mode<MODE>;
+  constexpr int NA = Md::NA, NB = Md::NB;
+  constexpr int WM = BM / 64, WN = BN / 64;           // 32x32 blocks per wave (2x2 waves)
+  constexpr int A_CH = BM * (BK / 8) / 256;          // 16-byte chunks per thread per A part
+  constexpr int B_CH = BN * (BK / 8) / 256;
+  static_assert(A_CH >= 1 && B_CH >= 1, "tile too small for 256 threads");
+  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+  constexpr int A_PART = BM * LDS_ROW, B_PART = BN * LDS_ROW;
+  constexpr int STAGE = NA * A_PART + NB * B_PART;
+
+  // XCD-aware tile order: launches round-robin blocks over the 8 XCDs; give
+  // each XCD a contiguous run of tiles so neighbours share L2.
+  const int ntm = (p.M + BM - 1) / BM, ntn = (p.N + BN - 1) / BN, nt = ntm * ntn;
+  int bid = blockIdx.x;
+  if ((nt & 7) == 0) bid = (bid & 7) * (nt >> 3) + (bid >> 3);
+  const int tm = bid / ntn, tn = bid % ntn;
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // global -> register staging (macros, not lambdas: the staging arrays must
+  // stay in registers)
+  u32x4 ra[NA][A_CH], rb[NB][B_CH];
+#define X3_GLOAD(k0)                                                              \
+  do {                                                                            \
+    _Pragma("unroll") for (int q = 0; q < NA; ++q)                                \
+    _Pragma("unroll") for (int i = 0; i < A_CH; ++i) {                            \
+      const int id = tid + 256 * i, row = id >> 2, c = id & 3;                    \
+      const int gr = min(m0 + row, p.M - 1);                                      \
+      ra[q][i] = *(const u32x4*)(p.A[q] + (size_t)gr * p.lda + (k0) + 8 * c);     \
+    }                                                                             \
+    _Pragma("unroll") for (int q = 0; q < NB; ++q)                                \
+    _Pragma("unroll") for (int i = 0; i < B_CH; ++i) {                            \
+      const int id = tid + 256 * i, row = id >> 2, c = id & 3;                    \
+      const int gr = min(n0 + row, p.N - 1);                                      \
+      rb[q][i] = *(const u32x4*)(p.B[q] + (size_t)gr * p.ldb + (k0) + 8 * c);     \
+    }                                                                             \
+  } while (0)
+#define X3_SSTORE(buf)                                                                          \
+  do {                                                                                          \
+    uint16_t* s_ = lds + (buf) * STAGE;                                                         \
+    _Pragma("unroll") for (int q = 0; q < NA; ++q)                                              \
+    _Pragma("unroll") for (int i = 0; i < A_CH; ++i) {                                          \
+      const int id = tid + 256 * i, row = id >> 2, c = id & 3;                                  \
+      *(u32x4*)(s_ + q * A_PART + row * LDS_ROW + 8 * c) = ra[q][i];                            \
+    }                                                                                           \
+    _Pragma("unroll") for (int q = 0; q < NB; ++q)                                              \
+    _Pragma("unroll") for (int i = 0; i < B_CH; ++i) {                                          \
+      const int id = tid + 256 * i, row = id >> 2, c = id & 3;                                  \
+      *(u32x4*)(s_ + NA * A_PART + q * B_PART + row * LDS_ROW + 8 * c) = rb[q][i];              \
+    }                                                                                           \
+  } while (0)
+
+  float16v acc[WM][WN];
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int j = 0; j < WN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int nk = p.K / BK;
+  X3_GLOAD(0);
+  X3_SSTORE(0);
+  __syncthreads();
+  const int frow = lane & 31, fk = (lane >> 5) * 8;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) X3_GLOAD((kt + 1) * BK);
+    const uint16_t* s = lds + buf * STAGE;
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 16) {
+      half8 af[NA][WM], bf[NB][WN];
+#pragma unroll
+      for (int q = 0; q < NA; ++q)
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+          af[q][i] = *(const half8*)(s + q * A_PART + (wm * WM * 32 + i * 32 + frow) * LDS_ROW + kk + fk);
+#pragma unroll
+      for (int q = 0; q < NB; ++q)
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+          bf[q][j] = *(const half8*)(s + NA * A_PART + q * B_PART + (wn * WN * 32 + j * 32 + frow) * LDS_ROW + kk + fk);
+#pragma unroll
+      for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j) {
+          if constexpr (MODE == X3_REF) {  // lo, mid, hi times the fp16 weight (tier.cpp:940)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[2][i], bf[0][j], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[1][i], bf[0][j], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[0][i], bf[0][j], acc[i][j], 0, 0, 0);
+          } else {  // hi*hi + hi*lo + lo*hi
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[0][i], bf[0][j], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[0][i], bf[1][j], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[1][i], bf[0][j], acc[i][j], 0, 0, 0);
+          }
+        }
+    }
+    if (kt + 1 < nk) X3_SSTORE(buf ^ 1);
+    __syncthreads();
+  }
+
+  // epilogue: 32x32 accumulator layout -- register r of lane l holds
+  // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+      const int col = n0 + wn * WN * 32 + j * 32 + (lane & 31);
+      if (col >= p.N) continue;
+      const int eb = p.bexp ? p.bexp[col] : 0;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * WM * 32 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (row >= p.M) continue;
+        float v = acc[i][j][r];
+        if (p.aexp || p.bexp) v = ldexpf(v, -((p.aexp ? p.aexp[row] : 0) + eb));
+        float* c = p.C + (size_t)row * p.ldc + col;
+        if (p.beta != 0.f) v = fmaf(p.beta, *c, v);
+        *c = v;
+      }
+    }
+#undef X3_GLOAD
+#undef X3_SSTORE
+}
+
+template <int BM, int BN, int MODE>
+int launch_x3(const X3Args& a, hipStream_t s, const char* who) {
+  using Md = X3Mode<MODE>;
+  const int nt = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+  constexpr size_t lds = 2 * (size_t)(Md::NA * BM + Md::NB * BN) * LDS_ROW * sizeof(uint16_t);
+  static bool attr_set = false;  // dynamic LDS above 64 KiB must be opted into once per kernel
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)gemm_x3_kernel<BM, BN, MODE>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return hip_fail(e, who);
+    attr_set = true;
+  }
+  gemm_x3_kernel<BM, BN, MODE><<<nt, 256, lds, s>>>(a);
+  TM_LAUNCH_CHECK(who);
+  return TIERMM_OK;
+}
+
+int check_nt(const char* who, int M, int N, int K) {
+  if (M < 0 || N < 0 || K < 0) return set_error(TIERMM_EINVAL, "%s: negative size", who);
+  if (K % BK) return set_error(TIERMM_UNSUPPORTED, "%s: K=%d is not a multiple of %d", who, K, BK);
+  return TIERMM_OK;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+
+// x3-ref product on pre-split activations: C[M][ldc] (beta)= sum_parts Xpart[M][K] * W[N][K]^T,
+// parts at xparts + {0, stride, 2*stride} in HML order, W fp16 with row stride ldw.
+int x3ref_nt(const uint16_t* xparts, size_t stride, const uint16_t* W, int ldw, float* C, int ldc, int M, int N,
+             int K, float beta, hipStream_t s, const char* who) {
+  X3Args a{};
+  a.A[0] = xparts;
+  a.A[1] = xparts + stride;
+  a.A[2] = xparts + 2 * stride;
+  a.B[0] = W;
+  a.lda = K;
+  a.ldb = ldw;
+  a.C = C;
+  a.ldc = ldc;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.aexp = nullptr;
+  a.bexp = nullptr;
+  a.beta = beta;
+  return launch_x3<128, 128, X3_REF>(a, s, who);
+}
+
+int split3_launch(const float* x, uint16_t* parts, size_t n, size_t stride, int order, hipStream_t s) {
+  if (n == 0) return TIERMM_OK;
+  const size_t want = (n + 255) / 256;
+  const unsigned grid = (unsigned)(want < 16384 ? want : 16384);
+  split3_kernel<<<grid, 256, 0, s>>>(x, parts, n, stride, order);
+  TM_LAUNCH_CHECK("split3: launch");
+  return TIERMM_OK;
+}
+
+}  // namespace tiermm
+
+using namespace tiermm;
+
+extern "C" {
+
+int tiermm_split3_f16(const float* x, uint16_t* parts, size_t n, size_t part_stride, int order,
+                      tiermm_stream_t stream) {
+  if (order != TIERMM_HML && order != TIERMM_LMH)
+    return set_error(TIERMM_EINVAL, "tiermm_split3_f16: order %d", order);
+  if (part_stride < n) return set_error(TIERMM_EINVAL, "tiermm_split3_f16: part_stride < n");
+  if (n && (!x || !parts)) return set_error(TIERMM_EINVAL, "tiermm_split3_f16: null buffer");
+  return split3_launch(x, parts, n, part_stride, order, (hipStream_t)stream);
+}
+
+int tiermm_x3s_split(const float* src, uint16_t* hi, uint16_t* lo, int32_t* exps, int rows, int cols,
+                     tiermm_stream_t stream) {
+  if (rows < 0 || cols < 0) return set_error(TIERMM_EINVAL, "tiermm_x3s_split: negative size");
+  if (rows == 0) return TIERMM_OK;
+  if (!src || !hi || !lo || !exps) return set_error(TIERMM_EINVAL, "tiermm_x3s_split: null buffer");
+  x3s_split_kernel<<<rows, 256, 0, (hipStream_t)stream>>>(src, hi, lo, exps, cols);
+  TM_LAUNCH_CHECK("tiermm_x3s_split: launch");
+  return TIERMM_OK;
+}
+
+int tiermm_x3s_gemm(const uint16_t* Xhi, const uint16_t* Xlo, const int32_t* xexp, const uint16_t* Whi,
+                    const uint16_t* Wlo, const int32_t* wexp, float* Y, int M, int N, int K, int ldy,
+                    tiermm_stream_t stream) {
+  int st = check_nt("tiermm_x3s_gemm", M, N, K);
+  if (st) return st;
+  if (ldy < N) return set_error(TIERMM_EINVAL, "tiermm_x3s_gemm: ldy < N");
+  if (M == 0 || N == 0) return TIERMM_OK;
+  if (!aligned16(Xhi) || !aligned16(Xlo) || !aligned16(Whi) || !aligned16(Wlo) || !Y || !xexp || !wexp)
+    return set_error(TIERMM_EINVAL, "tiermm_x3s_gemm: operands must be non-null and 16-byte aligned");
+  X3Args a{};
+  a.A[0] = Xhi;
+  a.A[1] = Xlo;
+  a.B[0] = Whi;
+  a.B[1] = Wlo;
+  a.lda = K;
+  a.ldb = K;
+  a.C = Y;
+  a.ldc = ldy;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.aexp = xexp;
+  a.bexp = wexp;
+  a.beta = 0.f;
+  return launch_x3<128, 128, X3_2X2>(a, (hipStream_t)stream, "tiermm_x3s_gemm: launch");
+}
+
+size_t tiermm_x3_gemm_ws_bytes(int m, int n, int k) {
+  (void)m;
+  return (size_t)3 * (size_t)n * (size_t)k * sizeof(uint16_t);
+}
+
+int tiermm_x3_gemm(int opA, int m, int n, int k, const uint16_t* A, int lda, const float* B, float beta, float* C,
+                   int ldc, void* ws, size_t ws_bytes, tiermm_stream_t stream) {
+  const char* who = "tiermm_x3_gemm";
+  if (opA != TIERMM_OP_T && opA != TIERMM_OP_N) return set_error(TIERMM_EINVAL, "%s: opA %d", who, opA);
+  if (opA == TIERMM_OP_N) return set_error(TIERMM_UNSUPPORTED, "%s: the OP_N (dX) layout is not built yet", who);
+  int st = check_nt(who, n, m, k);
+  if (st) return st;
+  if (lda < k || ldc < m) return set_error(TIERMM_EINVAL, "%s: lda < k or ldc < m", who);
+  if (m == 0 || n == 0) return TIERMM_OK;
+  if (!aligned16(A) || (lda % 8) || !B || !C)
+    return set_error(TIERMM_EINVAL, "%s: A must be 16-byte aligned with lda a multiple of 8", who);
+  void* w = nullptr;
+  const size_t nk = (size_t)n * k;
+  st = get_workspace(ws, ws_bytes, tiermm_x3_gemm_ws_bytes(m, n, k), &w, who);
+  if (st) return st;
+  hipStream_t s = (hipStream_t)stream;
+  uint16_t* parts = (uint16_t*)w;
+  st = split3_launch(B, parts, nk, nk, TIERMM_HML, s);
+  if (st) return st;
+  // column-major C(m x n) with ldc == row-major out[n][ldc] = x[n][k] * W[m][k]^T
+  return x3ref_nt(parts, nk, A, lda, C, ldc, n, m, k, beta, s, who);
+}
+
+size_t tiermm_x3_rows_ws_bytes(int M, int K, int N) {
+  (void)N;
+  return (size_t)3 * (size_t)M * (size_t)K * sizeof(uint16_t);
+}
+
+int tiermm_x3_rows(const uint16_t* W, const float* x, float* y, int M, int K, int N, int ldo, void* ws,
+                   size_t ws_bytes, tiermm_stream_t stream) {
+  const char* who = "tiermm_x3_rows";
+  int st = check_nt(who, M, N, K);
+  if (st) return st;
+  if (ldo < N) return set_error(TIERMM_EINVAL, "%s: ldo < N", who);
+  if (M == 0 || N == 0) return TIERMM_OK;
+  if (!aligned16(W) || !x || !y) return set_error(TIERMM_EINVAL, "%s: W must be 16-byte aligned", who);
+  void* w = nullptr;
+  st = get_workspace(ws, ws_bytes, tiermm_x3_rows_ws_bytes(M, K, N), &w, who);
+  if (st) return st;
+  hipStream_t s = (hipStream_t)stream;
+  const size_t mk = (size_t)M * K;
+  st = split3_launch(x, (uint16_t*)w, mk, mk, TIERMM_HML, s);
+  if (st) return st;
+  return x3ref_nt((const uint16_t*)w, mk, W, K, y, ldo, M, N, K, 0.f, s, who);
+}
+
+size_t tiermm_qgemm_ws_bytes(int qtype, int M, int N, int K, int mode) {
+  (void)qtype;
+  (void)mode;
+  return (size_t)N * K * sizeof(uint16_t) + (size_t)3 * M * K * sizeof(uint16_t);
+}
+
+int tiermm_qgemm(const void* W, int qtype, size_t rb, const float* X, float* Y, int M, int N, int K, int ldy,
+                 int mode, float beta, void* ws, size_t ws_bytes, tiermm_stream_t stream) {
+  const char* who = "tiermm_qgemm";
+  int st = check_qweight(who, W, qtype, rb, K);
+  if (st) return st;
+  if (mode != TIERMM_MODE_X3REF) return set_error(TIERMM_UNSUPPORTED, "%s: mode %d is not built yet", who, mode);
+  st = check_nt(who, M, N, K);
+  if (st) return st;
+  if (ldy < N) return set_error(TIERMM_EINVAL, "%s: ldy < N", who);
+  if (M == 0 || N == 0) return TIERMM_OK;
+  if (!X || !Y) return set_error(TIERMM_EINVAL, "%s: null buffer", who);
+  void* w = nullptr;
+  st = get_workspace(ws, ws_bytes, tiermm_qgemm_ws_bytes(qtype, M, N, K, mode), &w, who);
+  if (st) return st;
+  hipStream_t s = (hipStream_t)stream;
+  uint16_t* w16 = (uint16_t*)w;
+  uint16_t* parts = w16 + (size_t)N * K;
+  const size_t mk = (size_t)M * K;
+  st = dequant_f16_rows(W, qtype, rb, K, (size_t)N, w16, s);
+  if (st) return st;
+  st = split3_launch(X, parts, mk, mk, TIERMM_HML, s);
+  if (st) return st;
+  return x3ref_nt(parts, mk, w16, K, Y, ldy, M, N, K, beta, s, who);
+}
+
+}  // extern "C"
