@@ -17,10 +17,20 @@
 
 namespace tiermm {
 
+// The empty asm statements pin each conversion to a plain v_cvt_f32_f16 /
+// v_cvt_f16_f32 on an fp32 value.  Without them the compiler folds the
+// conversions into v_fma_mix* instructions (fp16 operands read in place, fp16
+// result rounded inside the fma), which gave results that differ from
+// fp32-then-RNE for some inputs (found by the bit-exact dequant tests).
 __device__ __forceinline__ float h2f(uint32_t h16) {
-  return (float)__builtin_bit_cast(_Float16, (uint16_t)h16);
+  float f = (float)__builtin_bit_cast(_Float16, (uint16_t)h16);
+  asm volatile("" : "+v"(f));
+  return f;
 }
-__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+__device__ __forceinline__ uint16_t f2h(float f) {
+  asm volatile("" : "+v"(f));
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
 
 // hip_bfloat16(float): round to nearest even on the top 16 bits; NaN stays NaN.
 __device__ __forceinline__ uint16_t f2bf(float f) {

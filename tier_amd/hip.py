@@ -57,9 +57,11 @@ def attribute(attr: int, dev: int = 0) -> int:
 
 
 # hipDeviceAttribute_t values used by the benchmark
+# (values of the ROCm 7 hip_runtime_api.h enum)
 ATTR_CLOCK_RATE_KHZ = 5      # hipDeviceAttributeClockRate
-ATTR_MEM_CLOCK_KHZ = 17      # hipDeviceAttributeMemoryClockRate
-ATTR_MULTIPROCESSORS = 45    # hipDeviceAttributeMultiprocessorCount
+ATTR_MEM_BUS_WIDTH = 59      # hipDeviceAttributeMemoryBusWidth
+ATTR_MEM_CLOCK_KHZ = 60      # hipDeviceAttributeMemoryClockRate
+ATTR_MULTIPROCESSORS = 63    # hipDeviceAttributeMultiprocessorCount
 
 
 class DeviceBuffer:
