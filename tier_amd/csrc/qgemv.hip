@@ -67,11 +67,15 @@ int launch_generic(const void* W, size_t rb, const float* x, float* y, int N, in
 
 }  // namespace
 
+int qgemv_q4k(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s);
+constexpr int kQ4kMaxK = 14336;  // equals the limit in qgemv_q4k.hip
+
 int qgemv_dispatch(const void* W, int qtype, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
   switch (qtype) {
     case QT_Q8_0: return launch_generic<QT_Q8_0>(W, rb, x, y, N, K, s);
     case QT_Q5_0: return launch_generic<QT_Q5_0>(W, rb, x, y, N, K, s);
-    case QT_Q4_K: return launch_generic<QT_Q4_K>(W, rb, x, y, N, K, s);
+    case QT_Q4_K:  // the MFMA kernel stages x in LDS up to kQ4kMaxK; beyond, the generic kernel
+      return K <= kQ4kMaxK ? qgemv_q4k(W, rb, x, y, N, K, s) : launch_generic<QT_Q4_K>(W, rb, x, y, N, K, s);
     case QT_Q5_K: return launch_generic<QT_Q5_K>(W, rb, x, y, N, K, s);
     default: return launch_generic<QT_Q6_K>(W, rb, x, y, N, K, s);
   }
