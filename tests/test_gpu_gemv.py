@@ -63,6 +63,19 @@ def test_gemv_ragged_shapes(gpu, t, N, K):
     assert oracle.rel_fro(y, oracle.gemv_f64(blocks, t, x, N, K)) <= TOL
 
 
+@pytest.mark.parametrize("N,K", [(10250, 4352), (10240, 256), (10256, 8192), (10240, 1280)])
+def test_gemv_q4k_tall_ragged(gpu, N, K):
+    """Tall q4_K matrices (the producer-wave kernel): a partial last row tile, K halves of
+    unequal super-block counts (17 = 8 + 9), a half with no super-block (K = 256)."""
+    t = tier_amd.Q4_K
+    rng = np.random.default_rng(N + K)
+    blocks = oracle.random_blocks(rng, t, N * (K // 256)).reshape(N, -1)
+    x = rng.standard_normal(K).astype(np.float32)
+    x[::131] *= np.float32(300.0)
+    y = _gemv(blocks, t, x, N, K)
+    assert oracle.rel_fro(y, oracle.gemv_f64(blocks, t, x, N, K)) <= TOL
+
+
 def test_gemv_zero_and_extreme_inputs(gpu):
     t, N, K = tier_amd.Q4_K, 64, 1024
     blocks = quantized_weight(t, N, K, seed=5)

@@ -1,0 +1,165 @@
+// q4k_mfma.h -- pieces shared by the Q4_K int8-MFMA decode GEMV kernels:
+// the x preparation into int8 digits, the LDS-DMA weight stage and the
+// per-super-block MFMA + scale epilogue.  The layouts are described in
+// qgemv_q4k.hip.
+#pragma once
+
+#include "tm_device.h"
+
+namespace tiermm {
+namespace {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int SB_BYTES = 144;          // Q4_K super-block
+constexpr int XQ_SB = 1024;            // LDS bytes of x digits per super-block: 4 t x 4 a x 4 digits x 16
+constexpr int XQ_T = 256;              // per MFMA step t
+constexpr int META_SB = 64;            // 4 g x float4 (f_g, f_4+g, S_g, S_4+g)
+constexpr int ZERO_BYTES = 4 * XQ_T;   // zero rows read by the A lanes that carry no digit
+
+// Prepare x elements [16h, 16h+16) of sub-block s (h = half, values in v): the
+// partner thread (lane ^ 1) holds the other half; both reach this together.
+__device__ __forceinline__ void prep_half(int s, int h, const float (&v)[16], uint8_t* xq, float* meta) {
+  float amax = 0.f, sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    amax = fmaxf(amax, fabsf(v[i]));
+    sum += v[i];
+  }
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  sum += __shfl_xor(sum, 1, 64);
+  int e = 0;
+  if (amax > 0.f) {
+    int ex;
+    (void)frexpf(amax, &ex);
+    e = min(126, max(-126, 29 - ex));
+  }
+  const int sb = s >> 3, sg = s & 7;              // super-block, sub-block within it
+  const int t = 2 * (sg >> 2) + (sg & 1);         // MFMA step covering this sub-block
+  const int a = 2 * ((sg & 3) >> 1) + h;          // virtual group of these 16 elements
+  if (h == 0) {
+    meta[sb * 16 + (sg & 3) * 4 + (sg >> 2)] = ldexpf(1.f, -e);
+    meta[sb * 16 + (sg & 3) * 4 + 2 + (sg >> 2)] = sum;
+  }
+  // x_int = trunc(x * 2^e): |x * 2^e| < 2^29, integral already wherever it is
+  // >= 2^23, otherwise off by < 1 unit (2^-28 of the sub-block max).
+  // Balanced int8 digits of x_int: with y = x_int + 0x808080, the digits are
+  // bytes 0..2 of y with the top bit flipped and byte 3 of y.
+  uint32_t yv[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) yv[i] = (uint32_t)(int)ldexpf(v[i], e) + 0x00808080u;
+  u32x4 L[4];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {  // 4x4 byte transpose of four elements
+    const uint32_t y0 = yv[4 * w], y1 = yv[4 * w + 1], y2 = yv[4 * w + 2], y3 = yv[4 * w + 3];
+    const uint32_t p01l = __builtin_amdgcn_perm(y1, y0, 0x05010400u), p01h = __builtin_amdgcn_perm(y1, y0, 0x07030602u);
+    const uint32_t p23l = __builtin_amdgcn_perm(y3, y2, 0x05010400u), p23h = __builtin_amdgcn_perm(y3, y2, 0x07030602u);
+    L[0][w] = __builtin_amdgcn_perm(p23l, p01l, 0x05040100u) ^ 0x80808080u;
+    L[1][w] = __builtin_amdgcn_perm(p23l, p01l, 0x07060302u) ^ 0x80808080u;
+    L[2][w] = __builtin_amdgcn_perm(p23h, p01h, 0x05040100u) ^ 0x80808080u;
+    L[3][w] = __builtin_amdgcn_perm(p23h, p01h, 0x07060302u);
+  }
+  uint8_t* dst = xq + sb * XQ_SB + t * XQ_T + a * 64;
+#pragma unroll
+  for (int l = 0; l < 4; ++l) *(u32x4*)(dst + 16 * l) = L[l];
+}
+
+// Vector-memory traffic of this kernel is issued and waited for by hand: the
+// compiler's wait insertion cannot follow global->LDS loads (it falls back to
+// waiting for everything before LDS reads), which would serialise the weight
+// stream.  Every vector load below is one instruction per wave regardless of
+// the lane mask, and loads retire in order, so "s_waitcnt vmcnt(N)" means all
+// but the N most recent ones have landed.
+__device__ __forceinline__ u32x4 gload16(const void* p) {
+  u32x4 r;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p) : "memory");
+  return r;
+}
+// 16 bytes per lane from p into LDS at lds_addr + 16*lane (lds_addr wave-uniform, through M0).
+__device__ __forceinline__ void dma16(const void* p, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(p),
+               "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+               : "memory");
+}
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(size_t)(const __attribute__((address_space(3))) uint8_t*)p;
+}
+
+// Async loads of group `grp` (GS super-blocks of the wave's 16 rows) into an
+// LDS stage in row-major order (row n at n*GS*144).  roff[j] / coff[j]: row
+// (0..15) and byte of the 16 bytes lane `lane` brings with load j; bytes past the
+// wave's K range re-read the last valid 16 bytes of the row segment, so the
+// number of loads is fixed.  When the stage is not a whole number of 1 KiB
+// loads, the last load runs on the lanes that still have bytes to bring.
+template <int GS>
+struct Stage {
+  static constexpr int GRP = GS * SB_BYTES;               // bytes of one row's group
+  static constexpr int BYTES = 16 * GRP;                  // one stage
+  static constexpr int NLD = (BYTES + 1023) / 1024;       // loads per stage
+  static constexpr int LAST = (BYTES - (NLD - 1) * 1024) / 16;  // lanes of the last load
+};
+
+template <int GS>
+__device__ __forceinline__ void load_group(const uint8_t* base0, size_t rb, const int (&roff)[Stage<GS>::NLD],
+                                           const int (&coff)[Stage<GS>::NLD], int lane, int grp, int nsb,
+                                           uint32_t stage) {
+  constexpr int NLD = Stage<GS>::NLD;
+  const int valid = min(GS, nsb - GS * grp);
+  const int lastb = valid > 0 ? SB_BYTES * valid - 16 : 0;
+  const uint8_t* b = base0 + (size_t)max(0, min(grp, (nsb - 1) / GS)) * Stage<GS>::GRP;
+#pragma unroll
+  for (int j = 0; j < NLD; ++j)
+    if (j < NLD - 1 || Stage<GS>::LAST == 64 || lane < Stage<GS>::LAST)
+      dma16(b + (size_t)roff[j] * rb + min(coff[j], lastb), stage + j * 1024);
+}
+
+constexpr int xq_bytes(int kmax) { return (kmax / 256) * (XQ_SB + META_SB) + ZERO_BYTES; }
+
+// One super-block of a 16-row tile (gemv_q's per-element sum, tier.cpp:299-306,
+// regrouped by sub-block): hp = the header of row n's super-block in the stage
+// (qs follows at +16), a0p / a1p = this lane's A-operand rows for MFMA parities
+// 0 / 1, mt = (2^-e_g, 2^-e_4+g, S_g, S_4+g) of the super-block's x.  Returns
+// acc + d * sum_s sc_s * f_s * D_s - dmin * sum_s m_s * S_s over sub-blocks g, 4+g.
+__device__ __forceinline__ float q4k_superblock(const uint8_t* hp, int g, const uint8_t* a0p, const uint8_t* a1p,
+                                                const float* mtp, float acc) {
+  const u32x4 H = *(const u32x4*)hp;
+  const u32x4 cA = *(const u32x4*)(hp + 16 + 16 * g);
+  const u32x4 cB = *(const u32x4*)(hp + 80 + 16 * g);
+  const i32x4 A0 = *(const i32x4*)(a0p), A1 = *(const i32x4*)(a1p + XQ_T);
+  const i32x4 A2 = *(const i32x4*)(a0p + 2 * XQ_T), A3 = *(const i32x4*)(a1p + 3 * XQ_T);
+  i32x4 B0, B1, B2, B3;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    B0[w] = (int)(cA[w] & 0x0f0f0f0fu);
+    B1[w] = (int)((cA[w] >> 4) & 0x0f0f0f0fu);
+    B2[w] = (int)(cB[w] & 0x0f0f0f0fu);
+    B3[w] = (int)((cB[w] >> 4) & 0x0f0f0f0fu);
+  }
+  const i32x4 z = {0, 0, 0, 0};
+  i32x4 Ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, z, 0, 0, 0);
+  Ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, Ca, 0, 0, 0);
+  i32x4 Cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(A2, B2, z, 0, 0, 0);
+  Cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(A3, B3, Cb, 0, 0, 0);
+  // |C| <= 32*15*128: both halves below 2^24, so the two conversions are exact
+  const float Da = fmaf((float)(Ca[3] * 256 + Ca[2]), 65536.f, (float)(Ca[1] * 256 + Ca[0]));
+  const float Db = fmaf((float)(Cb[3] * 256 + Cb[2]), 65536.f, (float)(Cb[1] * 256 + Cb[0]));
+  const float4 mt = *(const float4*)mtp;
+  const int sh = 8 * g;  // scale byte of sub-blocks g and 4+g (quant.h:47-48)
+  const uint32_t hy = H[1], hz = H[2], hw = H[3];
+  const int sca = (hy >> sh) & 63, mna = (hz >> sh) & 63;
+  const int scb = ((hw >> sh) & 15) | (((hy >> (sh + 6)) & 3) << 4);
+  const int mnb = ((hw >> (sh + 4)) & 15) | (((hz >> (sh + 6)) & 3) << 4);
+  const float d = h2f(H[0] & 0xffffu), dmin = h2f(H[0] >> 16);
+  const float u = fmaf((float)scb * mt.y, Db, (float)sca * mt.x * Da);
+  const float m = fmaf((float)mnb, mt.w, (float)mna * mt.z);
+  acc = fmaf(d, u, acc);
+  return fmaf(-dmin, m, acc);
+}
+
+}  // namespace
+}  // namespace tiermm

@@ -68,13 +68,15 @@ int launch_generic(const void* W, size_t rb, const float* x, float* y, int N, in
 }  // namespace
 
 int qgemv_q4k(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s);
+int qgemv_q4k_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s);
 constexpr int kQ4kMaxK = 14336;  // equals the limit in qgemv_q4k.hip
 
 int qgemv_dispatch(const void* W, int qtype, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
   switch (qtype) {
     case QT_Q8_0: return launch_generic<QT_Q8_0>(W, rb, x, y, N, K, s);
     case QT_Q5_0: return launch_generic<QT_Q5_0>(W, rb, x, y, N, K, s);
-    case QT_Q4_K:  // the MFMA kernel stages x in LDS up to kQ4kMaxK; beyond, the generic kernel
+    case QT_Q4_K:  // MFMA kernels up to kQ4kMaxK (x digits in LDS); beyond, the generic kernel
+      if (K <= 8192 && (N + 15) / 16 >= 640) return qgemv_q4k_ws(W, rb, x, y, N, K, s);
       return K <= kQ4kMaxK ? qgemv_q4k(W, rb, x, y, N, K, s) : launch_generic<QT_Q4_K>(W, rb, x, y, N, K, s);
     case QT_Q5_K: return launch_generic<QT_Q5_K>(W, rb, x, y, N, K, s);
     default: return launch_generic<QT_Q6_K>(W, rb, x, y, N, K, s);
