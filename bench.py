@@ -93,6 +93,19 @@ def time_launches(hip, stream, launch, steps: int, warmup: int) -> float:
     return per
 
 
+def measured_traffic():
+    """HBM bytes per headline launch from the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter's reading for a copy
+    of known size), or (None, None) when no summary is present."""
+    path = os.path.join(ROOT, "profiles", "q4k_gemv_13824x5120_traffic.json")
+    try:
+        with open(path) as f:
+            d = json.load(f)
+    except (OSError, ValueError):
+        return None, None
+    return int(d["bytes_per_launch"]), f"profiles/q4k_gemv_13824x5120.md ({d['kernel']})"
+
+
 def cpu_baseline(case: GemvCase, budget_s: float):
     """The reference q_val GEMV (oracle/_ref, built from quant.h) on every host thread; bounded repetitions."""
     import oracle
@@ -200,6 +213,7 @@ def main() -> int:
                                            "us_per_call": round(km * 1e3, 1), "includes": "X split + GEMM"}
         del bufs, Wf, Xf
 
+    traffic, traffic_src = measured_traffic()
     cpu = None
     if not args.no_cpu:
         log("bench: cpu baseline")
@@ -225,8 +239,8 @@ def main() -> int:
         "config": {"workload": "q4_K decode GEMV 13824x5120 (M=1), tiermm_qgemv", "N": 13824, "K": 5120, "M": 1,
                    "bytes_per_step": head.bytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "us_per_launch": round(per * 1e3, 3)},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": traffic_src, "us_per_launch": round(per * 1e3, 3)},
         "cpu_baseline": cpu,
         "device": {"cus": cus, "clock_mhz": clk_mhz},
         "secondary": secondary,
