@@ -10,7 +10,6 @@ namespace tiermm {
 namespace {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int SB_BYTES = 144;          // Q4_K super-block
 constexpr int XQ_SB = 1024;            // LDS bytes of x digits per super-block: 4 t x 4 a x 4 digits x 16
@@ -63,31 +62,6 @@ __device__ __forceinline__ void prep_half(int s, int h, const float (&v)[16], ui
   uint8_t* dst = xq + sb * XQ_SB + t * XQ_T + a * 64;
 #pragma unroll
   for (int l = 0; l < 4; ++l) *(u32x4*)(dst + 16 * l) = L[l];
-}
-
-// Vector-memory traffic of this kernel is issued and waited for by hand: the
-// compiler's wait insertion cannot follow global->LDS loads (it falls back to
-// waiting for everything before LDS reads), which would serialise the weight
-// stream.  Every vector load below is one instruction per wave regardless of
-// the lane mask, and loads retire in order, so "s_waitcnt vmcnt(N)" means all
-// but the N most recent ones have landed.
-__device__ __forceinline__ u32x4 gload16(const void* p) {
-  u32x4 r;
-  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p) : "memory");
-  return r;
-}
-// 16 bytes per lane from p into LDS at lds_addr + 16*lane (lds_addr wave-uniform, through M0).
-__device__ __forceinline__ void dma16(const void* p, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(p),
-               "s"(__builtin_amdgcn_readfirstlane(lds_addr))
-               : "memory");
-}
-template <int N>
-__device__ __forceinline__ void vm_wait() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(size_t)(const __attribute__((address_space(3))) uint8_t*)p;
 }
 
 // Async loads of group `grp` (GS super-blocks of the wave's 16 rows) into an

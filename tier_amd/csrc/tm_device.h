@@ -155,6 +155,32 @@ struct Dec<QT_Q6_K> {  // quant.h:88-90 -- 210-byte super-blocks (2-byte aligned
   }
 };
 
+// Hand-issued vector memory for the kernels that stream through LDS: the
+// compiler's wait insertion cannot follow global->LDS loads (it falls back to
+// waiting for everything before LDS reads), which would serialise the stream.
+// Every vector load below is one instruction per wave regardless of the lane
+// mask, and loads retire in order, so "s_waitcnt vmcnt(N)" means all but the N
+// most recent ones have landed.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x4 gload16(const void* p) {
+  u32x4 r;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p) : "memory");
+  return r;
+}
+// 16 bytes per lane from p into LDS at lds_addr + 16*lane (lds_addr wave-uniform, through M0).
+__device__ __forceinline__ void dma16(const void* p, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(p),
+               "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+               : "memory");
+}
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(size_t)(const __attribute__((address_space(3))) uint8_t*)p;
+}
+
 // Launch-shape guard: kernels assume their block size; a mismatch is a host bug.
 #define TM_LAUNCH_CHECK(what)                                  \
   do {                                                         \

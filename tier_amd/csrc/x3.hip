@@ -28,7 +28,6 @@ namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float16v __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------------------------ splits
 __global__ __launch_bounds__(256) void split3_kernel(const float* __restrict__ x, uint16_t* __restrict__ parts,
@@ -246,6 +245,179 @@ __global__ __launch_bounds__(256) void gemm_x3_kernel(const X3Args p) {
 #undef X3_SSTORE
 }
 
+// ------------------------------------------------------ big-tile GEMM core
+// Same products as gemm_x3_kernel on a 256 x 320 workgroup tile: 8 waves (4
+// along M x 2 along N), each 64 x 160 = 2 x 5 blocks of 32x32, K step 32.  The
+// operand tiles reach LDS by global_load_lds_dwordx4 (no register staging),
+// double-buffered: after the barrier that publishes stage k, the loads of
+// stage k+1 go out into the other buffer, then stage k is multiplied.  A row of
+// 32 halfs is four 16-byte chunks, chunk c stored at slot c ^ ((row >> 2) & 3):
+// a fragment read (16 consecutive rows, one chunk) then touches 16 distinct
+// 16-byte bank groups.  Per k-substep a wave reads 2*NA + 5*NB fragments for
+// 30 MFMAs (x3-2x2), which keeps LDS below half its bandwidth at full MFMA rate.
+constexpr int XB_M = 256, XB_N = 320, XB_WM = 2, XB_WN = 5;
+
+template <int MODE>
+__global__ __launch_bounds__(512) void gemm_x3_big(const X3Args p) {
+  using Md = X3Mode<MODE>;
+  constexpr int NA = Md::NA, NB = Md::NB;
+  constexpr int A_PART = XB_M * 64, B_PART = XB_N * 64;  // bytes of one part per stage
+  constexpr int STAGE = NA * A_PART + NB * B_PART;
+  constexpr int A_INST = XB_M * 64 / 1024, B_INST = XB_N * 64 / 1024;  // 1 KiB loads per part
+  constexpr int NINST = NA * A_INST + NB * B_INST;
+  constexpr int PER_WAVE = (NINST + 7) / 8;
+  extern __shared__ __attribute__((aligned(16))) uint16_t lds_h[];
+  uint8_t* lds = (uint8_t*)lds_h;
+
+  // Tile order: workgroups go round-robin over the 8 XCDs, so XCD x gets the
+  // x-th eighth of the tile sequence; the sequence walks groups of 4 tile rows
+  // column by column, so an XCD's share is a compact block (4 x 8 tiles at
+  // config 2) and its L2 holds few distinct operand panels.
+  const int ntm = (p.M + XB_M - 1) / XB_M, ntn = (p.N + XB_N - 1) / XB_N, nt = ntm * ntn;
+  int t = blockIdx.x;
+  if ((nt & 7) == 0) t = (t & 7) * (nt >> 3) + (t >> 3);
+  constexpr int GM = 4;
+  const int grp = t / (GM * ntn), first = grp * GM, gm = min(GM, ntm - first);
+  const int tin = t - grp * GM * ntn;
+  const int tm = first + tin % gm, tn = tin / gm;
+  const int m0 = tm * XB_M, n0 = tn * XB_N;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 3, wn = wave >> 2;
+  const uint32_t lds0 = lds_addr(lds);
+
+  // DMA of stage kt into buffer buf: instruction t = wave + 8u covers 16 rows
+  // of one part.  Sources and LDS offsets are fixed per lane, so they are set
+  // up once (no loads of kernel arguments inside the K loop, whose waits would
+  // also wait for the DMA).
+  const uint16_t* gsrc[PER_WAVE];
+  uint32_t loff[PER_WAVE];
+  {
+    const int drow = lane >> 2, dslot = lane & 3;
+#pragma unroll
+    for (int u = 0; u < PER_WAVE; ++u) {
+      const int t = min(wave + 8 * u, NINST - 1);
+      const uint16_t* src;
+      int ld, lim, r0, base, ch;
+      if (t < NA * A_INST) {
+        const int q = t / A_INST;
+        ch = t % A_INST;
+        src = q == 0 ? p.A[0] : q == 1 ? p.A[1] : p.A[2];
+        ld = p.lda; lim = p.M; r0 = m0; base = q * A_PART;
+      } else {
+        const int q = (t - NA * A_INST) / B_INST;
+        ch = (t - NA * A_INST) % B_INST;
+        src = q == 0 ? p.B[0] : p.B[1];
+        ld = p.ldb; lim = p.N; r0 = n0; base = NA * A_PART + q * B_PART;
+      }
+      const int row = ch * 16 + drow;
+      const int kc = dslot ^ ((row >> 2) & 3);
+      gsrc[u] = src + (size_t)min(r0 + row, lim - 1) * ld + kc * 8;
+      loff[u] = (uint32_t)(base + ch * 1024);
+    }
+  }
+  auto issue = [&](int kt, int buf) __attribute__((always_inline)) {
+    const int k0 = kt * BK;
+#pragma unroll
+    for (int u = 0; u < PER_WAVE; ++u)
+      if (wave + 8 * u < NINST) dma16(gsrc[u] + k0, lds0 + buf * STAGE + loff[u]);
+  };
+
+  float16v acc[XB_WM][XB_WN];
+#pragma unroll
+  for (int i = 0; i < XB_WM; ++i)
+#pragma unroll
+    for (int j = 0; j < XB_WN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int fr = lane & 31, fh = lane >> 5;
+  const int sw = (fr >> 2) & 3;
+  // byte offsets of this lane's fragment rows: chunk (2*kk + fh) of row fr
+  const uint32_t cofs0 = (uint32_t)(fr * 64 + ((fh ^ sw) * 16));
+  const uint32_t cofs1 = (uint32_t)(fr * 64 + (((2 + fh) ^ sw) * 16));
+  const int nk = p.K / BK;
+  issue(0, 0);
+  for (int kt = 0; kt < nk; ++kt) {
+    vm_wait<0>();
+    __syncthreads();  // stage kt is in LDS for every wave; buffer kt+1 is free
+    if (kt + 1 < nk) issue(kt + 1, (kt + 1) & 1);
+    const uint8_t* s = lds + (kt & 1) * STAGE;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const uint32_t co = kk ? cofs1 : cofs0;
+      // all fragments of the substep first, then the MFMAs product-major, so
+      // consecutive MFMAs on one accumulator are XB_WM*XB_WN apart
+      half8 af[NA][XB_WM], bf[NB][XB_WN];
+#pragma unroll
+      for (int q = 0; q < NA; ++q)
+#pragma unroll
+        for (int i = 0; i < XB_WM; ++i)
+          af[q][i] = *(const half8*)(s + q * A_PART + (wm * 64 + i * 32) * 64 + co);
+#pragma unroll
+      for (int q = 0; q < NB; ++q)
+#pragma unroll
+        for (int j = 0; j < XB_WN; ++j)
+          bf[q][j] = *(const half8*)(s + NA * A_PART + q * B_PART + (wn * 160 + j * 32) * 64 + co);
+      if constexpr (MODE == X3_REF) {  // lo, mid, hi times the fp16 weight (tier.cpp:940)
+#pragma unroll
+        for (int pa = 2; pa >= 0; --pa)
+#pragma unroll
+          for (int j = 0; j < XB_WN; ++j)
+#pragma unroll
+            for (int i = 0; i < XB_WM; ++i)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[pa][i], bf[0][j], acc[i][j], 0, 0, 0);
+      } else {  // hi*hi + hi*lo + lo*hi
+        constexpr int PA[3] = {0, 0, 1}, PB[3] = {0, 1, 0};
+#pragma unroll
+        for (int pr = 0; pr < 3; ++pr)
+#pragma unroll
+          for (int j = 0; j < XB_WN; ++j)
+#pragma unroll
+            for (int i = 0; i < XB_WM; ++i)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[PA[pr]][i], bf[PB[pr]][j], acc[i][j], 0, 0, 0);
+      }
+    }
+  }
+
+  // epilogue: register r of lane l holds row 8*(r/4) + 4*(l/32) + r%4, column l%32
+#pragma unroll
+  for (int i = 0; i < XB_WM; ++i)
+#pragma unroll
+    for (int j = 0; j < XB_WN; ++j) {
+      const int col = n0 + wn * 160 + j * 32 + (lane & 31);
+      if (col >= p.N) continue;
+      const int eb = p.bexp ? p.bexp[col] : 0;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (row >= p.M) continue;
+        float v = acc[i][j][r];
+        if (p.aexp || p.bexp) v = ldexpf(v, -((p.aexp ? p.aexp[row] : 0) + eb));
+        float* c = p.C + (size_t)row * p.ldc + col;
+        if (p.beta != 0.f) v = fmaf(p.beta, *c, v);
+        *c = v;
+      }
+    }
+}
+
+template <int MODE>
+int launch_x3_big(const X3Args& a, hipStream_t s, const char* who) {
+  using Md = X3Mode<MODE>;
+  const int nt = ((a.M + XB_M - 1) / XB_M) * ((a.N + XB_N - 1) / XB_N);
+  constexpr size_t lds = 2 * (size_t)(Md::NA * XB_M + Md::NB * XB_N) * 64;
+  static_assert(lds <= 160 * 1024, "LDS budget");
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)gemm_x3_big<MODE>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)lds);
+    if (e != hipSuccess) return hip_fail(e, who);
+    attr_set = true;
+  }
+  gemm_x3_big<MODE><<<nt, 512, lds, s>>>(a);
+  TM_LAUNCH_CHECK(who);
+  return TIERMM_OK;
+}
+
 template <int BM, int BN, int MODE>
 int launch_x3(const X3Args& a, hipStream_t s, const char* who) {
   using Md = X3Mode<MODE>;
@@ -353,6 +525,9 @@ int tiermm_x3s_gemm(const uint16_t* Xhi, const uint16_t* Xlo, const int32_t* xex
   a.aexp = xexp;
   a.bexp = wexp;
   a.beta = 0.f;
+  // the 256x320 tile needs enough tiles to occupy the CUs; smaller problems use 128x128
+  const long big_tiles = (long)((M + XB_M - 1) / XB_M) * ((N + XB_N - 1) / XB_N);
+  if (big_tiles >= 192) return launch_x3_big<X3_2X2>(a, (hipStream_t)stream, "tiermm_x3s_gemm: launch");
   return launch_x3<128, 128, X3_2X2>(a, (hipStream_t)stream, "tiermm_x3s_gemm: launch");
 }
 
