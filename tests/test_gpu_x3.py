@@ -85,6 +85,19 @@ def test_x3s_gemm_config2_sampled(gpu):
     assert oracle.rel_fro(Y[rows], ref) <= BAR
 
 
+def test_x3s_gemm_big_tiles_ragged(gpu):
+    """Large enough for the 256x320-tile kernel, with partial tiles along M and N."""
+    M, N, K = 4100, 5000, 640
+    W = (np.random.default_rng(10).standard_normal((N, K), dtype=np.float32) * 0.02).astype(np.float32)
+    X = activations(M, K, seed=11)
+    Y = _x3s_gemm(X, W)
+    rows = np.concatenate([np.arange(8), np.arange(M - 8, M), np.random.default_rng(2).choice(M, 112, replace=False)])
+    ref = X[rows].astype(np.float64) @ W.astype(np.float64).T
+    assert np.all(np.isfinite(Y))
+    assert oracle.rel_fro(Y[rows], ref) <= BAR
+    assert oracle.rel_fro(Y[rows][:, -7:], ref[:, -7:]) <= BAR
+
+
 def _fp16(w):
     return oracle.h2f(oracle.f2h(w)).reshape(w.shape)
 
@@ -134,6 +147,26 @@ def test_qgemm_x3ref(gpu, name, t, M, N, K):
     got = Y.download(np.float32, M * N).reshape(M, N)
     w16 = oracle.h2f(oracle.dequant(blocks, t, K, oracle.OUT_F16)).reshape(N, K)
     ref = x.astype(np.float64) @ w16.astype(np.float64).T
+    assert oracle.rel_fro(got, ref) <= BAR
+
+
+@pytest.mark.parametrize("M,N,K,beta", [(130, 100, 768, 0.0), (1, 50, 256, 0.0), (257, 1000, 2048, 1.0),
+                                         (512, 5120, 1024, 0.0)])
+def test_qgemm_q4k_fused_shapes(gpu, M, N, K, beta):
+    """The fused q4_K kernel: partial tiles along M and N, one-row and one-super-block
+    cases, beta = 1 accumulation, random blocks with extreme scale fields."""
+    t = tier_amd.Q4_K
+    rng = np.random.default_rng(M + N + K)
+    blocks = oracle.random_blocks(rng, t, N * (K // 256)).reshape(N, -1)
+    x = activations(M, K, seed=22)
+    y0 = rng.standard_normal((M, N)).astype(np.float32)
+    W, X, Y = hip.to_device(blocks), hip.to_device(x), hip.to_device(y0)
+    tier_amd.qgemm(W.ptr, t, tier_amd.q_row_bytes(t, K), X.ptr, Y.ptr, M, N, K, beta=beta)
+    hip.synchronize()
+    got = Y.download(np.float32, M * N).reshape(M, N)
+    w16 = oracle.h2f(oracle.dequant(blocks, t, K, oracle.OUT_F16)).reshape(N, K)
+    ref = x.astype(np.float64) @ w16.astype(np.float64).T + beta * y0.astype(np.float64)
+    assert np.all(np.isfinite(got))
     assert oracle.rel_fro(got, ref) <= BAR
 
 

@@ -5,6 +5,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -90,6 +91,27 @@ int get_workspace(void* ws, size_t ws_bytes, size_t need, void** out, const char
     p.bytes = grow;
   }
   *out = p.ptr;
+  return TIERMM_OK;
+}
+
+// Compute units of the current device, read once per device.
+int device_cus(int* cus) {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "device_cus: hipGetDevice");
+  if (dev >= 0 && dev < 64) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) {
+      *cus = c;
+      return TIERMM_OK;
+    }
+  }
+  int c = 0;
+  e = hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return hip_fail(e, "device_cus: hipDeviceGetAttribute");
+  if (dev >= 0 && dev < 64) cache[dev].store(c, std::memory_order_relaxed);
+  *cus = c;
   return TIERMM_OK;
 }
 

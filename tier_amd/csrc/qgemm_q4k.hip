@@ -1,0 +1,262 @@
+// qgemm_q4k.hip -- fused q4_K dequant + x3-ref GEMM for prefill (M > 1).
+//
+// Y[M][ldy] (beta)= sum over the parts p of x (lo, mid, hi) of X_p[M][K] * W16[N][K]^T,
+// W16 = fp16(q_val(W_n, k)) -- the training path's dq_k<tier_fp16> (tier.cpp:515,
+// 293-298) followed by fp3gemm (tier.cpp:922-943) -- without writing W16 to
+// memory: the q4_K rows are decoded into the LDS B tile as the K loop needs
+// them.
+//
+// Tiling: a workgroup owns BM=128 rows of X x BN rows of W (BN in 64..128, a
+// multiple of 16 picked per shape so the tile count fills the CUs); 4 waves,
+// wave w the X rows [32w, 32w+32) against all BN columns, on
+// v_mfma_f32_16x16x32_f16 (2 x BN/16 blocks per wave).  K advances 32 per
+// stage (one q4_K sub-block):
+//   * the three x parts (pre-split, HML planes) reach LDS by
+//     global_load_lds_dwordx4, double-buffered;
+//   * thread (r, h) of the first 2*BN decodes elements [16h, 16h+16) of the
+//     sub-block of W row r: its raw header and 16 qs bytes are loaded two stages
+//     ahead into registers, decoded exactly as q_val (d*sc*q - dmin*m, one
+//     rounding), rounded to fp16 (v_cvt, RNE) and stored in the other B buffer
+//     while the current stage's MFMAs run.
+// LDS rows hold 32 halfs as four 16-byte chunks, chunk c at slot
+// c ^ ((row >> 2) & 3), so the fragment reads (16 rows x 4 chunks) hit
+// distinct bank groups.
+#include "tm_device.h"
+
+namespace tiermm {
+
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+
+constexpr int QBM = 128, QBK = 32;
+constexpr int XPART = QBM * 64;  // bytes of one x part per stage
+constexpr int XRING = 4;         // x stages in LDS: three in flight while one is multiplied
+
+struct QArgs {
+  const uint8_t* W;
+  size_t rb;
+  const uint16_t* X;  // parts at X, X + xs, X + 2 xs (hi, mid, lo)
+  size_t xs;
+  float* Y;
+  int ldy, M, N, K;
+  float beta;
+};
+
+__device__ __forceinline__ uint32_t swz(int row, int chunk) { return (uint32_t)(row * 64 + ((chunk ^ ((row >> 2) & 3)) * 16)); }
+
+template <int BN>
+__global__ __launch_bounds__(256) void qgemm_q4k_x3ref(const QArgs p) {
+  constexpr int NB = BN / 16;
+  constexpr int BPART = BN * 64;
+  constexpr int XSTAGE = 3 * XPART;
+  constexpr int BOFF = XRING * XSTAGE;                 // the two B buffers follow the x ring
+  constexpr int RAWB = BN * 48, NRI = (RAWB + 1023) / 1024, RAWS = NRI * 1024;
+  constexpr int RAWOFF = BOFF + 2 * BPART;             // then the raw weight ring
+  constexpr int JUNK = RAWOFF + XRING * RAWS;          // then a KiB for loads past the raw image
+  extern __shared__ __attribute__((aligned(16))) uint16_t lds_h[];
+  uint8_t* lds = (uint8_t*)lds_h;
+  const uint32_t lds0 = lds_addr(lds);
+
+  const int ntn = (p.N + BN - 1) / BN;
+  const int tm = blockIdx.x / ntn, tn = blockIdx.x % ntn;
+  const int m0 = tm * QBM, n0 = tn * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  // x DMA: 3 parts x 8 loads of 16 rows per stage, 6 per wave
+  const uint16_t* xsrc[6];
+  uint32_t xoff[6];
+#pragma unroll
+  for (int u = 0; u < 6; ++u) {
+    const int t = wave + 4 * u, part = t >> 3, ch = t & 7;
+    const int row = ch * 16 + (lane >> 2), slot = lane & 3;
+    xsrc[u] = p.X + part * p.xs + (size_t)min(m0 + row, p.M - 1) * p.K + 8 * (slot ^ ((row >> 2) & 3));
+    xoff[u] = (uint32_t)(part * XPART + ch * 1024);
+  }
+  auto issue_x = [&](int kt) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < 6; ++u) dma16(xsrc[u] + kt * QBK, lds0 + (kt % XRING) * XSTAGE + xoff[u]);
+  };
+
+  // Raw weight bytes of a stage, per W row r: the super-block header and the two
+  // 16-byte qs chunks holding the sub-block ([r][3][16 bytes], RAWB bytes in a
+  // slot of RAWS).  They arrive by DMA like x, one stage ahead of x, so that
+  // stage kt's loads bring x(kt) and raw(kt+1).  A load writes 1 KiB at a
+  // wave-uniform LDS address: its lanes past RAWB land in the slot's padding,
+  // and whole loads past the image write a junk KiB, so that every wave issues
+  // the same number of loads.
+  constexpr int RAWI = (NRI + 3) / 4;  // raw loads per wave per stage
+  constexpr int GRPL = 6 + RAWI;       // loads per wave per stage
+  const int nk = p.K / QBK;
+  const uint8_t* rsrc[RAWI];
+  int rkind[RAWI];
+#pragma unroll
+  for (int u = 0; u < RAWI; ++u) {
+    const int f = (wave + 4 * u) * 1024 + lane * 16;
+    const int r = min(f / 48, BN - 1), c = (f % 48) >> 4;
+    rsrc[u] = p.W + (size_t)min(n0 + r, p.N - 1) * p.rb;
+    rkind[u] = c;
+  }
+  auto issue_raw = [&](int kt) __attribute__((always_inline)) {
+    kt = min(kt, nk - 1);
+    const int sb = kt >> 3, s = kt & 7;
+#pragma unroll
+    for (int u = 0; u < RAWI; ++u) {
+      const int ii = wave + 4 * u, c = rkind[u];
+      const uint8_t* g = rsrc[u] + (size_t)sb * 144 + (c == 0 ? 0 : 16 + 32 * (s >> 1) + 16 * (c - 1));
+      const uint32_t dst = ii < NRI ? (uint32_t)(RAWOFF + (kt % XRING) * RAWS + ii * 1024) : (uint32_t)JUNK;
+      dma16(g, lds0 + dst);
+    }
+  };
+
+  // decode: thread (r, h) turns elements [16h, 16h+16) of W row r into fp16
+  // (threads past 2*BN repeat row BN-1 and store to the junk KiB, so the code has
+  // no branch and the scheduler can interleave it with the MFMAs)
+  const int dr = min(tid >> 1, BN - 1), dh = tid & 1;
+  const bool dec = tid < 2 * BN;
+  auto decode = [&](int kt, uint32_t (&o)[8]) __attribute__((always_inline)) {
+    const int s = kt & 7;
+    const uint8_t* raw = lds + RAWOFF + (kt % XRING) * RAWS + dr * 48;
+    const u32x4 H = *(const u32x4*)raw;
+    const u32x4 Q = *(const u32x4*)(raw + 16 + 16 * dh);
+    int sc, mn;
+    kq_scale_min(s, H[1], H[2], H[3], sc, mn);
+    const float dsc = h2f(H[0] & 0xffffu) * (float)sc, dm = h2f(H[0] >> 16) * (float)mn;
+    const int sh = 4 * (s & 1);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t v = Q[w] >> sh;
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        // q_val (quant.h:83-84): both products exact, one rounding; then fp16 RNE
+        const float lo = fmaf(dsc, (float)((v >> (16 * b)) & 15u), -dm);
+        const float hi = fmaf(dsc, (float)((v >> (16 * b + 8)) & 15u), -dm);
+        o[2 * w + b] = (uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16);
+      }
+    }
+  };
+  auto store_b = [&](int buf, const uint32_t (&o)[8]) __attribute__((always_inline)) {
+    uint8_t* bt = dec ? lds + BOFF + buf * BPART : lds + JUNK;
+    const int r = dec ? dr : 0;
+    *(u32x4*)(bt + swz(r, 2 * dh)) = u32x4{o[0], o[1], o[2], o[3]};
+    *(u32x4*)(bt + swz(r, 2 * dh + 1)) = u32x4{o[4], o[5], o[6], o[7]};
+  };
+
+  float4v acc[2][NB];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[i][j] = float4v{0.f, 0.f, 0.f, 0.f};
+
+  // fragment offsets: lane l reads row (l%16) of a 16-row block, chunk l/16
+  const int fr = lane & 15, fc = lane >> 4;
+  const uint32_t fo = swz(fr, fc);
+
+  // Loads (every wave, in issue order): raw(0), then per stage q = 0, 1, 2, ...
+  // the group {raw(q+1), x(q)}; group q+3 is issued in stage q (past the end,
+  // the last stage is re-loaded into the free slots).  At the top of stage kt
+  // groups kt+1 and kt+2 are younger than group kt: 2*GRPL loads.
+  issue_raw(0);
+  for (int q = 0; q < XRING - 1; ++q) {
+    issue_raw(q + 1);
+    issue_x(min(q, nk - 1));
+  }
+  vm_wait<(XRING - 1) * GRPL>();  // raw(0)
+  __syncthreads();
+  {
+    uint32_t o[8];
+    decode(0, o);
+    store_b(0, o);
+  }
+  for (int kt = 0; kt < nk; ++kt) {
+    vm_wait<2 * GRPL>();  // group kt: x(kt), raw(kt+1)
+    __syncthreads();      // ... for every wave, and B(kt) is written; slot (kt-1) % XRING and B(kt-1) are free
+    issue_raw(kt + XRING);
+    issue_x(min(kt + XRING - 1, nk - 1));
+    uint32_t o[8];
+    decode(min(kt + 1, nk - 1), o);  // stage kt+1 (its raw bytes came with group kt)
+    const uint8_t* xs = lds + (kt % XRING) * XSTAGE;
+    const uint8_t* bs = lds + BOFF + (kt & 1) * BPART;
+    half8 bf[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) bf[j] = *(const half8*)(bs + j * 1024 + fo);
+    // parts lo, mid, hi (tier.cpp:940) into one fp32 accumulator
+#pragma unroll
+    for (int part = 2; part >= 0; --part) {
+      half8 af[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) af[i] = *(const half8*)(xs + part * XPART + (wave * 32 + i * 16) * 64 + fo);
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int i = 0; i < 2; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    store_b((kt + 1) & 1, o);
+  }
+  vm_wait<0>();  // drain the re-loads past the end
+
+  // epilogue: register i of lane l holds row 4*(l/16) + i, column l%16 of a 16x16 block
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const int col = n0 + j * 16 + (lane & 15);
+    if (col >= p.N) continue;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + wave * 32 + i * 16 + 4 * (lane >> 4) + r;
+        if (row >= p.M) continue;
+        float* c = p.Y + (size_t)row * p.ldy + col;
+        float v = acc[i][j][r];
+        if (p.beta != 0.f) v = fmaf(p.beta, *c, v);
+        *c = v;
+      }
+  }
+}
+
+template <int BN>
+int launch_q(const QArgs& a, hipStream_t s, const char* who) {
+  constexpr size_t lds = (size_t)XRING * 3 * XPART + 2 * (size_t)BN * 64 + (size_t)XRING * ((BN * 48 + 1023) / 1024) * 1024 + 1024;
+  static_assert(lds <= 160 * 1024, "LDS budget");
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)qgemm_q4k_x3ref<BN>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)lds);
+    if (e != hipSuccess) return hip_fail(e, who);
+    attr_set = true;
+  }
+  const unsigned grid = (unsigned)(((a.M + QBM - 1) / QBM) * ((a.N + BN - 1) / BN));
+  qgemm_q4k_x3ref<BN><<<grid, 256, lds, s>>>(a);
+  TM_LAUNCH_CHECK(who);
+  return TIERMM_OK;
+}
+
+}  // namespace
+
+// BN with the shortest critical path: rounds of workgroups over the CUs times
+// the work of one tile (proportional to BN); larger BN on ties.
+int qgemm_q4k_fused(const void* W, size_t rb, const uint16_t* xparts, size_t xs, float* Y, int ldy, int M, int N, int K,
+                    float beta, int cus, hipStream_t s, const char* who) {
+  QArgs a{(const uint8_t*)W, rb, xparts, xs, Y, ldy, M, N, K, beta};
+  const int cand[5] = {128, 112, 96, 80, 64};
+  int best = 128;
+  long best_t = -1;
+  for (int c : cand) {
+    const long tiles = (long)((M + QBM - 1) / QBM) * ((N + c - 1) / c);
+    const long t = (tiles + cus - 1) / cus * c;
+    if (best_t < 0 || t < best_t) {
+      best_t = t;
+      best = c;
+    }
+  }
+  switch (best) {
+    case 128: return launch_q<128>(a, s, who);
+    case 112: return launch_q<112>(a, s, who);
+    case 96: return launch_q<96>(a, s, who);
+    case 80: return launch_q<80>(a, s, who);
+    default: return launch_q<64>(a, s, who);
+  }
+}
+
+}  // namespace tiermm

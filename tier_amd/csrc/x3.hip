@@ -23,6 +23,9 @@ namespace tiermm {
 
 int check_qweight(const char* who, const void* W, int qtype, size_t rb, int cols);
 int dequant_f16_rows(const void* W, int qtype, size_t rb, int cols, size_t nrows, uint16_t* out, hipStream_t s);
+int qgemm_q4k_fused(const void* W, size_t rb, const uint16_t* xparts, size_t xs, float* Y, int ldy, int M, int N, int K,
+                    float beta, int cus, hipStream_t s, const char* who);
+int device_cus(int* cus);
 
 namespace {
 
@@ -583,9 +586,10 @@ int tiermm_x3_rows(const uint16_t* W, const float* x, float* y, int M, int K, in
 }
 
 size_t tiermm_qgemm_ws_bytes(int qtype, int M, int N, int K, int mode) {
-  (void)qtype;
   (void)mode;
-  return (size_t)N * K * sizeof(uint16_t) + (size_t)3 * M * K * sizeof(uint16_t);
+  const size_t parts = (size_t)3 * M * K * sizeof(uint16_t);  // x split in three fp16 planes
+  if (qtype == TIERMM_Q4_K) return parts;                      // W decoded inside the GEMM
+  return (size_t)N * K * sizeof(uint16_t) + parts;              // W16 staged in the workspace
 }
 
 int tiermm_qgemm(const void* W, int qtype, size_t rb, const float* X, float* Y, int M, int N, int K, int ldy,
@@ -603,9 +607,18 @@ int tiermm_qgemm(const void* W, int qtype, size_t rb, const float* X, float* Y, 
   st = get_workspace(ws, ws_bytes, tiermm_qgemm_ws_bytes(qtype, M, N, K, mode), &w, who);
   if (st) return st;
   hipStream_t s = (hipStream_t)stream;
+  const size_t mk = (size_t)M * K;
+  if (qtype == TIERMM_Q4_K) {
+    uint16_t* parts = (uint16_t*)w;
+    st = split3_launch(X, parts, mk, mk, TIERMM_HML, s);
+    if (st) return st;
+    int cus = 0;
+    st = device_cus(&cus);
+    if (st) return st;
+    return qgemm_q4k_fused(W, rb, parts, mk, Y, ldy, M, N, K, beta, cus, s, who);
+  }
   uint16_t* w16 = (uint16_t*)w;
   uint16_t* parts = w16 + (size_t)N * K;
-  const size_t mk = (size_t)M * K;
   st = dequant_f16_rows(W, qtype, rb, K, (size_t)N, w16, s);
   if (st) return st;
   st = split3_launch(X, parts, mk, mk, TIERMM_HML, s);
