@@ -98,4 +98,7 @@ def test_argument_checks_return_before_device_work():
 def test_workspace_sizes():
     assert tier_amd.x3_gemm_ws_bytes(5120, 4096, 5120) == 3 * 4096 * 5120 * 2
     assert tier_amd.x3_rows_ws_bytes(256, 5120, 14336) == 3 * 256 * 5120 * 2
-    assert tier_amd.qgemm_ws_bytes(tier_amd.Q4_K, 512, 5120, 5120) >= 5120 * 5120 * 2
+    # q4_K decodes W inside the GEMM: only the three fp16 planes of x
+    assert tier_amd.qgemm_ws_bytes(tier_amd.Q4_K, 512, 5120, 5120) == 3 * 512 * 5120 * 2
+    # other types stage fp16 W in the workspace as well
+    assert tier_amd.qgemm_ws_bytes(tier_amd.Q6_K, 512, 5120, 5120) == 5120 * 5120 * 2 + 3 * 512 * 5120 * 2
