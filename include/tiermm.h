@@ -117,15 +117,23 @@ int tiermm_qgemv(const void* W, int qtype, size_t rb, const float* x, float* y, 
 int tiermm_split3_f16(const float* x, uint16_t* parts, size_t n, size_t part_stride, int order,
                       tiermm_stream_t stream);
 
+/* ------------------------------------------------------- dense-row GEMV */
+/* gemv<T> (tier.cpp:2261-2268, launched at 2345, 2363, 2616 for the fp16/bf16
+ * frozen matrices and the LM head): y[r] = sum_k float(W[r][k]) * x[k], fp32
+ * accumulation.  wtype in {TIERMM_F32, TIERMM_F16 (tier_fp16 bits),
+ * TIERMM_BF16}; W: N rows of K elements, 16-byte aligned; K <= 16384. */
+int tiermm_gemv(const void* W, int wtype, const float* x, float* y, int N, int K, tiermm_stream_t stream);
+
 /* ------------------------------------------------------------ x3-ref GEMM */
 /* fp3gemm (tier.cpp:922-943) in its BLAS column-major contract:
  * C(m x n) = op(A)(m x k) * B(k x n) + beta * C, A fp16 (the frozen weight,
  * exact), B fp32 split into three fp16 parts; the three products run on fp16
  * MFMA with fp32 accumulation.  With opA = TIERMM_OP_T and lda = k this is the
  * forward linear out[n][m] = x[n][k] * W[m][k]^T (low3_linear, tier.cpp:1212);
- * ldc >= m.  opA = TIERMM_OP_N (the dX layout, tier.cpp:1226) returns
- * TIERMM_UNSUPPORTED in this version.  Accuracy: rel. Frobenius error <= 2^-20
- * against fp64(A * B). */
+ * with opA = TIERMM_OP_N and lda = m it is the dX product of linear_dx /
+ * linear_dx_acc (tier.cpp:1226, 1234): A is m x k column-major (W[k][m] in
+ * memory) and is transposed into the workspace first.  ldc >= m.  Accuracy:
+ * rel. Frobenius error <= 2^-20 against fp64(A * B). */
 int tiermm_x3_gemm(int opA, int m, int n, int k, const uint16_t* A, int lda, const float* B,
                    float beta, float* C, int ldc, void* ws, size_t ws_bytes,
                    tiermm_stream_t stream);
@@ -158,12 +166,35 @@ int tiermm_x3s_gemm(const uint16_t* Xhi, const uint16_t* Xlo, const int32_t* xex
  * mode TIERMM_MODE_X3REF: W is dequantized to fp16 (bit-exact with dq_k<tier_fp16>,
  * tier.cpp:515) inside the kernel and multiplied with x split in three fp16
  * parts (fp3gemm semantics, tier.cpp:922): rel. Frobenius error <= 2^-20
- * against fp64(fp16deq(W) * X).  TIERMM_MODE_F32 is reserved (returns
- * TIERMM_UNSUPPORTED).  qtype in {Q8_0, Q5_0, Q4_K, Q5_K, Q6_K}. */
+ * against fp64(fp16deq(W) * X).  mode TIERMM_MODE_F32: the chat prefill
+ * semantics (fp32 dequant, then an fp32 GEMM, tier.cpp:2358-2359): rel.
+ * Frobenius error <= 2^-20 against fp64(deq(W) * X).  qtype in {Q8_0, Q5_0,
+ * Q4_K, Q5_K, Q6_K}. */
 int tiermm_qgemm(const void* W, int qtype, size_t rb, const float* X, float* Y, int M, int N,
                  int K, int ldy, int mode, float beta, void* ws, size_t ws_bytes,
                  tiermm_stream_t stream);
 size_t tiermm_qgemm_ws_bytes(int qtype, int M, int N, int K, int mode);
+
+/* ------------------------------------------------- grouped (MoE) GEMM */
+/* No reference function (the reference refuses MoE models, arch.py:158-159):
+ * the experts' matmuls of a routed batch.  Rows [expert_offsets[e],
+ * expert_offsets[e+1]) of X_sorted[.][K] are the tokens routed to expert e
+ * (sorted by expert); Y_sorted[r][N] = X_sorted[r] * dequant(W_e[e])^T with
+ * tiermm_qgemm's semantics per expert (`mode`).  W_e, qtype_e, rb_e and
+ * expert_offsets (n_experts + 1 entries) are HOST arrays; W_e[e] are device
+ * pointers.  Expert down-projections whose K is not a multiple of 256 use a
+ * 32-element type (q5_0, as llama.cpp falls back). */
+int tiermm_qgemm_grouped(const void* const* W_e, const int* qtype_e, const size_t* rb_e,
+                         const float* X_sorted, const int* expert_offsets, int n_experts,
+                         float* Y_sorted, int N, int K, int mode, void* ws, size_t ws_bytes,
+                         tiermm_stream_t stream);
+size_t tiermm_qgemm_grouped_ws_bytes(const int* qtype_e, const int* expert_offsets, int n_experts,
+                                     int N, int K, int mode);
+/* Per-token weighted combine of the routed outputs: out[t][n] =
+ * sum_{j<topk} pair_weight[p] * Y_sorted[p][n], p = token_pairs[t*topk + j],
+ * summed in j order.  token_pairs, pair_weight: device arrays. */
+int tiermm_moe_combine(const float* Y_sorted, const int* token_pairs, const float* pair_weight,
+                       float* out, int T, int topk, int N, tiermm_stream_t stream);
 
 /* ------------------------------------------------------ host quantizer */
 /* q_row (quant.h:201-204) over `rows` rows of `cols` host floats, writing

@@ -83,10 +83,22 @@ def test_argument_checks_return_before_device_work():
     assert L.tiermm_qgemv(16, tier_amd.Q4_K, 792, 16, 16, 1, 1408, None) == tier_amd.UNSUPPORTED
     # K beyond the staged-x limit
     assert L.tiermm_qgemv(16, tier_amd.Q8_0, 34 * 1024, 16, 16, 1, 32768, None) == tier_amd.UNSUPPORTED
-    # dX layout not built yet; reserved fp32 mode
-    assert L.tiermm_x3_gemm(tier_amd.OP_N, 64, 64, 64, 16, 64, 16, 0.0, 16, 64, None, 0, None) == tier_amd.UNSUPPORTED
-    assert L.tiermm_qgemm(16, tier_amd.Q4_K, 144, 16, 16, 2, 4, 256, 4, tier_amd.MODE_F32, 0.0, None, 0,
-                          None) == tier_amd.UNSUPPORTED
+    # dX layout: lda must cover m (A is m x k column-major); unknown op / mode
+    assert L.tiermm_x3_gemm(tier_amd.OP_N, 64, 64, 64, 16, 32, 16, 0.0, 16, 64, None, 0, None) == tier_amd.EINVAL
+    assert L.tiermm_x3_gemm(7, 64, 64, 64, 16, 64, 16, 0.0, 16, 64, None, 0, None) == tier_amd.EINVAL
+    assert L.tiermm_qgemm(16, tier_amd.Q4_K, 144, 16, 16, 2, 4, 256, 4, 7, 0.0, None, 0, None) == tier_amd.EINVAL
+    # dense GEMV: unknown weight type, misaligned rows
+    assert L.tiermm_gemv(16, tier_amd.Q4_K, 16, 16, 4, 64, None) == tier_amd.UNSUPPORTED
+    assert L.tiermm_gemv(18, tier_amd.F16, 16, 16, 4, 64, None) == tier_amd.EINVAL
+    # grouped GEMM: offsets must start at 0 and not decrease
+    import ctypes
+    I2 = ctypes.c_int * 2
+    assert L.tiermm_qgemm_grouped((ctypes.c_void_p * 1)(16), (ctypes.c_int * 1)(tier_amd.Q4_K),
+                                  (ctypes.c_size_t * 1)(144), 16, I2(1, 2), 1, 16, 4, 256, 0, None, 0,
+                                  None) == tier_amd.EINVAL
+    assert L.tiermm_qgemm_grouped((ctypes.c_void_p * 1)(16), (ctypes.c_int * 1)(tier_amd.Q4_K),
+                                  (ctypes.c_size_t * 1)(144), 16, I2(0, -1), 1, 16, 4, 256, 0, None, 0,
+                                  None) == tier_amd.EINVAL
     # K not a multiple of the 32-element K step
     assert L.tiermm_x3s_gemm(16, 16, 16, 16, 16, 16, 16, 4, 4, 48, 4, None) == tier_amd.UNSUPPORTED
     assert L.tiermm_split3_f16(16, 16, 10, 5, 0, None) == tier_amd.EINVAL
@@ -96,7 +108,8 @@ def test_argument_checks_return_before_device_work():
 
 
 def test_workspace_sizes():
-    assert tier_amd.x3_gemm_ws_bytes(5120, 4096, 5120) == 3 * 4096 * 5120 * 2
+    # three planes of B, plus the transposed weight for TIERMM_OP_N
+    assert tier_amd.x3_gemm_ws_bytes(5120, 4096, 5120) == 3 * 4096 * 5120 * 2 + 5120 * 5120 * 2
     assert tier_amd.x3_rows_ws_bytes(256, 5120, 14336) == 3 * 256 * 5120 * 2
     # q4_K decodes W inside the GEMM: only the three fp16 planes of x
     assert tier_amd.qgemm_ws_bytes(tier_amd.Q4_K, 512, 5120, 5120) == 3 * 512 * 5120 * 2

@@ -99,3 +99,25 @@ def test_gemv_on_a_stream(gpu):
     y = Y.download(np.float32, N)
     s.destroy()
     assert oracle.rel_fro(y, oracle.gemv_f64(blocks, t, x, N, K)) <= TOL
+
+
+@pytest.mark.parametrize("wtype", [tier_amd.F32, tier_amd.F16, tier_amd.BF16])
+@pytest.mark.parametrize("N,K", [(1000, 4096), (33, 1001), (5, 16)])
+def test_gemv_dense_rows(gpu, wtype, N, K):
+    """gemv<T> (tier.cpp:2261-2268) on fp32 / fp16 / bf16 rows; K = 1001 takes the element-wise path."""
+    rng = np.random.default_rng(N + K + wtype)
+    w = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
+    if wtype == tier_amd.F32:
+        bits, wf = w, w
+    elif wtype == tier_amd.F16:
+        bits = oracle.f2h(w).reshape(N, K)
+        wf = oracle.h2f(bits).reshape(N, K)
+    else:
+        bits = oracle.f2bf(w).reshape(N, K)
+        wf = (bits.astype(np.uint32) << 16).view(np.float32)
+    x = rng.standard_normal(K).astype(np.float32)
+    W, X, Y = hip.to_device(bits), hip.to_device(x), hip.DeviceBuffer(N * 4)
+    tier_amd.gemv(W.ptr, wtype, X.ptr, Y.ptr, N, K)
+    hip.synchronize()
+    y = Y.download(np.float32, N)
+    assert oracle.rel_fro(y, wf.astype(np.float64) @ x.astype(np.float64)) <= TOL

@@ -1,0 +1,84 @@
+"""GPU parity of the grouped (MoE) quantized GEMM and the weighted combine.
+
+There is no reference function (the reference refuses MoE models,
+arch.py:158-159): the bar is the per-expert decomposition into dense products
+(fp64 of the oracle's fp16 dequantization times x) and an fp64 weighted sum,
+relative Frobenius error <= 2^-20.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+import tier_amd
+from helpers import activations
+from tier_amd import hip
+
+pytestmark = pytest.mark.gpu
+BAR = 2.0 ** -20
+
+
+def _route(rng, T, E, topk):
+    """Router logits ~N(0,1) -> softmax -> top-k; pairs sorted by expert (stable)."""
+    logits = rng.standard_normal((T, E))
+    p = np.exp(logits - logits.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    top = np.argsort(-p, axis=1, kind="stable")[:, :topk]
+    pair_tok = np.repeat(np.arange(T), topk)
+    pair_exp = top.ravel()
+    pair_w = p[np.arange(T)[:, None], top].ravel().astype(np.float32)
+    order = np.argsort(pair_exp, kind="stable")
+    offsets = np.zeros(E + 1, np.int32)
+    np.add.at(offsets, pair_exp + 1, 1)
+    offsets = np.cumsum(offsets).astype(np.int32)
+    inv = np.empty_like(order)
+    inv[order] = np.arange(order.size)
+    token_pairs = inv.reshape(T, topk).astype(np.int32)  # sorted-pair index of token t's j-th expert
+    return pair_tok[order], pair_exp[order], pair_w[order], offsets, token_pairs
+
+
+@pytest.mark.parametrize("t,N,K", [(tier_amd.Q4_K, 256, 512), (tier_amd.Q5_0, 192, 1408)])
+def test_grouped_gemm_and_combine(gpu, t, N, K):
+    rng = np.random.default_rng(N + K)
+    T, E, topk = 96, 8, 2
+    pair_tok, pair_exp, pair_w, offsets, token_pairs = _route(rng, T, E, topk)
+    be, _ = oracle.block(t)
+    blocks = [oracle.random_blocks(rng, t, N * (K // be)).reshape(N, -1) for _ in range(E)]
+    x = activations(T, K, seed=5)
+    xs = np.ascontiguousarray(x[pair_tok])
+    # an expert with no tokens: move expert 5's pairs to expert 6
+    sel = pair_exp == 5
+    pair_exp = np.where(sel, 6, pair_exp)
+    order = np.argsort(pair_exp, kind="stable")
+    pair_tok, pair_exp, pair_w, xs = pair_tok[order], pair_exp[order], pair_w[order], xs[order]
+    counts = np.bincount(pair_exp, minlength=E)
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    inv = np.empty_like(order)
+    inv[order] = np.arange(order.size)
+    token_pairs = inv[token_pairs.ravel()].reshape(T, topk).astype(np.int32)
+    assert counts[5] == 0
+
+    dW = [hip.to_device(b) for b in blocks]
+    rb = tier_amd.q_row_bytes(t, K)
+    X = hip.to_device(xs)
+    Y = hip.DeviceBuffer(xs.shape[0] * N * 4)
+    tier_amd.qgemm_grouped([w.ptr for w in dW], [t] * E, [rb] * E, X.ptr, offsets.tolist(), Y.ptr, N, K)
+    TP, PW, OUT = hip.to_device(token_pairs), hip.to_device(pair_w), hip.DeviceBuffer(T * N * 4)
+    tier_amd.moe_combine(Y.ptr, TP.ptr, PW.ptr, OUT.ptr, T, topk, N)
+    hip.synchronize()
+    ys = Y.download(np.float32, xs.shape[0] * N).reshape(-1, N)
+    out = OUT.download(np.float32, T * N).reshape(T, N)
+
+    w16 = [oracle.h2f(oracle.dequant(b, t, K, oracle.OUT_F16)).reshape(N, K).astype(np.float64) for b in blocks]
+    ref_s = np.empty((xs.shape[0], N))
+    for e in range(E):
+        a, b = offsets[e], offsets[e + 1]
+        ref_s[a:b] = xs[a:b].astype(np.float64) @ w16[e].T
+    assert oracle.rel_fro(ys, ref_s) <= BAR
+    ref = np.zeros((T, N))
+    for tt in range(T):
+        for j in range(topk):
+            p = token_pairs[tt, j]
+            ref[tt] += float(pair_w[p]) * ref_s[p]
+    assert oracle.rel_fro(out, ref) <= BAR

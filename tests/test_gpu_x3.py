@@ -183,3 +183,34 @@ def test_qgemm_config3_m512_sampled(gpu):
     w16 = oracle.h2f(oracle.dequant(blocks, t, K, oracle.OUT_F16)).reshape(N, K)
     ref = x[rows].astype(np.float64) @ w16.astype(np.float64).T
     assert oracle.rel_fro(got[rows], ref) <= BAR
+
+
+@pytest.mark.parametrize("beta", [0.0, 1.0])
+def test_fp3gemm_dx_contract(gpu, beta):
+    """fp3gemm(OP_N, m=K, n=M, k=N, W16, lda=K, dY, beta, dX, ldc=K): dX[M][K] = dY W16 (+ beta*dX),
+    the linear_dx / linear_dx_acc products (tier.cpp:1226, 1234)."""
+    rng = np.random.default_rng(17)
+    M, N, K = 96, 320, 200
+    w16 = oracle.f2h((rng.standard_normal((N, K)) * 0.02).astype(np.float32)).reshape(N, K)
+    dy = activations(M, N, seed=18)
+    dx0 = rng.standard_normal((M, K)).astype(np.float32)
+    A, B, C = hip.to_device(w16), hip.to_device(dy), hip.to_device(dx0)
+    tier_amd.fp3gemm(tier_amd.OP_N, K, M, N, A.ptr, K, B.ptr, beta, C.ptr, K)
+    hip.synchronize()
+    got = C.download(np.float32, M * K).reshape(M, K)
+    ref = dy.astype(np.float64) @ oracle.h2f(w16).reshape(N, K).astype(np.float64) + beta * dx0.astype(np.float64)
+    assert oracle.rel_fro(got, ref) <= BAR
+
+
+@pytest.mark.parametrize("name,t,M,N,K", [("q4_K", tier_amd.Q4_K, 70, 300, 1024), ("q6_K", tier_amd.Q6_K, 33, 64, 512),
+                                          ("q8_0", tier_amd.Q8_0, 300, 640, 1024)])
+def test_qgemm_f32_mode(gpu, name, t, M, N, K):
+    """TIERMM_MODE_F32 (chat prefill, tier.cpp:2358-2359): fp32 dequant times x, against fp64."""
+    blocks = quantized_weight(t, N, K, seed=40 + t)
+    x = activations(M, K, seed=41)
+    W, X, Y = hip.to_device(blocks), hip.to_device(x), hip.DeviceBuffer(M * N * 4)
+    tier_amd.qgemm(W.ptr, t, tier_amd.q_row_bytes(t, K), X.ptr, Y.ptr, M, N, K, mode=tier_amd.MODE_F32)
+    hip.synchronize()
+    got = Y.download(np.float32, M * N).reshape(M, N)
+    wf = oracle.dequant(blocks, t, K, oracle.OUT_F32).reshape(N, K)
+    assert oracle.rel_fro(got, x.astype(np.float64) @ wf.astype(np.float64).T) <= BAR

@@ -46,7 +46,8 @@ EXPORTS = (
     "tiermm_init", "tiermm_shutdown", "tiermm_last_error", "tiermm_version", "tiermm_q_info",
     "tiermm_q_row_bytes", "tiermm_dequant", "tiermm_qgemv", "tiermm_split3_f16", "tiermm_x3_gemm",
     "tiermm_x3_gemm_ws_bytes", "tiermm_x3_rows", "tiermm_x3_rows_ws_bytes", "tiermm_x3s_split",
-    "tiermm_x3s_gemm", "tiermm_qgemm", "tiermm_qgemm_ws_bytes", "tiermm_quantize",
+    "tiermm_x3s_gemm", "tiermm_qgemm", "tiermm_qgemm_ws_bytes", "tiermm_quantize", "tiermm_gemv",
+    "tiermm_qgemm_grouped", "tiermm_qgemm_grouped_ws_bytes", "tiermm_moe_combine",
 )
 
 
@@ -92,6 +93,12 @@ _sig("tiermm_x3s_gemm", [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]
 _sig("tiermm_qgemm", [_vp, _i, _sz, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp, _sz, _vp])
 _sig("tiermm_qgemm_ws_bytes", [_i, _i, _i, _i, _i], _sz)
 _sig("tiermm_quantize", [_i, _vp, _vp, _sz, _i, _i])
+_sig("tiermm_gemv", [_vp, _i, _vp, _vp, _i, _i, _vp])
+_pi = ctypes.POINTER(_i)
+_sig("tiermm_qgemm_grouped", [ctypes.POINTER(_vp), _pi, ctypes.POINTER(_sz), _vp, _pi, _i, _vp, _i, _i, _i, _vp,
+                              _sz, _vp])
+_sig("tiermm_qgemm_grouped_ws_bytes", [_pi, _pi, _i, _i, _i, _i], _sz)
+_sig("tiermm_moe_combine", [_vp, _vp, _vp, _vp, _i, _i, _i, _vp])
 
 
 def lib():
@@ -215,6 +222,35 @@ def qgemm(W: int, qtype: int, rb: int, X: int, Y: int, M: int, N: int, K: int, l
 
 def qgemm_ws_bytes(qtype: int, M: int, N: int, K: int, mode: int = MODE_X3REF) -> int:
     return _L.tiermm_qgemm_ws_bytes(qtype, M, N, K, mode)
+
+
+def gemv(W: int, wtype: int, x: int, y: int, N: int, K: int, stream=None) -> None:
+    """gemv<T> (tier.cpp:2261-2268): y = W x for fp32 / fp16 / bf16 rows (wtype F32, F16, BF16)."""
+    _check(_L.tiermm_gemv(W, wtype, x, y, N, K, _s(stream)))
+
+
+def _grouped_tables(W_e, qtype_e, rb_e, offsets):
+    n = len(W_e)
+    if not (len(qtype_e) == len(rb_e) == n and len(offsets) == n + 1):
+        raise ValueError("expert tables must have n_experts entries and offsets n_experts + 1")
+    return (n, (_vp * n)(*W_e), (_i * n)(*qtype_e), (_sz * n)(*rb_e), (_i * (n + 1))(*offsets))
+
+
+def qgemm_grouped_ws_bytes(qtype_e, offsets, N: int, K: int, mode: int = MODE_X3REF) -> int:
+    n = len(qtype_e)
+    return _L.tiermm_qgemm_grouped_ws_bytes((_i * n)(*qtype_e), (_i * (n + 1))(*offsets), n, N, K, mode)
+
+
+def qgemm_grouped(W_e, qtype_e, rb_e, X_sorted: int, offsets, Y_sorted: int, N: int, K: int,
+                  mode: int = MODE_X3REF, ws: int | None = None, ws_bytes: int = 0, stream=None) -> None:
+    """Experts' quantized matmuls of a routed batch (host tables; device W_e, X, Y)."""
+    n, w, q, r, o = _grouped_tables(W_e, qtype_e, rb_e, offsets)
+    _check(_L.tiermm_qgemm_grouped(w, q, r, X_sorted, o, n, Y_sorted, N, K, mode, ws, ws_bytes, _s(stream)))
+
+
+def moe_combine(Y_sorted: int, token_pairs: int, pair_weight: int, out: int, T: int, topk: int, N: int,
+                stream=None) -> None:
+    _check(_L.tiermm_moe_combine(Y_sorted, token_pairs, pair_weight, out, T, topk, N, _s(stream)))
 
 
 def qlinear(W: int, qtype: int, rb: int, x: int, y: int, M: int, N: int, K: int, ws: int | None = None,

@@ -17,6 +17,8 @@
 // stage; the next stage's global loads are issued before the MFMAs of the
 // current one).  LDS rows are 64 data bytes + 16 pad bytes so the 16-byte
 // fragment reads of 8 consecutive rows hit distinct banks.
+#include <algorithm>
+
 #include "tm_device.h"
 
 namespace tiermm {
@@ -88,6 +90,40 @@ __global__ __launch_bounds__(256) void x3s_split_kernel(const float* __restrict_
     lo[base + k] = f2h(s - h2f(h));
   }
   if (threadIdx.x == 0) exps[blockIdx.x] = e;
+}
+
+// fp16 transpose: dst[c][r] = src[r][c] for r < rows, c < cols (src row stride ld,
+// dst row stride rows), through a 64x64 LDS tile (odd column stride: no bank conflicts).
+__global__ __launch_bounds__(256) void transpose16_kernel(const uint16_t* __restrict__ src, int ld,
+                                                          uint16_t* __restrict__ dst, int rows, int cols) {
+  __shared__ uint16_t t[64][65];
+  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int i = ty; i < 64; i += 4) {
+    const int r = r0 + i, c = c0 + tx;
+    if (r < rows && c < cols) t[i][tx] = src[(size_t)r * ld + c];
+  }
+  __syncthreads();
+  for (int i = ty; i < 64; i += 4) {
+    const int c = c0 + i, r = r0 + tx;
+    if (r < rows && c < cols) dst[(size_t)c * rows + r] = t[tx][i];
+  }
+}
+
+// Weighted combine of routed expert outputs: out[t][n] = sum_j w[p_j] * Y[p_j][n],
+// p_j = token_pairs[t*topk + j], summed in j order (deterministic).
+__global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ Y, const int* __restrict__ tp,
+                                                          const float* __restrict__ pw, float* __restrict__ out,
+                                                          int topk, int N) {
+  const int t = blockIdx.x;
+  for (int n = threadIdx.x; n < N; n += 256) {
+    float acc = 0.f;
+    for (int j = 0; j < topk; ++j) {
+      const int p = tp[(size_t)t * topk + j];
+      acc = fmaf(pw[p], Y[(size_t)p * N + n], acc);
+    }
+    out[(size_t)t * N + n] = acc;
+  }
 }
 
 // ------------------------------------------------------------- GEMM core
@@ -438,6 +474,9 @@ int launch_x3(const X3Args& a, hipStream_t s, const char* who) {
   return TIERMM_OK;
 }
 
+// Tiles of the 256x320 kernel: it pays off once they occupy most of the CUs.
+long big_tiles(int M, int N) { return (long)((M + XB_M - 1) / XB_M) * ((N + XB_N - 1) / XB_N); }
+
 int check_nt(const char* who, int M, int N, int K) {
   if (M < 0 || N < 0 || K < 0) return set_error(TIERMM_EINVAL, "%s: negative size", who);
   if (K % BK) return set_error(TIERMM_UNSUPPORTED, "%s: K=%d is not a multiple of %d", who, K, BK);
@@ -467,6 +506,7 @@ int x3ref_nt(const uint16_t* xparts, size_t stride, const uint16_t* W, int ldw, 
   a.aexp = nullptr;
   a.bexp = nullptr;
   a.beta = beta;
+  if (big_tiles(M, N) >= 192) return launch_x3_big<X3_REF>(a, s, who);
   return launch_x3<128, 128, X3_REF>(a, s, who);
 }
 
@@ -529,26 +569,25 @@ int tiermm_x3s_gemm(const uint16_t* Xhi, const uint16_t* Xlo, const int32_t* xex
   a.bexp = wexp;
   a.beta = 0.f;
   // the 256x320 tile needs enough tiles to occupy the CUs; smaller problems use 128x128
-  const long big_tiles = (long)((M + XB_M - 1) / XB_M) * ((N + XB_N - 1) / XB_N);
-  if (big_tiles >= 192) return launch_x3_big<X3_2X2>(a, (hipStream_t)stream, "tiermm_x3s_gemm: launch");
+  if (big_tiles(M, N) >= 192) return launch_x3_big<X3_2X2>(a, (hipStream_t)stream, "tiermm_x3s_gemm: launch");
   return launch_x3<128, 128, X3_2X2>(a, (hipStream_t)stream, "tiermm_x3s_gemm: launch");
 }
 
 size_t tiermm_x3_gemm_ws_bytes(int m, int n, int k) {
-  (void)m;
-  return (size_t)3 * (size_t)n * (size_t)k * sizeof(uint16_t);
+  // three fp16 planes of B, and for TIERMM_OP_N the transposed weight
+  return (size_t)3 * (size_t)n * (size_t)k * sizeof(uint16_t) + (size_t)m * (size_t)k * sizeof(uint16_t);
 }
 
 int tiermm_x3_gemm(int opA, int m, int n, int k, const uint16_t* A, int lda, const float* B, float beta, float* C,
                    int ldc, void* ws, size_t ws_bytes, tiermm_stream_t stream) {
   const char* who = "tiermm_x3_gemm";
   if (opA != TIERMM_OP_T && opA != TIERMM_OP_N) return set_error(TIERMM_EINVAL, "%s: opA %d", who, opA);
-  if (opA == TIERMM_OP_N) return set_error(TIERMM_UNSUPPORTED, "%s: the OP_N (dX) layout is not built yet", who);
   int st = check_nt(who, n, m, k);
   if (st) return st;
-  if (lda < k || ldc < m) return set_error(TIERMM_EINVAL, "%s: lda < k or ldc < m", who);
+  if ((opA == TIERMM_OP_T && lda < k) || (opA == TIERMM_OP_N && lda < m) || ldc < m)
+    return set_error(TIERMM_EINVAL, "%s: lda or ldc too small", who);
   if (m == 0 || n == 0) return TIERMM_OK;
-  if (!aligned16(A) || (lda % 8) || !B || !C)
+  if (!A || !B || !C || (opA == TIERMM_OP_T && (!aligned16(A) || (lda % 8))))
     return set_error(TIERMM_EINVAL, "%s: A must be 16-byte aligned with lda a multiple of 8", who);
   void* w = nullptr;
   const size_t nk = (size_t)n * k;
@@ -558,8 +597,20 @@ int tiermm_x3_gemm(int opA, int m, int n, int k, const uint16_t* A, int lda, con
   uint16_t* parts = (uint16_t*)w;
   st = split3_launch(B, parts, nk, nk, TIERMM_HML, s);
   if (st) return st;
+  const uint16_t* At = A;
+  int ldt = lda;
+  if (opA == TIERMM_OP_N) {
+    // A is m x k column-major ([k][lda] in memory, the dX layout of tier.cpp:1226):
+    // transpose it to [m][k] so the product runs in the NT form below
+    uint16_t* t = parts + 3 * nk;
+    dim3 grid((unsigned)((m + 63) / 64), (unsigned)((k + 63) / 64));
+    transpose16_kernel<<<grid, 256, 0, s>>>(A, lda, t, k, m);
+    TM_LAUNCH_CHECK("tiermm_x3_gemm: transpose");
+    At = t;
+    ldt = k;
+  }
   // column-major C(m x n) with ldc == row-major out[n][ldc] = x[n][k] * W[m][k]^T
-  return x3ref_nt(parts, nk, A, lda, C, ldc, n, m, k, beta, s, who);
+  return x3ref_nt(parts, nk, At, ldt, C, ldc, n, m, k, beta, s, who);
 }
 
 size_t tiermm_x3_rows_ws_bytes(int M, int K, int N) {
@@ -585,11 +636,15 @@ int tiermm_x3_rows(const uint16_t* W, const float* x, float* y, int M, int K, in
   return x3ref_nt((const uint16_t*)w, mk, W, K, y, ldo, M, N, K, 0.f, s, who);
 }
 
+static size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
+
 size_t tiermm_qgemm_ws_bytes(int qtype, int M, int N, int K, int mode) {
-  (void)mode;
+  if (mode == TIERMM_MODE_F32)  // fp32 W, its two-part split, and x's
+    return al256((size_t)N * K * 4) + 2 * al256((size_t)N * K * 2) + al256((size_t)N * 4) +
+           2 * al256((size_t)M * K * 2) + al256((size_t)M * 4);
   const size_t parts = (size_t)3 * M * K * sizeof(uint16_t);  // x split in three fp16 planes
-  if (qtype == TIERMM_Q4_K) return parts;                      // W decoded inside the GEMM
-  return (size_t)N * K * sizeof(uint16_t) + parts;              // W16 staged in the workspace
+  if (qtype == TIERMM_Q4_K && big_tiles(M, N) < 192) return parts;  // W decoded inside the GEMM
+  return (size_t)N * K * sizeof(uint16_t) + parts;                   // W16 staged in the workspace
 }
 
 int tiermm_qgemm(const void* W, int qtype, size_t rb, const float* X, float* Y, int M, int N, int K, int ldy,
@@ -597,7 +652,7 @@ int tiermm_qgemm(const void* W, int qtype, size_t rb, const float* X, float* Y, 
   const char* who = "tiermm_qgemm";
   int st = check_qweight(who, W, qtype, rb, K);
   if (st) return st;
-  if (mode != TIERMM_MODE_X3REF) return set_error(TIERMM_UNSUPPORTED, "%s: mode %d is not built yet", who, mode);
+  if (mode != TIERMM_MODE_X3REF && mode != TIERMM_MODE_F32) return set_error(TIERMM_EINVAL, "%s: mode %d", who, mode);
   st = check_nt(who, M, N, K);
   if (st) return st;
   if (ldy < N) return set_error(TIERMM_EINVAL, "%s: ldy < N", who);
@@ -608,7 +663,31 @@ int tiermm_qgemm(const void* W, int qtype, size_t rb, const float* X, float* Y, 
   if (st) return st;
   hipStream_t s = (hipStream_t)stream;
   const size_t mk = (size_t)M * K;
-  if (qtype == TIERMM_Q4_K) {
+  if (mode == TIERMM_MODE_F32) {
+    // chat prefill semantics (tier.cpp:2358-2359): fp32 dequant, fp32-accurate
+    // product -- here the two-part split GEMM (relative error ~2^-21 of fp64)
+    uint8_t* b = (uint8_t*)w;
+    float* wf = (float*)b;                    b += al256((size_t)N * K * 4);
+    uint16_t* whi = (uint16_t*)b;             b += al256((size_t)N * K * 2);
+    uint16_t* wlo = (uint16_t*)b;             b += al256((size_t)N * K * 2);
+    int32_t* wexp = (int32_t*)b;              b += al256((size_t)N * 4);
+    uint16_t* xhi = (uint16_t*)b;             b += al256(mk * 2);
+    uint16_t* xlo = (uint16_t*)b;             b += al256(mk * 2);
+    int32_t* xexp = (int32_t*)b;
+    st = tiermm_dequant(W, qtype, rb, K, 0, (size_t)N, wf, TIERMM_OUT_F32, stream);
+    if (st) return st;
+    x3s_split_kernel<<<N, 256, 0, s>>>(wf, whi, wlo, wexp, K);
+    TM_LAUNCH_CHECK("tiermm_qgemm: split W");
+    x3s_split_kernel<<<M, 256, 0, s>>>(X, xhi, xlo, xexp, K);
+    TM_LAUNCH_CHECK("tiermm_qgemm: split x");
+    X3Args a{};
+    a.A[0] = xhi; a.A[1] = xlo; a.B[0] = whi; a.B[1] = wlo;
+    a.lda = K; a.ldb = K; a.C = Y; a.ldc = ldy; a.M = M; a.N = N; a.K = K;
+    a.aexp = xexp; a.bexp = wexp; a.beta = beta;
+    if (big_tiles(M, N) >= 192) return launch_x3_big<X3_2X2>(a, s, who);
+    return launch_x3<128, 128, X3_2X2>(a, s, who);
+  }
+  if (qtype == TIERMM_Q4_K && big_tiles(M, N) < 192) {  // small M: decode W inside the GEMM
     uint16_t* parts = (uint16_t*)w;
     st = split3_launch(X, parts, mk, mk, TIERMM_HML, s);
     if (st) return st;
@@ -624,6 +703,51 @@ int tiermm_qgemm(const void* W, int qtype, size_t rb, const float* X, float* Y, 
   st = split3_launch(X, parts, mk, mk, TIERMM_HML, s);
   if (st) return st;
   return x3ref_nt(parts, mk, w16, K, Y, ldy, M, N, K, beta, s, who);
+}
+
+size_t tiermm_qgemm_grouped_ws_bytes(const int* qtype_e, const int* expert_offsets, int n_experts, int N, int K,
+                                     int mode) {
+  size_t need = 0;
+  for (int e = 0; e < n_experts; ++e) {
+    const int Me = expert_offsets[e + 1] - expert_offsets[e];
+    if (Me > 0) need = std::max(need, tiermm_qgemm_ws_bytes(qtype_e[e], Me, N, K, mode));
+  }
+  return need;
+}
+
+int tiermm_qgemm_grouped(const void* const* W_e, const int* qtype_e, const size_t* rb_e, const float* X_sorted,
+                         const int* expert_offsets, int n_experts, float* Y_sorted, int N, int K, int mode, void* ws,
+                         size_t ws_bytes, tiermm_stream_t stream) {
+  const char* who = "tiermm_qgemm_grouped";
+  if (n_experts < 0 || !expert_offsets || (n_experts && (!W_e || !qtype_e || !rb_e)))
+    return set_error(TIERMM_EINVAL, "%s: null expert tables", who);
+  if (n_experts && expert_offsets[0] != 0) return set_error(TIERMM_EINVAL, "%s: expert_offsets[0] != 0", who);
+  for (int e = 0; e < n_experts; ++e)
+    if (expert_offsets[e + 1] < expert_offsets[e]) return set_error(TIERMM_EINVAL, "%s: offsets decrease at %d", who, e);
+  void* w = nullptr;
+  int st = get_workspace(ws, ws_bytes, tiermm_qgemm_grouped_ws_bytes(qtype_e, expert_offsets, n_experts, N, K, mode),
+                         &w, who);
+  if (st) return st;
+  const size_t wsb = tiermm_qgemm_grouped_ws_bytes(qtype_e, expert_offsets, n_experts, N, K, mode);
+  // one stream: the experts' GEMMs run in order and share the workspace
+  for (int e = 0; e < n_experts; ++e) {
+    const int o = expert_offsets[e], Me = expert_offsets[e + 1] - o;
+    if (Me == 0) continue;
+    st = tiermm_qgemm(W_e[e], qtype_e[e], rb_e[e], X_sorted + (size_t)o * K, Y_sorted + (size_t)o * N, Me, N, K, N,
+                      mode, 0.f, w, wsb, stream);
+    if (st) return st;
+  }
+  return TIERMM_OK;
+}
+
+int tiermm_moe_combine(const float* Y_sorted, const int* token_pairs, const float* pair_weight, float* out, int T,
+                       int topk, int N, tiermm_stream_t stream) {
+  if (T < 0 || topk < 0 || N < 0) return set_error(TIERMM_EINVAL, "tiermm_moe_combine: negative size");
+  if (T == 0 || N == 0) return TIERMM_OK;
+  if (!Y_sorted || !token_pairs || !pair_weight || !out) return set_error(TIERMM_EINVAL, "tiermm_moe_combine: null buffer");
+  moe_combine_kernel<<<T, 256, 0, (hipStream_t)stream>>>(Y_sorted, token_pairs, pair_weight, out, topk, N);
+  TM_LAUNCH_CHECK("tiermm_moe_combine: launch");
+  return TIERMM_OK;
 }
 
 }  // extern "C"
