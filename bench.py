@@ -93,6 +93,97 @@ def time_launches(hip, stream, launch, steps: int, warmup: int) -> float:
     return per
 
 
+def _quantized(tier_amd, qtype, N, K, seed):
+    """W ~N(0,0.02) through the host quantizer; q5_0 (no quantizer in the reference) as
+    random 5-bit values with fp16 d ~ N(0, 0.004), the scale such W would get."""
+    rng = np.random.default_rng(seed)
+    if qtype == tier_amd.Q5_0:
+        nb = K // 32
+        b = rng.integers(0, 256, size=(N * nb, 22), dtype=np.uint8)
+        b[:, 0:2] = (rng.standard_normal(N * nb) * 0.004).astype(np.float16).view(np.uint8).reshape(-1, 2)
+        return b.reshape(N, nb * 22)
+    return tier_amd.q_row(qtype, rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
+
+
+def bench_decoder_layer(tier_amd, hip, stream):
+    """Config 4: the 7 projections of one decoder layer (hidden 5120, 32 q / 8 kv heads x 128,
+    ffn 14336) on a packed 4096-token batch, q4_K_S recipe (q/k/o/gate/up q4_K, v/down q5_K),
+    each a tiermm_qgemm (fp16-dequant x3 semantics)."""
+    T, H, Q, KV, F = 4096, 5120, 4096, 1024, 14336
+    mats = (("q", tier_amd.Q4_K, Q, H), ("k", tier_amd.Q4_K, KV, H), ("v", tier_amd.Q5_K, KV, H),
+            ("o", tier_amd.Q4_K, H, Q), ("gate", tier_amd.Q4_K, F, H), ("up", tier_amd.Q4_K, F, H),
+            ("down", tier_amd.Q5_K, H, F))
+    rng = np.random.default_rng(10)
+    xs = {K: hip.to_device(rng.standard_normal((T, K), dtype=np.float32)) for K in (H, Q, F)}
+    Y = hip.DeviceBuffer(T * F * 4)
+    wsb = max(tier_amd.qgemm_ws_bytes(qt, T, N, K) for _, qt, N, K in mats)
+    WS = hip.DeviceBuffer(wsb)
+    out, total_us, total_flop = {}, 0.0, 0.0
+    for i, (name, qt, N, K) in enumerate(mats):
+        log(f"bench: decoder layer {name} {N}x{K}")
+        Wd = hip.to_device(_quantized(tier_amd, qt, N, K, 11 + i))
+        rb = tier_amd.q_row_bytes(qt, K)
+        f = lambda _i: tier_amd.qgemm(Wd.ptr, qt, rb, xs[K].ptr, Y.ptr, T, N, K, N,  # noqa: E731
+                                      tier_amd.MODE_X3REF, 0.0, WS.ptr, wsb, stream)
+        km = time_launches(hip, stream, f, 5, 2)
+        flop = 2.0 * T * N * K
+        out[name] = {"type": tier_amd.TYPE_NAMES[qt], "N": N, "K": K, "us": round(km * 1e3, 1),
+                     "TFLOPS": round(flop / (km * 1e-3) / 1e12, 1)}
+        total_us += km * 1e3
+        total_flop += flop
+        del Wd
+    tf = total_flop / (total_us * 1e-6) / 1e12
+    return {"recipe": "q4_K_S (v, down q5_K)", "T": T, "total_us": round(total_us, 1),
+            "TFLOPS": round(tf, 1), "frac_x3_peak": round(tf / X3_PEAK_TFLOPS, 4), "per_matrix": out}
+
+
+def bench_moe(tier_amd, hip, stream):
+    """Config 5: 64 experts, top-8 of softmax(router logits ~N(0,1)), hidden 2048, expert ffn
+    1408; 4096 tokens sorted by expert; gate/up q4_K, down q5_0 (K = 1408 is not a whole
+    number of 256-element super-blocks); grouped GEMMs + per-token weighted combine."""
+    T, E, topk, H, F = 4096, 64, 8, 2048, 1408
+    rng = np.random.default_rng(18)
+    logits = rng.standard_normal((T, E))
+    prob = np.exp(logits - logits.max(1, keepdims=True))
+    prob /= prob.sum(1, keepdims=True)
+    top = np.argsort(-prob, axis=1, kind="stable")[:, :topk]
+    pair_exp = top.ravel()
+    pair_w = prob[np.arange(T)[:, None], top].ravel().astype(np.float32)
+    order = np.argsort(pair_exp, kind="stable")
+    inv = np.empty_like(order)
+    inv[order] = np.arange(order.size)
+    offsets = np.concatenate([[0], np.cumsum(np.bincount(pair_exp, minlength=E))]).astype(np.int32).tolist()
+    P = T * topk
+    # 8 distinct quantized experts per matrix, copied to 64 device buffers
+    log("bench: moe weights")
+    ws_ = {}
+    for name, qt, N, K in (("gate", tier_amd.Q4_K, F, H), ("up", tier_amd.Q4_K, F, H), ("down", tier_amd.Q5_0, H, F)):
+        base = [_quantized(tier_amd, qt, N, K, 19 + 31 * j + len(ws_)) for j in range(8)]
+        ws_[name] = (qt, N, K, [hip.to_device(base[e % 8]) for e in range(E)])
+    Xs = hip.to_device(rng.standard_normal((P, H), dtype=np.float32))
+    A = hip.to_device(rng.standard_normal((P, F), dtype=np.float32))
+    G, U, D = hip.DeviceBuffer(P * F * 4), hip.DeviceBuffer(P * F * 4), hip.DeviceBuffer(P * H * 4)
+    TP, PW, OUT = hip.to_device(inv.reshape(T, topk).astype(np.int32)), hip.to_device(pair_w[order]), \
+        hip.DeviceBuffer(T * H * 4)
+    wsb = max(tier_amd.qgemm_grouped_ws_bytes([q] * E, offsets, N, K) for q, N, K, _ in ws_.values())
+    WS = hip.DeviceBuffer(wsb)
+
+    def step(_i):
+        for name, dst, src in (("gate", G, Xs), ("up", U, Xs), ("down", D, A)):
+            qt, N, K, bufs = ws_[name]
+            tier_amd.qgemm_grouped([b.ptr for b in bufs], [qt] * E, [tier_amd.q_row_bytes(qt, K)] * E, src.ptr,
+                                   offsets, dst.ptr, N, K, tier_amd.MODE_X3REF, WS.ptr, wsb, stream)
+        tier_amd.moe_combine(D.ptr, TP.ptr, PW.ptr, OUT.ptr, T, topk, H, stream)
+
+    log("bench: moe grouped GEMMs")
+    km = time_launches(hip, stream, step, 3, 1)
+    flop = 2.0 * P * (2 * F * H + H * F)
+    tf = flop / (km * 1e-3) / 1e12
+    return {"experts": E, "topk": topk, "tokens": T, "us": round(km * 1e3, 1), "TFLOPS": round(tf, 1),
+            "frac_x3_peak": round(tf / X3_PEAK_TFLOPS, 4), "types": "gate/up q4_K, down q5_0",
+            "includes": "3 grouped GEMMs (64 experts each) + combine; no activation between"}
+
+
 def measured_traffic():
     """HBM bytes per headline launch from the committed rocprofv3 PMC summary
     (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter's reading for a copy
@@ -212,6 +303,8 @@ def main() -> int:
         secondary["x3s_4096x5120x5120"] = {"TFLOPS": round(tf, 2), "frac_x3_peak": round(tf / X3_PEAK_TFLOPS, 4),
                                            "us_per_call": round(km * 1e3, 1), "includes": "X split + GEMM"}
         del bufs, Wf, Xf
+        secondary["decoder_layer_t4096"] = bench_decoder_layer(tier_amd, hip, stream)
+        secondary["moe_t4096"] = bench_moe(tier_amd, hip, stream)
 
     traffic, traffic_src = measured_traffic()
     cpu = None
