@@ -204,6 +204,15 @@ int tiermm_moe_combine(const float* Y_sorted, const int* token_pairs, const floa
  * threads (<= 0: all hardware threads). */
 int tiermm_quantize(int qtype, const float* x, void* out, size_t rows, int cols, int nthreads);
 
+/* Type of one projection under a quantization recipe (tier.cpp:2701-2713, the
+ * same rule as recipe_types in tierlm.py:1858-1874).  recipe: "Q8_0", "Q6_K",
+ * "Q5_K_M", "Q5_K_S", "Q4_K_M" or "Q4_K_S"; slot 0..6 = q, k, v, o, gate, up,
+ * down projection; for slot 2 (index, count) = the v_proj's rank among the
+ * layers that have one and their number, for slot 6 the layer index and the
+ * number of layers (ignored for other slots).  Returns the type id, or
+ * TIERMM_EINVAL for an unknown recipe. */
+int tiermm_recipe_type(const char* recipe, int slot, int index, int count);
+
 #ifdef __cplusplus
 }
 #endif

@@ -115,3 +115,35 @@ def test_workspace_sizes():
     assert tier_amd.qgemm_ws_bytes(tier_amd.Q4_K, 512, 5120, 5120) == 3 * 512 * 5120 * 2
     # other types stage fp16 W in the workspace as well
     assert tier_amd.qgemm_ws_bytes(tier_amd.Q6_K, 512, 5120, 5120) == 5120 * 5120 * 2 + 3 * 512 * 5120 * 2
+
+
+def _mats(n_layers, no_v=()):
+    keys = tier_amd.SLOTS
+    return [(l, k, 0, 0) for l in range(n_layers) for k in keys if not (k == "self_attn.v_proj" and l in no_v)]
+
+
+def test_recipe_types_hand_checked():
+    """tier.cpp:2701-2713 / tierlm.py:1858-1874 on stacks worked out by hand: with 8 layers the
+    "more" layers are 0 (first eighth), 7 (last eighth), 3 and 6 (every third after the first eighth)."""
+    def of(rec, mats, key):
+        return [t for (l, k, *_), t in zip(mats, tier_amd.recipe_types(rec, mats)) if k == key]
+    m8 = _mats(8)
+    assert of("Q4_K_M", m8, "self_attn.v_proj") == ["q6_K", "q4_K", "q4_K", "q6_K", "q4_K", "q4_K", "q6_K", "q6_K"]
+    assert of("Q4_K_M", m8, "mlp.down_proj") == ["q6_K", "q4_K", "q4_K", "q6_K", "q4_K", "q4_K", "q6_K", "q6_K"]
+    assert of("Q4_K_M", m8, "self_attn.q_proj") == ["q4_K"] * 8
+    assert of("Q4_K_S", m8, "self_attn.v_proj") == ["q5_K"] * 4 + ["q4_K"] * 4
+    assert of("Q4_K_S", m8, "mlp.down_proj") == ["q5_K"] + ["q4_K"] * 7
+    assert of("Q5_K_S", m8, "self_attn.v_proj") == ["q5_K"] * 8
+    assert of("Q5_K_M", m8, "mlp.down_proj") == ["q6_K", "q5_K", "q5_K", "q6_K", "q5_K", "q5_K", "q6_K", "q6_K"]
+    assert set(tier_amd.recipe_types("Q6_K", m8)) == {"q6_K"}
+    assert set(tier_amd.recipe_types("Q8_0", m8)) == {"q8_0"}
+    # 48 layers: first and last six, and 8, 11, ..., 41
+    raised = set(range(6)) | set(range(42, 48)) | set(range(8, 42, 3))
+    downs = of("Q4_K_M", _mats(48), "mlp.down_proj")
+    assert [i for i, t in enumerate(downs) if t == "q6_K"] == sorted(raised)
+    # v_proj ranks count only the layers that have one: without v in layers 2 and 5, the
+    # six v_proj have ranks 0..5 and the raised ranks are 2 and 5 (layers 3 and 7)
+    mv = _mats(8, no_v=(2, 5))
+    assert of("Q4_K_M", mv, "self_attn.v_proj") == ["q4_K", "q4_K", "q6_K", "q4_K", "q4_K", "q6_K"]
+    with pytest.raises(tier_amd.TiermmError):
+        tier_amd.recipe_types("Q3_K", m8)

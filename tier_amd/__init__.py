@@ -47,7 +47,7 @@ EXPORTS = (
     "tiermm_q_row_bytes", "tiermm_dequant", "tiermm_qgemv", "tiermm_split3_f16", "tiermm_x3_gemm",
     "tiermm_x3_gemm_ws_bytes", "tiermm_x3_rows", "tiermm_x3_rows_ws_bytes", "tiermm_x3s_split",
     "tiermm_x3s_gemm", "tiermm_qgemm", "tiermm_qgemm_ws_bytes", "tiermm_quantize", "tiermm_gemv",
-    "tiermm_qgemm_grouped", "tiermm_qgemm_grouped_ws_bytes", "tiermm_moe_combine",
+    "tiermm_qgemm_grouped", "tiermm_qgemm_grouped_ws_bytes", "tiermm_moe_combine", "tiermm_recipe_type",
 )
 
 
@@ -99,6 +99,7 @@ _sig("tiermm_qgemm_grouped", [ctypes.POINTER(_vp), _pi, ctypes.POINTER(_sz), _vp
                               _sz, _vp])
 _sig("tiermm_qgemm_grouped_ws_bytes", [_pi, _pi, _i, _i, _i, _i], _sz)
 _sig("tiermm_moe_combine", [_vp, _vp, _vp, _vp, _i, _i, _i, _vp])
+_sig("tiermm_recipe_type", [ctypes.c_char_p, _i, _i, _i])
 
 
 def lib():
@@ -246,6 +247,31 @@ def qgemm_grouped(W_e, qtype_e, rb_e, X_sorted: int, offsets, Y_sorted: int, N: 
     """Experts' quantized matmuls of a routed batch (host tables; device W_e, X, Y)."""
     n, w, q, r, o = _grouped_tables(W_e, qtype_e, rb_e, offsets)
     _check(_L.tiermm_qgemm_grouped(w, q, r, X_sorted, o, n, Y_sorted, N, K, mode, ws, ws_bytes, _s(stream)))
+
+
+SLOTS = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj", "mlp.gate_proj",
+         "mlp.up_proj", "mlp.down_proj")
+
+
+def recipe_types(rec: str, mats) -> list[str]:
+    """tierlm.py:1858-1874 recipe_types: the type name of each matrix (layer, key, rows, cols)
+    under recipe `rec`, by the library's rule (tier.cpp:2701-2713)."""
+    mats = list(mats)
+    n_layers = 1 + max((l for l, k, *_ in mats if k == "mlp.down_proj"), default=-1)
+    n_v = sum(1 for _, k, *_ in mats if k == "self_attn.v_proj")
+    out, v_rank = [], 0
+    for layer, key, *_ in mats:
+        slot = SLOTS.index(key) if key in SLOTS else 0
+        if slot == 2:
+            index, count = v_rank, n_v
+            v_rank += 1
+        else:
+            index, count = layer, n_layers
+        t = _L.tiermm_recipe_type(rec.encode(), slot, index, count)
+        if t < 0 or t == EINVAL:
+            raise TiermmError(t, last_error())
+        out.append(TYPE_NAMES[t])
+    return out
 
 
 def moe_combine(Y_sorted: int, token_pairs: int, pair_weight: int, out: int, T: int, topk: int, N: int,

@@ -34,14 +34,22 @@ constexpr int QBM = 128, QBK = 32;
 constexpr int XPART = QBM * 64;  // bytes of one x part per stage
 constexpr int XRING = 4;         // x stages in LDS: three in flight while one is multiplied
 
+// A launch covers up to QG groups (one plain GEMM, or the experts of a routed
+// batch): group g multiplies rows [row0[g], row0[g] + rows[g]) of X and Y with
+// weight W[g]; its tiles are workgroups [tile0[g], tile0[g+1]).
+constexpr int QG = 64;
 struct QArgs {
-  const uint8_t* W;
-  size_t rb;
-  const uint16_t* X;  // parts at X, X + xs, X + 2 xs (hi, mid, lo)
+  const uint16_t* X;  // parts at X, X + xs, X + 2 xs (hi, mid, lo), rows of K halfs
   size_t xs;
   float* Y;
-  int ldy, M, N, K;
+  size_t rb;
+  int ldy, N, K;
   float beta;
+  int ngroups;
+  int tile0[QG + 1];
+  int row0[QG];
+  int rows[QG];
+  const uint8_t* W[QG];
 };
 
 __device__ __forceinline__ uint32_t swz(int row, int chunk) { return (uint32_t)(row * 64 + ((chunk ^ ((row >> 2) & 3)) * 16)); }
@@ -59,9 +67,16 @@ __global__ __launch_bounds__(256) void qgemm_q4k_x3ref(const QArgs p) {
   uint8_t* lds = (uint8_t*)lds_h;
   const uint32_t lds0 = lds_addr(lds);
 
+  int grp = 0;  // the group of this workgroup (uniform scan over the tile prefix)
+  while (grp + 1 < p.ngroups && (int)blockIdx.x >= p.tile0[grp + 1]) ++grp;
+  const int tile = (int)blockIdx.x - p.tile0[grp];
   const int ntn = (p.N + BN - 1) / BN;
-  const int tm = blockIdx.x / ntn, tn = blockIdx.x % ntn;
+  const int tm = tile / ntn, tn = tile % ntn;
   const int m0 = tm * QBM, n0 = tn * BN;
+  const int M = p.rows[grp];
+  const uint16_t* Xg = p.X + (size_t)p.row0[grp] * p.K;
+  float* Yg = p.Y + (size_t)p.row0[grp] * p.ldy;
+  const uint8_t* Wg = p.W[grp];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
   // x DMA: 3 parts x 8 loads of 16 rows per stage, 6 per wave
@@ -71,7 +86,7 @@ __global__ __launch_bounds__(256) void qgemm_q4k_x3ref(const QArgs p) {
   for (int u = 0; u < 6; ++u) {
     const int t = wave + 4 * u, part = t >> 3, ch = t & 7;
     const int row = ch * 16 + (lane >> 2), slot = lane & 3;
-    xsrc[u] = p.X + part * p.xs + (size_t)min(m0 + row, p.M - 1) * p.K + 8 * (slot ^ ((row >> 2) & 3));
+    xsrc[u] = Xg + part * p.xs + (size_t)min(m0 + row, M - 1) * p.K + 8 * (slot ^ ((row >> 2) & 3));
     xoff[u] = (uint32_t)(part * XPART + ch * 1024);
   }
   auto issue_x = [&](int kt) __attribute__((always_inline)) {
@@ -95,7 +110,7 @@ __global__ __launch_bounds__(256) void qgemm_q4k_x3ref(const QArgs p) {
   for (int u = 0; u < RAWI; ++u) {
     const int f = (wave + 4 * u) * 1024 + lane * 16;
     const int r = min(f / 48, BN - 1), c = (f % 48) >> 4;
-    rsrc[u] = p.W + (size_t)min(n0 + r, p.N - 1) * p.rb;
+    rsrc[u] = Wg + (size_t)min(n0 + r, p.N - 1) * p.rb;
     rkind[u] = c;
   }
   auto issue_raw = [&](int kt) __attribute__((always_inline)) {
@@ -206,8 +221,8 @@ __global__ __launch_bounds__(256) void qgemm_q4k_x3ref(const QArgs p) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = m0 + wave * 32 + i * 16 + 4 * (lane >> 4) + r;
-        if (row >= p.M) continue;
-        float* c = p.Y + (size_t)row * p.ldy + col;
+        if (row >= M) continue;
+        float* c = Yg + (size_t)row * p.ldy + col;
         float v = acc[i][j][r];
         if (p.beta != 0.f) v = fmaf(p.beta, *c, v);
         *c = v;
@@ -226,37 +241,68 @@ int launch_q(const QArgs& a, hipStream_t s, const char* who) {
     if (e != hipSuccess) return hip_fail(e, who);
     attr_set = true;
   }
-  const unsigned grid = (unsigned)(((a.M + QBM - 1) / QBM) * ((a.N + BN - 1) / BN));
-  qgemm_q4k_x3ref<BN><<<grid, 256, lds, s>>>(a);
+  qgemm_q4k_x3ref<BN><<<(unsigned)a.tile0[a.ngroups], 256, lds, s>>>(a);
   TM_LAUNCH_CHECK(who);
   return TIERMM_OK;
 }
 
+// Tiles of one BN over the groups' row counts.
+long q_tiles(const int* rows, int n, int N, int bn) {
+  long t = 0;
+  for (int g = 0; g < n; ++g) t += (long)((rows[g] + QBM - 1) / QBM) * ((N + bn - 1) / bn);
+  return t;
+}
+
 }  // namespace
 
-// BN with the shortest critical path: rounds of workgroups over the CUs times
-// the work of one tile (proportional to BN); larger BN on ties.
-int qgemm_q4k_fused(const void* W, size_t rb, const uint16_t* xparts, size_t xs, float* Y, int ldy, int M, int N, int K,
-                    float beta, int cus, hipStream_t s, const char* who) {
-  QArgs a{(const uint8_t*)W, rb, xparts, xs, Y, ldy, M, N, K, beta};
+// Fused q4_K x3-ref GEMM over n groups (rows[g] rows of x from row0[g], weight W[g]);
+// the x planes hold every group's rows (plane stride xs).  BN is the one with the
+// shortest critical path: rounds of workgroups over the CUs times the work of a
+// tile (proportional to BN), larger BN on ties.
+int qgemm_q4k_fused_groups(const void* const* W, const int* row0, const int* rows, int n, size_t rb,
+                           const uint16_t* xparts, size_t xs, float* Y, int ldy, int N, int K, float beta, int cus,
+                           hipStream_t s, const char* who) {
   const int cand[5] = {128, 112, 96, 80, 64};
   int best = 128;
   long best_t = -1;
   for (int c : cand) {
-    const long tiles = (long)((M + QBM - 1) / QBM) * ((N + c - 1) / c);
-    const long t = (tiles + cus - 1) / cus * c;
+    const long t = (q_tiles(rows, n, N, c) + cus - 1) / cus * c;
     if (best_t < 0 || t < best_t) {
       best_t = t;
       best = c;
     }
   }
-  switch (best) {
-    case 128: return launch_q<128>(a, s, who);
-    case 112: return launch_q<112>(a, s, who);
-    case 96: return launch_q<96>(a, s, who);
-    case 80: return launch_q<80>(a, s, who);
-    default: return launch_q<64>(a, s, who);
+  for (int g0 = 0; g0 < n; g0 += QG) {
+    QArgs a{};
+    a.X = xparts; a.xs = xs; a.Y = Y; a.rb = rb; a.ldy = ldy; a.N = N; a.K = K; a.beta = beta;
+    a.ngroups = 0;
+    a.tile0[0] = 0;
+    for (int g = g0; g < n && g < g0 + QG; ++g) {
+      if (rows[g] == 0) continue;
+      const int j = a.ngroups++;
+      a.row0[j] = row0[g];
+      a.rows[j] = rows[g];
+      a.W[j] = (const uint8_t*)W[g];
+      a.tile0[j + 1] = a.tile0[j] + (int)q_tiles(&rows[g], 1, N, best);
+    }
+    if (a.ngroups == 0) continue;
+    int st;
+    switch (best) {
+      case 128: st = launch_q<128>(a, s, who); break;
+      case 112: st = launch_q<112>(a, s, who); break;
+      case 96: st = launch_q<96>(a, s, who); break;
+      case 80: st = launch_q<80>(a, s, who); break;
+      default: st = launch_q<64>(a, s, who); break;
+    }
+    if (st) return st;
   }
+  return TIERMM_OK;
+}
+
+int qgemm_q4k_fused(const void* W, size_t rb, const uint16_t* xparts, size_t xs, float* Y, int ldy, int M, int N, int K,
+                    float beta, int cus, hipStream_t s, const char* who) {
+  const int row0 = 0;
+  return qgemm_q4k_fused_groups(&W, &row0, &M, 1, rb, xparts, xs, Y, ldy, N, K, beta, cus, s, who);
 }
 
 }  // namespace tiermm

@@ -11,6 +11,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <string>
 #include <thread>
 #include <vector>
 
@@ -339,3 +340,33 @@ int quantize_rows(int qtype, const float* x, void* out, size_t rows, int cols, i
 }
 
 }  // namespace tiermm
+
+using namespace tiermm;
+
+// Type of one matrix under a quantization recipe (tier.cpp:2701-2713, mirrored
+// by tierlm.py:1858-1874).  The recipe names a base type; "_M" recipes raise the
+// v_proj and down_proj of the "more" layers to Q6_K -- the first and last eighth
+// of the stack and every third layer between -- and "_S" recipes with a Q4_K
+// base raise the first four v_proj and the down_proj of the first eighth of the
+// layers to Q5_K.  slot: 0..6 = q, k, v, o, gate, up, down; (index, count) =
+// the v_proj's rank among the layers that have one and their number for slot 2,
+// the layer and the number of layers for slot 6.
+extern "C" int tiermm_recipe_type(const char* recipe, int slot, int index, int count) {
+  if (!recipe) return set_error(TIERMM_EINVAL, "tiermm_recipe_type: null recipe");
+  const std::string r(recipe);
+  int base;
+  if (r == "Q8_0") base = QT_Q8_0;
+  else if (r == "Q6_K") base = QT_Q6_K;
+  else if (r.compare(0, 4, "Q5_K") == 0) base = QT_Q5_K;
+  else if (r.compare(0, 4, "Q4_K") == 0) base = QT_Q4_K;
+  else return set_error(TIERMM_EINVAL, "tiermm_recipe_type: unknown recipe %s", recipe);
+  const bool m_rec = r.size() > 2 && r.compare(r.size() - 2, 2, "_M") == 0;
+  const bool s_rec = r.size() > 2 && r.compare(r.size() - 2, 2, "_S") == 0;
+  if (slot != 2 && slot != 6) return base;
+  const int eighth = count / 8;
+  const bool raised = index < eighth || index >= 7 * count / 8 || (index >= eighth && (index - eighth) % 3 == 2);
+  if (m_rec && raised) return QT_Q6_K;
+  const int limit = slot == 2 ? 4 : eighth;  // first four v_proj / first eighth of the down_proj
+  if (s_rec && base == QT_Q4_K && index < limit) return QT_Q5_K;
+  return base;
+}

@@ -18,6 +18,7 @@
 // current one).  LDS rows are 64 data bytes + 16 pad bytes so the 16-byte
 // fragment reads of 8 consecutive rows hit distinct banks.
 #include <algorithm>
+#include <vector>
 
 #include "tm_device.h"
 
@@ -27,6 +28,9 @@ int check_qweight(const char* who, const void* W, int qtype, size_t rb, int cols
 int dequant_f16_rows(const void* W, int qtype, size_t rb, int cols, size_t nrows, uint16_t* out, hipStream_t s);
 int qgemm_q4k_fused(const void* W, size_t rb, const uint16_t* xparts, size_t xs, float* Y, int ldy, int M, int N, int K,
                     float beta, int cus, hipStream_t s, const char* who);
+int qgemm_q4k_fused_groups(const void* const* W, const int* row0, const int* rows, int n, size_t rb,
+                           const uint16_t* xparts, size_t xs, float* Y, int ldy, int N, int K, float beta, int cus,
+                           hipStream_t s, const char* who);
 int device_cus(int* cus);
 
 namespace {
@@ -708,11 +712,22 @@ int tiermm_qgemm(const void* W, int qtype, size_t rb, const float* X, float* Y, 
 size_t tiermm_qgemm_grouped_ws_bytes(const int* qtype_e, const int* expert_offsets, int n_experts, int N, int K,
                                      int mode) {
   size_t need = 0;
+  if (mode == TIERMM_MODE_F32) {  // expert by expert through tiermm_qgemm
+    for (int e = 0; e < n_experts; ++e) {
+      const int Me = expert_offsets[e + 1] - expert_offsets[e];
+      if (Me > 0) need = std::max(need, tiermm_qgemm_ws_bytes(qtype_e[e], Me, N, K, mode));
+    }
+    return need;
+  }
+  // x3-ref: the three fp16 planes of all routed rows, plus one expert's fp16 W for
+  // the experts that are not decoded inside the GEMM
+  const size_t P = n_experts > 0 ? (size_t)expert_offsets[n_experts] : 0;
+  bool staged = false;
   for (int e = 0; e < n_experts; ++e) {
     const int Me = expert_offsets[e + 1] - expert_offsets[e];
-    if (Me > 0) need = std::max(need, tiermm_qgemm_ws_bytes(qtype_e[e], Me, N, K, mode));
+    if (Me > 0 && qtype_e[e] != TIERMM_Q4_K) staged = true;
   }
-  return need;
+  return al256(3 * P * K * sizeof(uint16_t)) + (staged ? (size_t)N * K * sizeof(uint16_t) : 0);
 }
 
 int tiermm_qgemm_grouped(const void* const* W_e, const int* qtype_e, const size_t* rb_e, const float* X_sorted,
@@ -724,17 +739,64 @@ int tiermm_qgemm_grouped(const void* const* W_e, const int* qtype_e, const size_
   if (n_experts && expert_offsets[0] != 0) return set_error(TIERMM_EINVAL, "%s: expert_offsets[0] != 0", who);
   for (int e = 0; e < n_experts; ++e)
     if (expert_offsets[e + 1] < expert_offsets[e]) return set_error(TIERMM_EINVAL, "%s: offsets decrease at %d", who, e);
-  void* w = nullptr;
-  int st = get_workspace(ws, ws_bytes, tiermm_qgemm_grouped_ws_bytes(qtype_e, expert_offsets, n_experts, N, K, mode),
-                         &w, who);
+  if (mode != TIERMM_MODE_X3REF && mode != TIERMM_MODE_F32) return set_error(TIERMM_EINVAL, "%s: mode %d", who, mode);
+  int st = check_nt(who, 1, N, K);
   if (st) return st;
+  for (int e = 0; e < n_experts; ++e) {
+    if (expert_offsets[e + 1] == expert_offsets[e]) continue;
+    st = check_qweight(who, W_e[e], qtype_e[e], rb_e[e], K);
+    if (st) return st;
+  }
+  if (n_experts == 0 || expert_offsets[n_experts] == 0 || N == 0) return TIERMM_OK;
+  if (!X_sorted || !Y_sorted) return set_error(TIERMM_EINVAL, "%s: null buffer", who);
   const size_t wsb = tiermm_qgemm_grouped_ws_bytes(qtype_e, expert_offsets, n_experts, N, K, mode);
-  // one stream: the experts' GEMMs run in order and share the workspace
+  void* w = nullptr;
+  st = get_workspace(ws, ws_bytes, wsb, &w, who);
+  if (st) return st;
+  hipStream_t s = (hipStream_t)stream;
+  if (mode == TIERMM_MODE_F32) {  // one stream: the experts run in order and share the workspace
+    for (int e = 0; e < n_experts; ++e) {
+      const int o = expert_offsets[e], Me = expert_offsets[e + 1] - o;
+      if (Me == 0) continue;
+      st = tiermm_qgemm(W_e[e], qtype_e[e], rb_e[e], X_sorted + (size_t)o * K, Y_sorted + (size_t)o * N, Me, N, K, N,
+                        mode, 0.f, w, wsb, stream);
+      if (st) return st;
+    }
+    return TIERMM_OK;
+  }
+  // x3-ref: split every routed row once; each expert multiplies its slice of the planes
+  const size_t P = (size_t)expert_offsets[n_experts], pk = P * K;
+  uint16_t* parts = (uint16_t*)w;
+  uint16_t* w16 = (uint16_t*)((uint8_t*)w + al256(3 * pk * sizeof(uint16_t)));
+  st = split3_launch(X_sorted, parts, pk, pk, TIERMM_HML, s);
+  if (st) return st;
+  int cus = 0;
+  st = device_cus(&cus);
+  if (st) return st;
+  // q4_K experts: one launch (per 64 experts) whose workgroups cover every expert's tiles
+  std::vector<const void*> gw;
+  std::vector<int> g0, gr;
+  size_t grb = 0;
   for (int e = 0; e < n_experts; ++e) {
     const int o = expert_offsets[e], Me = expert_offsets[e + 1] - o;
-    if (Me == 0) continue;
-    st = tiermm_qgemm(W_e[e], qtype_e[e], rb_e[e], X_sorted + (size_t)o * K, Y_sorted + (size_t)o * N, Me, N, K, N,
-                      mode, 0.f, w, wsb, stream);
+    if (Me == 0 || qtype_e[e] != TIERMM_Q4_K) continue;
+    if (grb && rb_e[e] != grb) return set_error(TIERMM_EINVAL, "%s: q4_K experts with different row bytes", who);
+    grb = rb_e[e];
+    gw.push_back(W_e[e]);
+    g0.push_back(o);
+    gr.push_back(Me);
+  }
+  if (!gw.empty()) {
+    st = qgemm_q4k_fused_groups(gw.data(), g0.data(), gr.data(), (int)gw.size(), grb, parts, pk, Y_sorted, N, N, K,
+                                0.f, cus, s, who);
+    if (st) return st;
+  }
+  // other types: fp16 W staged per expert, then the x3-ref GEMM on the expert's rows
+  for (int e = 0; e < n_experts; ++e) {
+    const int o = expert_offsets[e], Me = expert_offsets[e + 1] - o;
+    if (Me == 0 || qtype_e[e] == TIERMM_Q4_K) continue;
+    st = dequant_f16_rows(W_e[e], qtype_e[e], rb_e[e], K, (size_t)N, w16, s);
+    if (!st) st = x3ref_nt(parts + (size_t)o * K, pk, w16, K, Y_sorted + (size_t)o * N, N, Me, N, K, 0.f, s, who);
     if (st) return st;
   }
   return TIERMM_OK;
