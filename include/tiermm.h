@@ -124,6 +124,11 @@ int tiermm_split3_f16(const float* x, uint16_t* parts, size_t n, size_t part_str
  * TIERMM_BF16}; W: N rows of K elements, 16-byte aligned; K <= 16384. */
 int tiermm_gemv(const void* W, int wtype, const float* x, float* y, int N, int K, tiermm_stream_t stream);
 
+/* split3_k (tier.cpp:866-867) / split3s (tier.cpp:2159-2161): the same split
+ * in bf16 parts (hip_bfloat16 rounding: nearest even), layouts as above. */
+int tiermm_split3_bf16(const float* x, uint16_t* parts, size_t n, size_t part_stride, int order,
+                       tiermm_stream_t stream);
+
 /* ------------------------------------------------------------ x3-ref GEMM */
 /* fp3gemm (tier.cpp:922-943) in its BLAS column-major contract:
  * C(m x n) = op(A)(m x k) * B(k x n) + beta * C, A fp16 (the frozen weight,
@@ -139,12 +144,22 @@ int tiermm_x3_gemm(int opA, int m, int n, int k, const uint16_t* A, int lda, con
                    tiermm_stream_t stream);
 size_t tiermm_x3_gemm_ws_bytes(int m, int n, int k);
 
+/* bf3gemm (tier.cpp:900-921): tiermm_x3_gemm with the weight in bf16 and x split
+ * in three bf16 parts, on bf16 MFMA (the engine's fallback when fp16 x3 is not
+ * available).  Same arguments, workspace size and accuracy bar. */
+int tiermm_x3_gemm_bf16(int opA, int m, int n, int k, const uint16_t* A, int lda, const float* B,
+                        float beta, float* C, int ldc, void* ws, size_t ws_bytes,
+                        tiermm_stream_t stream);
+
 /* chat_fp3 (tier.cpp:2195-2219): y[M][ldo] = x[M][K] * W[N][K]^T with x split
  * into three fp16 parts and W fp16, fp32 accumulation (the reference sums the
  * parts as (lo + mid) + hi, add3ld tier.cpp:2162-2164). ldo >= N. */
 int tiermm_x3_rows(const uint16_t* W, const float* x, float* y, int M, int K, int N, int ldo,
                    void* ws, size_t ws_bytes, tiermm_stream_t stream);
 size_t tiermm_x3_rows_ws_bytes(int M, int K, int N);
+/* chat_bf3 (tier.cpp:2165-2189): tiermm_x3_rows with a bf16 weight and bf16 parts. */
+int tiermm_x3_rows_bf16(const uint16_t* W, const float* x, float* y, int M, int K, int N, int ldo,
+                        void* ws, size_t ws_bytes, tiermm_stream_t stream);
 
 /* ------------------------------------------------------------ x3-2x2 GEMM */
 /* Two-part split with a power-of-two exponent per row (the storage of the 2x2

@@ -214,3 +214,65 @@ def test_qgemm_f32_mode(gpu, name, t, M, N, K):
     got = Y.download(np.float32, M * N).reshape(M, N)
     wf = oracle.dequant(blocks, t, K, oracle.OUT_F32).reshape(N, K)
     assert oracle.rel_fro(got, x.astype(np.float64) @ wf.astype(np.float64).T) <= BAR
+
+
+def _bf16(w):
+    return oracle.f2bf(np.ascontiguousarray(w, np.float32)).reshape(w.shape)
+
+
+def _bf16_to_f64(b):
+    return (b.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+def test_split3_bf16_bit_exact(gpu):
+    """split3_k / split3s (tier.cpp:866-867, 2159-2161): hip_bfloat16 rounding of v, v - h, v - h - m."""
+    rng = np.random.default_rng(23)
+    x = np.concatenate([rng.standard_normal(5000).astype(np.float32) * 3,
+                        np.array([0.0, -0.0, 1e-30, -7.5e4, 3.0e38], np.float32)])
+    n = x.size
+    X, P = hip.to_device(x), hip.DeviceBuffer(3 * n * 2)
+    for order in (tier_amd.HML, tier_amd.LMH):
+        tier_amd.split3_bf16(X.ptr, P.ptr, n, n, order)
+        hip.synchronize()
+        got = P.download(np.uint16, 3 * n).reshape(3, n)
+        h = _bf16(x)
+        r = x - (h.astype(np.uint32) << 16).view(np.float32)
+        m = _bf16(r)
+        l = _bf16(r - (m.astype(np.uint32) << 16).view(np.float32))
+        want = np.stack([h, m, l]) if order == tier_amd.HML else np.stack([l, m, h])
+        assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("opA", [tier_amd.OP_T, tier_amd.OP_N])
+def test_bf3gemm_contract(gpu, opA):
+    """bf3gemm (tier.cpp:900-921): the fp3gemm contract with bf16 storage, forward (OP_T) and dX (OP_N)."""
+    rng = np.random.default_rng(29)
+    M, N, K = 130, 256, 320
+    w16 = _bf16((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    if opA == tier_amd.OP_T:  # out[M][N] = x W^T
+        x = activations(M, K, seed=30)
+        A, B, C = hip.to_device(w16), hip.to_device(x), hip.DeviceBuffer(M * N * 4)
+        tier_amd.bf3gemm(opA, N, M, K, A.ptr, K, B.ptr, 0.0, C.ptr, N)
+        ref = x.astype(np.float64) @ _bf16_to_f64(w16).T
+        shape = (M, N)
+    else:  # dX[M][K] = dY W
+        dy = activations(M, N, seed=31)
+        A, B, C = hip.to_device(w16), hip.to_device(dy), hip.DeviceBuffer(M * K * 4)
+        tier_amd.bf3gemm(opA, K, M, N, A.ptr, K, B.ptr, 0.0, C.ptr, K)
+        ref = dy.astype(np.float64) @ _bf16_to_f64(w16)
+        shape = (M, K)
+    hip.synchronize()
+    got = C.download(np.float32, shape[0] * shape[1]).reshape(shape)
+    assert oracle.rel_fro(got, ref) <= BAR
+
+
+def test_chat_bf3_rows(gpu):
+    rng = np.random.default_rng(33)
+    M, N, K, ldo = 64, 200, 1024, 208
+    w16 = _bf16((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    x = activations(M, K, seed=34)
+    A, B, Y = hip.to_device(w16), hip.to_device(x), hip.DeviceBuffer(M * ldo * 4)
+    assert tier_amd.chat_bf3(A.ptr, B.ptr, Y.ptr, M, K, N, ldo)
+    hip.synchronize()
+    got = Y.download(np.float32, M * ldo).reshape(M, ldo)[:, :N]
+    assert oracle.rel_fro(got, x.astype(np.float64) @ _bf16_to_f64(w16).T) <= BAR

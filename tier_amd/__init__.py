@@ -48,6 +48,7 @@ EXPORTS = (
     "tiermm_x3_gemm_ws_bytes", "tiermm_x3_rows", "tiermm_x3_rows_ws_bytes", "tiermm_x3s_split",
     "tiermm_x3s_gemm", "tiermm_qgemm", "tiermm_qgemm_ws_bytes", "tiermm_quantize", "tiermm_gemv",
     "tiermm_qgemm_grouped", "tiermm_qgemm_grouped_ws_bytes", "tiermm_moe_combine", "tiermm_recipe_type",
+    "tiermm_split3_bf16", "tiermm_x3_gemm_bf16", "tiermm_x3_rows_bf16",
 )
 
 
@@ -100,6 +101,9 @@ _sig("tiermm_qgemm_grouped", [ctypes.POINTER(_vp), _pi, ctypes.POINTER(_sz), _vp
 _sig("tiermm_qgemm_grouped_ws_bytes", [_pi, _pi, _i, _i, _i, _i], _sz)
 _sig("tiermm_moe_combine", [_vp, _vp, _vp, _vp, _i, _i, _i, _vp])
 _sig("tiermm_recipe_type", [ctypes.c_char_p, _i, _i, _i])
+_sig("tiermm_split3_bf16", [_vp, _vp, _sz, _sz, _i, _vp])
+_sig("tiermm_x3_gemm_bf16", [_i, _i, _i, _i, _vp, _i, _vp, _f, _vp, _i, _vp, _sz, _vp])
+_sig("tiermm_x3_rows_bf16", [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp])
 
 
 def lib():
@@ -186,6 +190,27 @@ def fp3gemm(opA: int, m: int, n: int, k: int, A: int, lda: int, B: int, beta: fl
             ws: int | None = None, ws_bytes: int = 0, stream=None) -> None:
     """fp3gemm (tier.cpp:922) in its BLAS column-major contract."""
     _check(_L.tiermm_x3_gemm(opA, m, n, k, A, lda, B, beta, C, ldc, ws, ws_bytes, _s(stream)))
+
+
+def split3_bf16(x: int, parts: int, n: int, stride: int | None = None, order: int = HML, stream=None) -> None:
+    """split3_k / split3s (tier.cpp:866, 2159): bf16 parts."""
+    _check(_L.tiermm_split3_bf16(x, parts, n, n if stride is None else stride, order, _s(stream)))
+
+
+def bf3gemm(opA: int, m: int, n: int, k: int, A: int, lda: int, B: int, beta: float, C: int, ldc: int,
+            ws: int | None = None, ws_bytes: int = 0, stream=None) -> None:
+    """bf3gemm (tier.cpp:900): fp3gemm's contract with a bf16 weight and bf16 parts."""
+    _check(_L.tiermm_x3_gemm_bf16(opA, m, n, k, A, lda, B, beta, C, ldc, ws, ws_bytes, _s(stream)))
+
+
+def chat_bf3(W: int, x: int, y: int, M: int, K: int, N: int, ldo: int, ws: int | None = None, ws_bytes: int = 0,
+             stream=None) -> bool:
+    """chat_bf3 (tier.cpp:2165): False when the shape is not handled (the caller falls back)."""
+    code = _L.tiermm_x3_rows_bf16(W, x, y, M, K, N, ldo, ws, ws_bytes, _s(stream))
+    if code == UNSUPPORTED:
+        return False
+    _check(code)
+    return True
 
 
 def x3_gemm_ws_bytes(m: int, n: int, k: int) -> int:

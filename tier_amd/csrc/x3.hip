@@ -39,18 +39,25 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 
 // ------------------------------------------------------------------ splits
+// BF = false: fp16 parts (split3_fp_k / split3s_fp16); true: bf16 parts with
+// hip_bfloat16 rounding (split3_k tier.cpp:866-867, split3s 2159-2161).
+template <bool BF>
 __global__ __launch_bounds__(256) void split3_kernel(const float* __restrict__ x, uint16_t* __restrict__ parts,
                                                      size_t n, size_t stride, int order) {
   const size_t step = (size_t)gridDim.x * blockDim.x;
   uint16_t* p0 = parts;
   uint16_t* p1 = parts + stride;
   uint16_t* p2 = parts + 2 * stride;
+  auto to16 = [](float f) __attribute__((always_inline)) { return BF ? f2bf(f) : f2h(f); };
+  auto from16 = [](uint16_t u) __attribute__((always_inline)) {
+    return BF ? __uint_as_float((uint32_t)u << 16) : h2f(u);
+  };
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) {
     const float v = x[i];
-    const uint16_t h = f2h(v);
-    const float r = v - h2f(h);
-    const uint16_t m = f2h(r);
-    const uint16_t l = f2h(r - h2f(m));
+    const uint16_t h = to16(v);
+    const float r = v - from16(h);
+    const uint16_t m = to16(r);
+    const uint16_t l = to16(r - from16(m));
     if (order == TIERMM_HML) {
       p0[i] = h; p1[i] = m; p2[i] = l;
     } else {
@@ -135,7 +142,7 @@ constexpr int BK = 32;            // K per LDS stage (two 32x32x16 MFMA steps)
 constexpr int LDS_ROW = 40;       // halfs per LDS row: 32 data + 8 pad
 
 // Operand parts per GEMM flavour (the products are spelled out in the kernel).
-enum { X3_REF = 0, X3_2X2 = 1 };
+enum { X3_REF = 0, X3_2X2 = 1, X3_REF_BF16 = 2 };
 template <int MODE>
 struct X3Mode;
 template <>
@@ -143,9 +150,24 @@ struct X3Mode<X3_REF> {  // A = x hi/mid/lo, B = the fp16 weight
   static constexpr int NA = 3, NB = 1;
 };
 template <>
+struct X3Mode<X3_REF_BF16> {  // bf3gemm: A = x hi/mid/lo in bf16, B = the bf16 weight
+  static constexpr int NA = 3, NB = 1;
+};
+template <>
 struct X3Mode<X3_2X2> {  // A = X hi/lo, B = W hi/lo
   static constexpr int NA = 2, NB = 2;
 };
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+// One 32x32x16 MFMA step on 16-bit operands: bf16 for X3_REF_BF16, fp16 otherwise.
+template <int MODE>
+__device__ __forceinline__ float16v mfma16(const half8& a, const half8& b, const float16v& c) {
+  if constexpr (MODE == X3_REF_BF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                   0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
 
 struct X3Args {
   const uint16_t* A[3];  // [M][lda]
@@ -249,10 +271,10 @@ __global__ __launch_bounds__(256) void gemm_x3_kernel(const X3Args p) {
       for (int i = 0; i < WM; ++i)
 #pragma unroll
         for (int j = 0; j < WN; ++j) {
-          if constexpr (MODE == X3_REF) {  // lo, mid, hi times the fp16 weight (tier.cpp:940)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[2][i], bf[0][j], acc[i][j], 0, 0, 0);
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[1][i], bf[0][j], acc[i][j], 0, 0, 0);
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[0][i], bf[0][j], acc[i][j], 0, 0, 0);
+          if constexpr (MODE != X3_2X2) {  // lo, mid, hi times the weight (tier.cpp:940, 918)
+            acc[i][j] = mfma16<MODE>(af[2][i], bf[0][j], acc[i][j]);
+            acc[i][j] = mfma16<MODE>(af[1][i], bf[0][j], acc[i][j]);
+            acc[i][j] = mfma16<MODE>(af[0][i], bf[0][j], acc[i][j]);
           } else {  // hi*hi + hi*lo + lo*hi
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[0][i], bf[0][j], acc[i][j], 0, 0, 0);
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[0][i], bf[1][j], acc[i][j], 0, 0, 0);
@@ -401,14 +423,14 @@ __global__ __launch_bounds__(512) void gemm_x3_big(const X3Args p) {
 #pragma unroll
         for (int j = 0; j < XB_WN; ++j)
           bf[q][j] = *(const half8*)(s + NA * A_PART + q * B_PART + (wn * 160 + j * 32) * 64 + co);
-      if constexpr (MODE == X3_REF) {  // lo, mid, hi times the fp16 weight (tier.cpp:940)
+      if constexpr (MODE != X3_2X2) {  // lo, mid, hi times the weight (tier.cpp:940, 918)
 #pragma unroll
         for (int pa = 2; pa >= 0; --pa)
 #pragma unroll
           for (int j = 0; j < XB_WN; ++j)
 #pragma unroll
             for (int i = 0; i < XB_WM; ++i)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[pa][i], bf[0][j], acc[i][j], 0, 0, 0);
+              acc[i][j] = mfma16<MODE>(af[pa][i], bf[0][j], acc[i][j]);
       } else {  // hi*hi + hi*lo + lo*hi
         constexpr int PA[3] = {0, 0, 1}, PB[3] = {0, 1, 0};
 #pragma unroll
@@ -494,7 +516,7 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 // x3-ref product on pre-split activations: C[M][ldc] (beta)= sum_parts Xpart[M][K] * W[N][K]^T,
 // parts at xparts + {0, stride, 2*stride} in HML order, W fp16 with row stride ldw.
 int x3ref_nt(const uint16_t* xparts, size_t stride, const uint16_t* W, int ldw, float* C, int ldc, int M, int N,
-             int K, float beta, hipStream_t s, const char* who) {
+             int K, float beta, hipStream_t s, const char* who, bool bf16 = false) {
   X3Args a{};
   a.A[0] = xparts;
   a.A[1] = xparts + stride;
@@ -510,15 +532,22 @@ int x3ref_nt(const uint16_t* xparts, size_t stride, const uint16_t* W, int ldw, 
   a.aexp = nullptr;
   a.bexp = nullptr;
   a.beta = beta;
+  if (bf16) {
+    if (big_tiles(M, N) >= 192) return launch_x3_big<X3_REF_BF16>(a, s, who);
+    return launch_x3<128, 128, X3_REF_BF16>(a, s, who);
+  }
   if (big_tiles(M, N) >= 192) return launch_x3_big<X3_REF>(a, s, who);
   return launch_x3<128, 128, X3_REF>(a, s, who);
 }
 
-int split3_launch(const float* x, uint16_t* parts, size_t n, size_t stride, int order, hipStream_t s) {
+int split3_launch(const float* x, uint16_t* parts, size_t n, size_t stride, int order, hipStream_t s, bool bf16 = false) {
   if (n == 0) return TIERMM_OK;
   const size_t want = (n + 255) / 256;
   const unsigned grid = (unsigned)(want < 16384 ? want : 16384);
-  split3_kernel<<<grid, 256, 0, s>>>(x, parts, n, stride, order);
+  if (bf16)
+    split3_kernel<true><<<grid, 256, 0, s>>>(x, parts, n, stride, order);
+  else
+    split3_kernel<false><<<grid, 256, 0, s>>>(x, parts, n, stride, order);
   TM_LAUNCH_CHECK("split3: launch");
   return TIERMM_OK;
 }
@@ -536,6 +565,15 @@ int tiermm_split3_f16(const float* x, uint16_t* parts, size_t n, size_t part_str
   if (part_stride < n) return set_error(TIERMM_EINVAL, "tiermm_split3_f16: part_stride < n");
   if (n && (!x || !parts)) return set_error(TIERMM_EINVAL, "tiermm_split3_f16: null buffer");
   return split3_launch(x, parts, n, part_stride, order, (hipStream_t)stream);
+}
+
+int tiermm_split3_bf16(const float* x, uint16_t* parts, size_t n, size_t part_stride, int order,
+                       tiermm_stream_t stream) {
+  if (order != TIERMM_HML && order != TIERMM_LMH)
+    return set_error(TIERMM_EINVAL, "tiermm_split3_bf16: order %d", order);
+  if (part_stride < n) return set_error(TIERMM_EINVAL, "tiermm_split3_bf16: part_stride < n");
+  if (n && (!x || !parts)) return set_error(TIERMM_EINVAL, "tiermm_split3_bf16: null buffer");
+  return split3_launch(x, parts, n, part_stride, order, (hipStream_t)stream, true);
 }
 
 int tiermm_x3s_split(const float* src, uint16_t* hi, uint16_t* lo, int32_t* exps, int rows, int cols,
@@ -582,9 +620,8 @@ size_t tiermm_x3_gemm_ws_bytes(int m, int n, int k) {
   return (size_t)3 * (size_t)n * (size_t)k * sizeof(uint16_t) + (size_t)m * (size_t)k * sizeof(uint16_t);
 }
 
-int tiermm_x3_gemm(int opA, int m, int n, int k, const uint16_t* A, int lda, const float* B, float beta, float* C,
-                   int ldc, void* ws, size_t ws_bytes, tiermm_stream_t stream) {
-  const char* who = "tiermm_x3_gemm";
+static int x3_gemm_impl(int opA, int m, int n, int k, const uint16_t* A, int lda, const float* B, float beta, float* C,
+                        int ldc, void* ws, size_t ws_bytes, tiermm_stream_t stream, bool bf16, const char* who) {
   if (opA != TIERMM_OP_T && opA != TIERMM_OP_N) return set_error(TIERMM_EINVAL, "%s: opA %d", who, opA);
   int st = check_nt(who, n, m, k);
   if (st) return st;
@@ -599,7 +636,7 @@ int tiermm_x3_gemm(int opA, int m, int n, int k, const uint16_t* A, int lda, con
   if (st) return st;
   hipStream_t s = (hipStream_t)stream;
   uint16_t* parts = (uint16_t*)w;
-  st = split3_launch(B, parts, nk, nk, TIERMM_HML, s);
+  st = split3_launch(B, parts, nk, nk, TIERMM_HML, s, bf16);
   if (st) return st;
   const uint16_t* At = A;
   int ldt = lda;
@@ -614,7 +651,17 @@ int tiermm_x3_gemm(int opA, int m, int n, int k, const uint16_t* A, int lda, con
     ldt = k;
   }
   // column-major C(m x n) with ldc == row-major out[n][ldc] = x[n][k] * W[m][k]^T
-  return x3ref_nt(parts, nk, At, ldt, C, ldc, n, m, k, beta, s, who);
+  return x3ref_nt(parts, nk, At, ldt, C, ldc, n, m, k, beta, s, who, bf16);
+}
+
+int tiermm_x3_gemm(int opA, int m, int n, int k, const uint16_t* A, int lda, const float* B, float beta, float* C,
+                   int ldc, void* ws, size_t ws_bytes, tiermm_stream_t stream) {
+  return x3_gemm_impl(opA, m, n, k, A, lda, B, beta, C, ldc, ws, ws_bytes, stream, false, "tiermm_x3_gemm");
+}
+
+int tiermm_x3_gemm_bf16(int opA, int m, int n, int k, const uint16_t* A, int lda, const float* B, float beta,
+                        float* C, int ldc, void* ws, size_t ws_bytes, tiermm_stream_t stream) {
+  return x3_gemm_impl(opA, m, n, k, A, lda, B, beta, C, ldc, ws, ws_bytes, stream, true, "tiermm_x3_gemm_bf16");
 }
 
 size_t tiermm_x3_rows_ws_bytes(int M, int K, int N) {
@@ -622,9 +669,8 @@ size_t tiermm_x3_rows_ws_bytes(int M, int K, int N) {
   return (size_t)3 * (size_t)M * (size_t)K * sizeof(uint16_t);
 }
 
-int tiermm_x3_rows(const uint16_t* W, const float* x, float* y, int M, int K, int N, int ldo, void* ws,
-                   size_t ws_bytes, tiermm_stream_t stream) {
-  const char* who = "tiermm_x3_rows";
+static int x3_rows_impl(const uint16_t* W, const float* x, float* y, int M, int K, int N, int ldo, void* ws,
+                        size_t ws_bytes, tiermm_stream_t stream, bool bf16, const char* who) {
   int st = check_nt(who, M, N, K);
   if (st) return st;
   if (ldo < N) return set_error(TIERMM_EINVAL, "%s: ldo < N", who);
@@ -635,9 +681,19 @@ int tiermm_x3_rows(const uint16_t* W, const float* x, float* y, int M, int K, in
   if (st) return st;
   hipStream_t s = (hipStream_t)stream;
   const size_t mk = (size_t)M * K;
-  st = split3_launch(x, (uint16_t*)w, mk, mk, TIERMM_HML, s);
+  st = split3_launch(x, (uint16_t*)w, mk, mk, TIERMM_HML, s, bf16);
   if (st) return st;
-  return x3ref_nt((const uint16_t*)w, mk, W, K, y, ldo, M, N, K, 0.f, s, who);
+  return x3ref_nt((const uint16_t*)w, mk, W, K, y, ldo, M, N, K, 0.f, s, who, bf16);
+}
+
+int tiermm_x3_rows(const uint16_t* W, const float* x, float* y, int M, int K, int N, int ldo, void* ws,
+                   size_t ws_bytes, tiermm_stream_t stream) {
+  return x3_rows_impl(W, x, y, M, K, N, ldo, ws, ws_bytes, stream, false, "tiermm_x3_rows");
+}
+
+int tiermm_x3_rows_bf16(const uint16_t* W, const float* x, float* y, int M, int K, int N, int ldo, void* ws,
+                        size_t ws_bytes, tiermm_stream_t stream) {
+  return x3_rows_impl(W, x, y, M, K, N, ldo, ws, ws_bytes, stream, true, "tiermm_x3_rows_bf16");
 }
 
 static size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
