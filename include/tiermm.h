@@ -219,6 +219,37 @@ int tiermm_moe_combine(const float* Y_sorted, const int* token_pairs, const floa
  * threads (<= 0: all hardware threads). */
 int tiermm_quantize(int qtype, const float* x, void* out, size_t rows, int cols, int nthreads);
 
+/* ------------------------------------------------------- .tq container */
+/* A quantized base on disk (reader tq_load/tq_of, tier.cpp:273-292; writers
+ * tier.cpp:2716-2744 and quant.py:60-105): a NUL-padded text header of hb
+ * bytes -- "TQB1 <hb> <n>", "#key value" meta lines, and one line per matrix
+ * "<name> <type> <rows> <cols> <offset> <bytes> [err]" -- then the matrices at
+ * 4096-aligned offsets, rows of q_row_bytes(type, cols) bytes back to back.
+ * Host-side only; the rows a caller reads go to device memory with its own
+ * copies (see tiermm_qgemv and friends for the layout they expect). */
+typedef struct tiermm_tq tiermm_tq;
+/* Parse the header; TIERMM_EINVAL for a file that is not a .tq or a matrix
+ * line that does not parse (unknown type, columns not whole blocks, byte count
+ * other than rows * q_row_bytes).  A repeated name replaces the earlier one. */
+int tiermm_tq_open(const char* path, tiermm_tq** out);
+void tiermm_tq_close(tiermm_tq* tq);
+int tiermm_tq_count(const tiermm_tq* tq);
+/* Index of the matrix called `name`, or -1 (tq_of, tier.cpp:292). */
+int tiermm_tq_find(const tiermm_tq* tq, const char* name);
+/* Fields of matrix i (any pointer may be NULL); err is -1 when the file has none. */
+int tiermm_tq_info(const tiermm_tq* tq, int i, const char** name, int* qtype, int* rows, int* cols,
+                   uint64_t* offset, uint64_t* bytes, size_t* rb, double* err);
+int tiermm_tq_meta_count(const tiermm_tq* tq);
+int tiermm_tq_meta(const tiermm_tq* tq, int i, const char** key, const char** value);
+/* Copy rows [r0, r0 + nrows) of matrix i (nrows * rb bytes) to host memory dst. */
+int tiermm_tq_read_rows(const tiermm_tq* tq, int i, size_t r0, size_t nrows, void* dst);
+/* Write n matrices (host data, rows * q_row_bytes bytes each) and nmeta meta
+ * pairs to `path` through "<path>.part" and a rename, as the reference writers
+ * do; errs (may be NULL: "-1") are written with 6 decimals. */
+int tiermm_tq_write(const char* path, int n, const char* const* names, const int* qtypes, const int* rows,
+                    const int* cols, const void* const* data, const double* errs, int nmeta,
+                    const char* const* keys, const char* const* values);
+
 /* Type of one projection under a quantization recipe (tier.cpp:2701-2713, the
  * same rule as recipe_types in tierlm.py:1858-1874).  recipe: "Q8_0", "Q6_K",
  * "Q5_K_M", "Q5_K_S", "Q4_K_M" or "Q4_K_S"; slot 0..6 = q, k, v, o, gate, up,

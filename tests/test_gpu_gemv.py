@@ -121,3 +121,21 @@ def test_gemv_dense_rows(gpu, wtype, N, K):
     hip.synchronize()
     y = Y.download(np.float32, N)
     assert oracle.rel_fro(y, wf.astype(np.float64) @ x.astype(np.float64)) <= TOL
+
+
+def test_gemv_from_a_tq_base(gpu, tmp_path):
+    """A quantized base written to .tq, opened by name, its rows uploaded and multiplied."""
+    from tier_amd import tq
+    t, N, K = tier_amd.Q4_K, 300, 2048
+    blocks = quantized_weight(t, N, K, seed=12)
+    p = str(tmp_path / "base.tq")
+    tq.write_tq_arrays(p, [("model.layers.0.mlp.up_proj.weight", t, N, K, blocks)], {"from": "test"})
+    with tq.TqFile(p) as f:
+        i = f.find("model.layers.0.mlp.up_proj.weight")
+        e = f.entry(i)
+        rows = f.read_rows(i)
+    x = activations(1, K, seed=13)[0]
+    W, X, Y = hip.to_device(rows), hip.to_device(x), hip.DeviceBuffer(N * 4)
+    tier_amd.gemv_q(W.ptr, e["qtype"], e["rb"], X.ptr, Y.ptr, e["rows"], e["cols"])
+    hip.synchronize()
+    assert oracle.rel_fro(Y.download(np.float32, N), oracle.gemv_f64(blocks, t, x, N, K)) <= TOL

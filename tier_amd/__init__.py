@@ -48,7 +48,9 @@ EXPORTS = (
     "tiermm_x3_gemm_ws_bytes", "tiermm_x3_rows", "tiermm_x3_rows_ws_bytes", "tiermm_x3s_split",
     "tiermm_x3s_gemm", "tiermm_qgemm", "tiermm_qgemm_ws_bytes", "tiermm_quantize", "tiermm_gemv",
     "tiermm_qgemm_grouped", "tiermm_qgemm_grouped_ws_bytes", "tiermm_moe_combine", "tiermm_recipe_type",
-    "tiermm_split3_bf16", "tiermm_x3_gemm_bf16", "tiermm_x3_rows_bf16",
+    "tiermm_split3_bf16", "tiermm_x3_gemm_bf16", "tiermm_x3_rows_bf16", "tiermm_tq_open", "tiermm_tq_close",
+    "tiermm_tq_count", "tiermm_tq_find", "tiermm_tq_info", "tiermm_tq_meta_count", "tiermm_tq_meta",
+    "tiermm_tq_read_rows", "tiermm_tq_write",
 )
 
 
@@ -104,6 +106,18 @@ _sig("tiermm_recipe_type", [ctypes.c_char_p, _i, _i, _i])
 _sig("tiermm_split3_bf16", [_vp, _vp, _sz, _sz, _i, _vp])
 _sig("tiermm_x3_gemm_bf16", [_i, _i, _i, _i, _vp, _i, _vp, _f, _vp, _i, _vp, _sz, _vp])
 _sig("tiermm_x3_rows_bf16", [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp])
+_cp, _u64 = ctypes.c_char_p, ctypes.c_uint64
+_sig("tiermm_tq_open", [_cp, ctypes.POINTER(_vp)])
+_sig("tiermm_tq_close", [_vp], None)
+_sig("tiermm_tq_count", [_vp])
+_sig("tiermm_tq_find", [_vp, _cp])
+_sig("tiermm_tq_info", [_vp, _i, ctypes.POINTER(_cp), _pi, _pi, _pi, ctypes.POINTER(_u64), ctypes.POINTER(_u64),
+                        ctypes.POINTER(_sz), ctypes.POINTER(ctypes.c_double)])
+_sig("tiermm_tq_meta_count", [_vp])
+_sig("tiermm_tq_meta", [_vp, _i, ctypes.POINTER(_cp), ctypes.POINTER(_cp)])
+_sig("tiermm_tq_read_rows", [_vp, _i, _sz, _sz, _vp])
+_sig("tiermm_tq_write", [_cp, _i, ctypes.POINTER(_cp), _pi, _pi, _pi, ctypes.POINTER(_vp),
+                         ctypes.POINTER(ctypes.c_double), _i, ctypes.POINTER(_cp), ctypes.POINTER(_cp)])
 
 
 def lib():
