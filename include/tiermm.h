@@ -250,6 +250,11 @@ int tiermm_tq_write(const char* path, int n, const char* const* names, const int
                     const int* cols, const void* const* data, const double* errs, int nmeta,
                     const char* const* keys, const char* const* values);
 
+/* q_val (quant.h:59-121) on the host: out[r*cols + c] for nrows rows of rb bytes,
+ * types F32, F16, BF16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K, Q6_K (host
+ * memory; the comparison behind tier --tq-check, tier.cpp:2749-2765). */
+int tiermm_dequant_host(const void* W, int qtype, size_t rb, int cols, size_t nrows, float* out);
+
 /* Type of one projection under a quantization recipe (tier.cpp:2701-2713, the
  * same rule as recipe_types in tierlm.py:1858-1874).  recipe: "Q8_0", "Q6_K",
  * "Q5_K_M", "Q5_K_S", "Q4_K_M" or "Q4_K_S"; slot 0..6 = q, k, v, o, gate, up,

@@ -114,3 +114,80 @@ def test_python_writer_copies_from_a_source_file(tmp_path):
         assert f.read_rows(0).tobytes() == blob[1000:]
     with pytest.raises(ValueError):
         tq.write_tq(p, [("w", "Q4_K", 2, 256, (str(src), 1000, 280))], {})
+
+
+@pytest.mark.parametrize("name", ["q4_0", "q4_1", "q5_0", "q5_1", "q8_0", "q4_K", "q5_K", "q6_K"])
+def test_host_dequant_matches_reference_golden(golden, name):
+    """tiermm_dequant_host against q_val values written by the reference's quant.h (fixtures)."""
+    g = golden["dequant"]
+    blocks, want = g[f"{name}_blocks"], g[f"{name}_f32bits"]
+    t = int(g[f"{name}_type"])
+    cols = int(g["cols"])
+    got = tier_amd.dequant_host(blocks.reshape(-1, blocks.shape[-1]), t, cols)
+    assert np.array_equal(got.view(np.uint32).ravel(), want.ravel())
+
+
+def _write_safetensors(path, tensors):
+    import json
+    import struct
+    head, off, blobs = {}, 0, []
+    for name, arr in tensors.items():
+        b = arr.tobytes()
+        head[name] = {"dtype": "BF16", "shape": list(arr.shape), "data_offsets": [off, off + len(b)]}
+        off += len(b)
+        blobs.append(b)
+    h = json.dumps(head).encode()
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(h)))
+        f.write(h)
+        for b in blobs:
+            f.write(b)
+
+
+def test_tq_check_metrics(tmp_path):
+    """tier --tq-check (tier.cpp:2749-2765) on a two-matrix base: q8_0 and q4_K error levels
+    (check_quant.py:117 bounds: 0.7 %, 8 %) and correlations near 1; a matrix quantized from
+    other weights is caught (correlation near 0, result 2)."""
+    from tier_amd import tq
+    rng = np.random.default_rng(9)
+    w = {n: (rng.standard_normal(s) * 0.02).astype(np.float32) for n, s in (("a.weight", (64, 512)),
+                                                                           ("b.weight", (50, 256)))}
+    bf = {n: ((v.view(np.uint32) + 0x8000) >> 16).astype(np.uint16) for n, v in w.items()}  # bf16 source
+    model = str(tmp_path / "m.safetensors")
+    _write_safetensors(model, bf)
+    src = {n: (b.astype(np.uint32) << 16).view(np.float32) for n, b in bf.items()}
+    base = str(tmp_path / "m.tq")
+    tq.write_tq_arrays(base, [("a.weight", tier_amd.Q8_0, 64, 512, tier_amd.q_row(tier_amd.Q8_0, src["a.weight"])),
+                              ("b.weight", tier_amd.Q4_K, 50, 256, tier_amd.q_row(tier_amd.Q4_K, src["b.weight"]))])
+    lines = []
+    assert tq.check(model, base, say=lines.append) == 0
+    import re
+    errs = {m.group(1): (float(m.group(2)), float(m.group(3)))
+            for m in (re.search(r" (\S+) \S+, ошибка ([\d.]+)%, корреляция ([\d.]+)", l) for l in lines[:-1]) if m}
+    assert errs["a.weight"][0] < 0.7 and errs["a.weight"][1] > 0.9999
+    assert errs["b.weight"][0] < 8.0 and errs["b.weight"][1] > 0.99
+    m = re.search(r"ошибка весов ([\d.]+)%, худшая корреляция (-?[\d.]+) \((.*?)\)", lines[-1], re.I)
+    assert m and m.group(3) == "b.weight"
+    # a base made from other weights
+    other = (rng.standard_normal((50, 256)) * 0.02).astype(np.float32)
+    base2 = str(tmp_path / "o.tq")
+    tq.write_tq_arrays(base2, [("b.weight", tier_amd.Q4_K, 50, 256, tier_amd.q_row(tier_amd.Q4_K, other))])
+    lines = []
+    assert tq.check(model, base2, say=lines.append) == 2
+    assert "обнаружены" in lines[-1]
+    # a matrix the model does not have
+    base3 = str(tmp_path / "x.tq")
+    tq.write_tq_arrays(base3, [("c.weight", tier_amd.Q4_K, 50, 256, tier_amd.q_row(tier_amd.Q4_K, other))])
+    assert tq.check(model, base3, say=lambda s: None) == 2
+
+
+@pytest.mark.parametrize("t", [tier_amd.Q8_0, tier_amd.Q5_0, tier_amd.Q4_K, tier_amd.Q5_K, tier_amd.Q6_K])
+def test_host_dequant_matches_oracle_on_random_blocks(t):
+    import oracle
+    rng = np.random.default_rng(100 + t)
+    be, _ = oracle.block(t)
+    K = 1024
+    blocks = oracle.random_blocks(rng, t, 16 * (K // be)).reshape(16, -1)
+    got = tier_amd.dequant_host(blocks, t, K)
+    want = oracle.dequant(blocks, t, K, oracle.OUT_F32).reshape(16, K)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))

@@ -50,7 +50,7 @@ EXPORTS = (
     "tiermm_qgemm_grouped", "tiermm_qgemm_grouped_ws_bytes", "tiermm_moe_combine", "tiermm_recipe_type",
     "tiermm_split3_bf16", "tiermm_x3_gemm_bf16", "tiermm_x3_rows_bf16", "tiermm_tq_open", "tiermm_tq_close",
     "tiermm_tq_count", "tiermm_tq_find", "tiermm_tq_info", "tiermm_tq_meta_count", "tiermm_tq_meta",
-    "tiermm_tq_read_rows", "tiermm_tq_write",
+    "tiermm_tq_read_rows", "tiermm_tq_write", "tiermm_dequant_host",
 )
 
 
@@ -116,6 +116,7 @@ _sig("tiermm_tq_info", [_vp, _i, ctypes.POINTER(_cp), _pi, _pi, _pi, ctypes.POIN
 _sig("tiermm_tq_meta_count", [_vp])
 _sig("tiermm_tq_meta", [_vp, _i, ctypes.POINTER(_cp), ctypes.POINTER(_cp)])
 _sig("tiermm_tq_read_rows", [_vp, _i, _sz, _sz, _vp])
+_sig("tiermm_dequant_host", [_vp, _i, _sz, _i, _sz, _vp])
 _sig("tiermm_tq_write", [_cp, _i, ctypes.POINTER(_cp), _pi, _pi, _pi, ctypes.POINTER(_vp),
                          ctypes.POINTER(ctypes.c_double), _i, ctypes.POINTER(_cp), ctypes.POINTER(_cp)])
 
@@ -310,6 +311,16 @@ def recipe_types(rec: str, mats) -> list[str]:
         if t < 0 or t == EINVAL:
             raise TiermmError(t, last_error())
         out.append(TYPE_NAMES[t])
+    return out
+
+
+def dequant_host(blocks: np.ndarray, qtype: int, cols: int) -> np.ndarray:
+    """q_val of every element of host rows (quant.h:59-121), fp32 [rows][cols]."""
+    b = np.ascontiguousarray(blocks, np.uint8)
+    rows = b.shape[0] if b.ndim == 2 else 1
+    rb = q_row_bytes(qtype, cols)
+    out = np.empty((rows, cols), np.float32)
+    _check(_L.tiermm_dequant_host(b.ctypes.data_as(_vp), qtype, rb, cols, rows, out.ctypes.data_as(_vp)))
     return out
 
 

@@ -19,11 +19,14 @@ import re
 
 import numpy as np
 
-from . import _L, _check, TYPE_NAMES, q_info
+from . import _L, _check, q_info
 
 # block geometry by type name (quant.h:26-30)
 _TYPES = {"F32": 0, "F16": 1, "BF16": 30, "Q4_0": 2, "Q4_1": 3, "Q5_0": 6, "Q5_1": 7, "Q8_0": 8, "Q2_K": 10,
           "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
+
+
+_NAMES = {v: k for k, v in _TYPES.items()}
 
 
 def _geometry(ty: str):
@@ -141,7 +144,7 @@ class TqFile:
         off, size, rb, err = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_size_t(), ctypes.c_double()
         _check(_L.tiermm_tq_info(self._h, i, ctypes.byref(nm), ctypes.byref(qt), ctypes.byref(rows), ctypes.byref(cols),
                                  ctypes.byref(off), ctypes.byref(size), ctypes.byref(rb), ctypes.byref(err)))
-        return {"name": nm.value.decode(), "qtype": qt.value, "type": TYPE_NAMES.get(qt.value, str(qt.value)),
+        return {"name": nm.value.decode(), "qtype": qt.value, "type": _NAMES.get(qt.value, str(qt.value)),
                 "rows": rows.value, "cols": cols.value, "offset": off.value, "bytes": size.value, "rb": rb.value,
                 "err": err.value}
 
@@ -177,3 +180,66 @@ def write_tq_arrays(out: str, mats, meta: dict | None = None, errs=None) -> None
     keys = (ctypes.c_char_p * max(1, len(meta)))(*[k.encode() for k in meta])
     vals = (ctypes.c_char_p * max(1, len(meta)))(*[str(v).encode() for v in meta.values()])
     _check(_L.tiermm_tq_write(out.encode(), n, names, qt, rows, cols, data, e, len(meta), keys, vals))
+
+
+def _safetensors_index(path: str) -> tuple[dict, int]:
+    """Tensor table of a safetensors file: {name: (dtype, shape, begin, end)}, data start."""
+    import json
+    import struct
+    with open(path, "rb") as f:
+        n = struct.unpack("<Q", f.read(8))[0]
+        head = json.loads(f.read(n))
+    tab = {k: (v["dtype"], tuple(v["shape"]), v["data_offsets"][0], v["data_offsets"][1])
+           for k, v in head.items() if k != "__metadata__"}
+    return tab, 8 + n
+
+
+def check(model: str, base: str, say=print) -> int:
+    """tier --tq-check (tier.cpp:2749-2765): for every matrix of the base (by name order),
+    up to 48 rows spread evenly over the matrix are dequantized (q_val) and compared with the
+    bf16 source tensor: relative error and correlation per matrix, then the total error and
+    the worst correlation.  Returns 2 when a matrix is missing from the model, has another
+    shape, or correlates below 0.5 (a base of another model), else 0.  The last line keeps
+    the engine's wording, which quant.py's check (quant.py:337-358) parses."""
+    from . import dequant_host
+    tab, data0 = _safetensors_index(model)
+    SE = SS = 0.0
+    worst, wname, bad = 1.0, "", 0
+    with TqFile(base) as f, open(model, "rb") as src:
+        entries = sorted((f.entry(i) for i in range(len(f))), key=lambda e: e["name"].encode())
+        for k, e in enumerate(entries, 1):
+            t = tab.get(e["name"])
+            cols_ok = t is not None and (len(t[1]) < 2 or t[1][-1] == e["cols"])
+            if t is None or t[3] - t[2] != e["rows"] * e["cols"] * 2 or not cols_ok:
+                say(f"Сверка {k}/{len(entries)} {e['name']}: в модели нет такой матрицы или у неё другая форма.")
+                bad += 1
+                continue
+            S = min(e["rows"], 48)
+            rows = [j * (e["rows"] - 1) // max(1, S - 1) for j in range(S)]
+            se = ss = sx = sy = sxy = sxx = syy = 0.0
+            n = 0
+            i = f.find(e["name"])
+            for r in rows:
+                src.seek(data0 + t[2] + r * e["cols"] * 2)
+                raw = np.frombuffer(src.read(e["cols"] * 2), np.uint16)
+                x = (raw.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+                y = dequant_host(f.read_rows(i, r, 1), e["qtype"], e["cols"])[0].astype(np.float64)
+                d = y - x
+                se += float(d @ d); ss += float(x @ x); sx += float(x.sum()); sy += float(y.sum())
+                sxy += float(x @ y); sxx += float(x @ x); syy += float(y @ y)
+                n += x.size
+            cov, vx, vy = sxy - sx * sy / n, sxx - sx * sx / n, syy - sy * sy / n
+            cr = cov / (vx * vy) ** 0.5 if vx > 0 and vy > 0 else 0.0
+            er = (se / ss) ** 0.5 if ss > 0 else 0.0
+            SE += se
+            SS += ss
+            if cr < worst:
+                worst, wname = cr, e["name"]
+            if cr < 0.5:
+                bad += 1
+            say(f"Сверка {k}/{len(entries)} {e['name']} {e['type']}, ошибка {100 * er:.2f}%, "
+                f"корреляция {cr:.4f}")
+    total = 100 * (SE / SS) ** 0.5 if SS > 0 else 0.0
+    say(f"Итог: ошибка весов {total:.2f}%, худшая корреляция {worst:.4f} ({wname})"
+        f"{', обнаружены матрицы от другой модели' if bad else ''}")
+    return 2 if bad else 0
