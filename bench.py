@@ -15,8 +15,10 @@ out).
 
 Secondary measurements in the same JSON line (``secondary``): the other config
 shapes at M=1, q8_0 4096x4096 (config 1), the fused-path quantized GEMM at
-M=512 (config 3, TFLOPS against fp16 peak/3) and the x3-2x2 GEMM at M=4096
-(config 2).
+M=512 (config 3, TFLOPS against fp16 peak/3), the x3-2x2 GEMM at M=4096
+(config 2), the seven projections of a decoder layer (config 4), the routed MoE
+experts (config 5), and the chat linears of four config-4 layers streamed from
+pinned host memory against the host-to-device copy rate.
 
 ``cpu_baseline``: the reference's own q_val GEMV (oracle/_ref, compiled from
 quant.h) on the host's threads, on the same weight (timed over a bounded number
@@ -25,6 +27,7 @@ of repetitions).
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -93,9 +96,19 @@ def time_launches(hip, stream, launch, steps: int, warmup: int) -> float:
     return per
 
 
+_QCACHE = {}
+
+
 def _quantized(tier_amd, qtype, N, K, seed):
     """W ~N(0,0.02) through the host quantizer; q5_0 (no quantizer in the reference) as
     random 5-bit values with fp16 d ~ N(0, 0.004), the scale such W would get."""
+    key = (qtype, N, K, seed)
+    if key not in _QCACHE:
+        _QCACHE[key] = _quantize(tier_amd, qtype, N, K, seed)
+    return _QCACHE[key]
+
+
+def _quantize(tier_amd, qtype, N, K, seed):
     rng = np.random.default_rng(seed)
     if qtype == tier_amd.Q5_0:
         nb = K // 32
@@ -135,6 +148,90 @@ def bench_decoder_layer(tier_amd, hip, stream):
     tf = total_flop / (total_us * 1e-6) / 1e12
     return {"recipe": "q4_K_S (v, down q5_K)", "T": T, "total_us": round(total_us, 1),
             "TFLOPS": round(tf, 1), "frac_x3_peak": round(tf / X3_PEAK_TFLOPS, 4), "per_matrix": out}
+
+
+def bench_chat_stream(tier_amd, hip, stream, layers=4):
+    """chat_lin with weight streaming (tier.cpp:2283-2285, 2351-2378): the 28 linears of
+    `layers` config-4 decoder layers (q4_K_S, 155.6 MiB each) with every matrix streamed from
+    pinned host memory through 2 device slots, against the same set resident, at M=1 (decode)
+    and M=4096 (prefill, MODE_X3REF).  The roof of the streamed decode pass is the
+    host-to-device copy rate, measured here as the same 28 copies back to back without
+    compute.  Every figure is taken after warm-up passes (the first DMA reads of fresh
+    pinned pages and a new copy queue run up to 35 % slower) and is the median over
+    passes timed one at a time with a synchronisation after each, as the engine's token
+    loop reads the logits back after every pass.  (Passes queued back to back without a
+    synchronisation stream at ~44 GB/s: the copy queue falls behind by ~80 us per copy.)"""
+    H, Q, KV, F = 5120, 4096, 1024, 14336
+    shapes = ((tier_amd.Q4_K, Q, H), (tier_amd.Q4_K, KV, H), (tier_amd.Q5_K, KV, H), (tier_amd.Q4_K, H, Q),
+              (tier_amd.Q4_K, F, H), (tier_amd.Q4_K, F, H), (tier_amd.Q5_K, H, F))
+    log("bench: chat streaming: host rows")
+    host = []
+    for i, (qt, N, K) in enumerate(shapes):
+        rows = _quantized(tier_amd, qt, N, K, 11 + i)
+        h = tier_amd.HostRows(rows.nbytes)
+        h.array()[:] = rows.ravel()
+        host.append(h)
+    layer_bytes = sum(h.nbytes for h in host)
+    big = max(h.nbytes for h in host)
+    D = [hip.DeviceBuffer(big) for _ in range(2)]
+    t0, t1 = hip.Event(), hip.Event()
+
+    def copies():  # the pass's 28 copies back to back, no compute between them
+        for i in range(7 * layers):
+            h = host[i % 7]
+            hip.check(hip.lib().hipMemcpyAsync(ctypes.c_void_p(D[i % 2].ptr), ctypes.c_void_p(h.ptr),
+                                               ctypes.c_size_t(h.nbytes), hip.H2D, ctypes.c_void_p(stream.handle)),
+                      "hipMemcpyAsync")
+    copies()  # first DMA touches of the pinned pages run slower
+    stream.synchronize()
+    per = []
+    for _ in range(7):  # one pass of copies per step, synchronised, as the passes below
+        t0.record(stream)
+        copies()
+        t1.record(stream)
+        t1.synchronize()
+        per.append(t0.elapsed_ms(t1))
+    h2d = layers * layer_bytes / (float(np.median(per)) * 1e-3) / 1e9
+    for d in D:
+        d.free()
+    T = 4096
+    rng = np.random.default_rng(12)
+    X = {K: hip.to_device(rng.standard_normal((T, K), dtype=np.float32)) for K in (H, Q, F)}
+    Y = hip.DeviceBuffer(T * F * 4)
+    out = {"layers": layers, "matrices": 7 * layers, "bytes_per_pass": layers * layer_bytes,
+           "h2d_GBps": round(h2d, 1)}
+    for placement, budget, nslots in (("streamed", 0, 2), ("streamed_4slots", 0, 4), ("resident", None, 2)):
+        c = tier_amd.Chat(nslots, stream)
+        ids = [c.add(qt, N, K, host=host[j].ptr) for _ in range(layers) for j, (qt, N, K) in enumerate(shapes)]
+        c.place(budget=budget, reserve=0)
+        for M, passes in ((1, 9), (T, 3)):
+            log(f"bench: chat {placement} M={M}")
+
+            def one_pass():
+                for i, idx in enumerate(ids):
+                    qt, N, K = shapes[i % 7]
+                    c.lin(idx, X[K].ptr, Y.ptr, M, tier_amd.MODE_X3REF)
+            for _ in range(3):  # the first passes over fresh host rows and a new copy queue run slower
+                one_pass()
+            stream.synchronize()
+            per = []
+            for _ in range(passes):  # one pass per step, synchronised, as the engine's token loop is
+                t0.record(stream)
+                one_pass()
+                t1.record(stream)
+                t1.synchronize()
+                per.append(t0.elapsed_ms(t1))
+            ms = float(np.median(per))
+            key = f"{placement}_m{M}"
+            out[key] = {"ms_per_pass": round(ms, 3), "GBps": round(layers * layer_bytes / (ms * 1e-3) / 1e9, 1)}
+            if placement.startswith("streamed"):
+                out[key]["frac_h2d"] = round(out[key]["GBps"] / h2d, 3)
+        c.close()
+    t0.destroy()
+    t1.destroy()
+    for h in host:
+        h.free()
+    return out
 
 
 def bench_moe(tier_amd, hip, stream):
@@ -305,6 +402,7 @@ def main() -> int:
         del bufs, Wf, Xf
         secondary["decoder_layer_t4096"] = bench_decoder_layer(tier_amd, hip, stream)
         secondary["moe_t4096"] = bench_moe(tier_amd, hip, stream)
+        secondary["chat_streamed_4_layers"] = bench_chat_stream(tier_amd, hip, stream)
 
     traffic, traffic_src = measured_traffic()
     cpu = None

@@ -52,7 +52,10 @@ enum {
 enum {
   TIERMM_F32 = 0,
   TIERMM_F16 = 1,
+  TIERMM_Q4_0 = 2,
+  TIERMM_Q4_1 = 3,
   TIERMM_Q5_0 = 6,
+  TIERMM_Q5_1 = 7,
   TIERMM_Q8_0 = 8,
   TIERMM_Q4_K = 12,
   TIERMM_Q5_K = 13,
@@ -97,15 +100,17 @@ int tiermm_q_row_bytes(int qtype, int cols, size_t* rb);
 /* dq_k<T> / dq_launch (tier.cpp:293-298): for i < nrows*cols,
  * out[i] = T(q_val(W + (r0 + i/cols)*rb, qtype, i%cols)), T = fp32, fp16
  * (round to nearest even, subnormals kept, as tier_fp16) or bf16 (RNE, as
- * hip_bfloat16).  qtype in {Q8_0, Q5_0, Q4_K, Q5_K, Q6_K}.  Bit-exact with
- * the reference's q_val for finite block scales. */
+ * hip_bfloat16).  qtype in {F32, F16, BF16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q4_K,
+ * Q5_K, Q6_K}, cols a multiple of 8 and of the block.
+ * Bit-exact with the reference's q_val for finite block scales. */
 int tiermm_dequant(const void* W, int qtype, size_t rb, int cols, size_t r0, size_t nrows,
                    void* out, int out_dtype, tiermm_stream_t stream);
 
 /* --------------------------------------------------------------- decode GEMV */
 /* gemv_q (tier.cpp:299-306, launched at 2357): y[r] = sum_k q_val(W_r, k) * x[k]
  * for r < N, fp32 accumulation.  W: N rows of rb bytes; x: K fp32; y: N fp32.
- * qtype in {Q8_0, Q5_0, Q4_K, Q5_K, Q6_K}. */
+ * qtype: the GPU types of tiermm_dequant; dense rows (F32/F16/BF16) go to
+ * tiermm_gemv's kernel and must start 16-byte aligned. */
 int tiermm_qgemv(const void* W, int qtype, size_t rb, const float* x, float* y, int N, int K,
                  tiermm_stream_t stream);
 
@@ -183,8 +188,8 @@ int tiermm_x3s_gemm(const uint16_t* Xhi, const uint16_t* Xlo, const int32_t* xex
  * parts (fp3gemm semantics, tier.cpp:922): rel. Frobenius error <= 2^-20
  * against fp64(fp16deq(W) * X).  mode TIERMM_MODE_F32: the chat prefill
  * semantics (fp32 dequant, then an fp32 GEMM, tier.cpp:2358-2359): rel.
- * Frobenius error <= 2^-20 against fp64(deq(W) * X).  qtype in {Q8_0, Q5_0,
- * Q4_K, Q5_K, Q6_K}. */
+ * Frobenius error <= 2^-20 against fp64(deq(W) * X).  qtype: the GPU types of
+ * tiermm_dequant. */
 int tiermm_qgemm(const void* W, int qtype, size_t rb, const float* X, float* Y, int M, int N,
                  int K, int ldy, int mode, float beta, void* ws, size_t ws_bytes,
                  tiermm_stream_t stream);
@@ -263,6 +268,54 @@ int tiermm_dequant_host(const void* W, int qtype, size_t rb, int cols, size_t nr
  * number of layers (ignored for other slots).  Returns the type id, or
  * TIERMM_EINVAL for an unknown recipe. */
 int tiermm_recipe_type(const char* recipe, int slot, int index, int count);
+
+/* ------------------------------------------ chat linears with weight streaming */
+/* The chat engine's per-linear dispatch, chat_lin (tier.cpp:2351-2378), and its
+ * double-buffered weight streaming (g_chat_SQ / chat_slot / chat_issue,
+ * tier.cpp:2283-2285; placement tier.cpp:2549-2555).  A set holds the
+ * matrices of a model's linears.  Each is resident in device memory or
+ * streamed from pinned host memory through `nslots` device slots on a copy
+ * stream of its own, overlapped with compute on the set's compute stream.
+ * Streamed matrices must be used in registration order, cyclically (the
+ * engine's layer order); a use out of that order is refused (TIERMM_EINVAL)
+ * and tiermm_chat_restart(c, 1) rewinds.  A set is used from one host thread
+ * with the device it was created on current. */
+typedef struct tiermm_chat tiermm_chat;
+/* New set; nslots in 2..8 (the engine uses 2), compute_stream as chat_lin's g_chat_cs. */
+int tiermm_chat_create(int nslots, tiermm_stream_t compute_stream, tiermm_chat** out);
+/* Waits for the set's work, frees what it allocated (not the caller's rows). */
+void tiermm_chat_destroy(tiermm_chat* c);
+/* Register a matrix (rows x cols of qtype, row bytes rb) before tiermm_chat_place.
+ * dev != NULL: resident in the caller's device memory (16-byte aligned).
+ * dev == NULL: host rows, placed by tiermm_chat_place (pinned when streamed).
+ * *id is its handle for tiermm_chat_lin.  qtype: the GPU types of tiermm_dequant. */
+int tiermm_chat_add(tiermm_chat* c, int qtype, size_t rb, int rows, int cols, const void* host, void* dev, int* id);
+/* Placement (tier.cpp:2549-2555): in registration order a matrix is copied to
+ * device memory while (resident bytes + its bytes) <= budget and
+ * (resident bytes + its bytes + reserve) < free memory less the slots; after
+ * the first that is not, every later one is streamed.  Allocates the slots and
+ * issues their first copies (tier.cpp:2569).  On failure the set is as before. */
+int tiermm_chat_place(tiermm_chat* c, size_t budget, size_t reserve, size_t* resident_bytes,
+                      size_t* streamed_bytes);
+/* chat_lin: y[M][rows] = x[M][cols] * W^T on the compute stream.  M == 1:
+ * gemv_q / gemv<T> (tiermm_qgemv, tiermm_gemv); M > 1: quantized rows through
+ * tiermm_qgemm(mode), fp16 / bf16 rows through tiermm_x3_rows(_bf16) when
+ * mode is TIERMM_MODE_X3REF (chat_fp3 / chat_bf3) and else, as fp32 rows always,
+ * through tiermm_qgemm(TIERMM_MODE_F32) (the engine's expand + SGEMM).  x, y:
+ * device fp32, x 16-byte aligned.  A streamed matrix waits for its copy and
+ * then refills its slot with the use nslots ahead (tier.cpp:2377). */
+int tiermm_chat_lin(tiermm_chat* c, int id, const float* x, float* y, int M, int mode);
+/* After the host rows of streamed matrices changed (or to rewind the cyclic
+ * order, rewind != 0): wait for the set's streams and issue the pending copies
+ * again (the engine's chat_issue(qi), chat_issue(qi+1), tier.cpp:2666-2676). */
+int tiermm_chat_restart(tiermm_chat* c, int rewind);
+/* *streamed: 1 if matrix id is streamed, 0 if resident (-1 for id < 0); the
+ * set's resident and streamed bytes and the streamed uses so far. */
+int tiermm_chat_info(const tiermm_chat* c, int id, int* streamed, size_t* resident_bytes, size_t* streamed_bytes,
+                     long long* uses);
+/* Pinned host memory for streamed rows (hipHostMalloc). */
+int tiermm_host_alloc(size_t bytes, void** out);
+int tiermm_host_free(void* p);
 
 #ifdef __cplusplus
 }

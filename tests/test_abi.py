@@ -105,6 +105,24 @@ def test_argument_checks_return_before_device_work():
     assert "part_stride" in tier_amd.last_error()
     # chat_fp3 mirror: unsupported shape -> False, not an exception
     assert tier_amd.chat_fp3(16, 16, 16, 4, 48, 4, 4) is False
+    # legacy 32-blocks and dense rows are GPU types now; dense rows decode 8 columns at a time
+    assert L.tiermm_dequant(16, tier_amd.Q4_1, 19, 32, 0, 1, 16, tier_amd.OUT_F16, None) == tier_amd.EINVAL
+    assert L.tiermm_dequant(16, tier_amd.F16, 24, 12, 0, 1, 16, tier_amd.OUT_F16, None) == tier_amd.UNSUPPORTED
+    assert L.tiermm_qgemv(18, tier_amd.F16, 128, 16, 16, 1, 64, None) == tier_amd.EINVAL  # dense rows 16-aligned
+    # chat set: slot count, null handles, registration checks (no HIP call on these paths)
+    out = ctypes.c_void_p()
+    assert L.tiermm_chat_create(1, None, ctypes.byref(out)) == tier_amd.EINVAL and not out.value
+    assert L.tiermm_chat_create(9, None, ctypes.byref(out)) == tier_amd.EINVAL
+    assert L.tiermm_chat_create(2, None, None) == tier_amd.EINVAL
+    i = ctypes.c_int()
+    assert L.tiermm_chat_add(None, tier_amd.Q4_K, 144, 1, 256, 16, None, ctypes.byref(i)) == tier_amd.EINVAL
+    assert L.tiermm_chat_place(None, 0, 0, None, None) == tier_amd.EINVAL
+    assert L.tiermm_chat_lin(None, 0, 16, 16, 1, 0) == tier_amd.EINVAL
+    assert L.tiermm_chat_restart(None, 0) == tier_amd.EINVAL
+    assert L.tiermm_chat_info(None, 0, None, None, None, None) == tier_amd.EINVAL
+    L.tiermm_chat_destroy(None)
+    assert L.tiermm_host_free(None) == tier_amd.OK
+    assert L.tiermm_host_alloc(16, None) == tier_amd.EINVAL
 
 
 def test_workspace_sizes():

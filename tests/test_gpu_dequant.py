@@ -98,3 +98,50 @@ def test_dequant_full_layer_shape(gpu):
     rows = np.concatenate([rows, [0, N - 1]])
     for r in rows:
         assert np.array_equal(got[r], _expect(blocks[r:r + 1], t, K, tier_amd.OUT_F16)), r
+
+
+MORE = {"q4_0": tier_amd.Q4_0, "q4_1": tier_amd.Q4_1, "q5_1": tier_amd.Q5_1}
+
+
+@pytest.mark.parametrize("name", list(MORE))
+@pytest.mark.parametrize("outname", list(OUTS))
+def test_dequant_golden_blocks_legacy_types(gpu, golden, name, outname):
+    """Q4_0 / Q4_1 / Q5_1 (quant.h:64-67) against the reference's own values and the oracle."""
+    t, out = MORE[name], OUTS[outname][0]
+    blocks = golden["dequant"][f"{name}_blocks"]
+    got = _run(gpu, blocks, t, 512, out)
+    want = _expect(blocks, t, 512, out)
+    if out == tier_amd.OUT_F32:
+        assert np.array_equal(want, golden["dequant"][f"{name}_f32bits"].ravel())
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("name", list(MORE))
+def test_dequant_legacy_types_random_rows(gpu, name):
+    """Random blocks (fp16 scales and minimums ~N(0,0.02)), a row window, every output type."""
+    t = MORE[name]
+    rng = np.random.default_rng(50 + t)
+    K = 1024
+    blocks = oracle.random_blocks(rng, t, 37 * K // 32)
+    for out in OUTS.values():
+        got = _run(gpu, blocks, t, K, out[0], r0=5, nrows=31)
+        assert np.array_equal(got, _expect(blocks, t, K, out[0], 5, 31))
+
+
+@pytest.mark.parametrize("t", [tier_amd.F32, tier_amd.F16, tier_amd.BF16])
+def test_dequant_dense_rows(gpu, t):
+    """q_val's F32 / F16 / BF16 cases (quant.h:61-63): conversions of stored rows, incl. fp16 subnormals."""
+    rng = np.random.default_rng(60 + t)
+    K, N = 264, 9
+    w = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
+    w[0, :8] = [0.0, -0.0, 2.0 ** -24, -(2.0 ** -20), 65504.0, -65504.0, 1e-30, 1.5e4]
+    if t == tier_amd.F32:
+        blocks = w.view(np.uint8)
+    elif t == tier_amd.F16:
+        blocks = w.astype(np.float16).view(np.uint8)
+    else:
+        blocks = oracle.f2bf(w).view(np.uint8)
+    blocks = np.ascontiguousarray(blocks).reshape(N, -1)
+    for out in OUTS.values():
+        got = _run(gpu, blocks, t, K, out[0])
+        assert np.array_equal(got, _expect(blocks, t, K, out[0]))

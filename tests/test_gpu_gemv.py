@@ -51,7 +51,8 @@ def test_gemv_config_shapes(gpu, name, t, N, K):
     assert oracle.rel_fro(y, want) <= TOL
 
 
-@pytest.mark.parametrize("t", [tier_amd.Q8_0, tier_amd.Q5_0, tier_amd.Q4_K, tier_amd.Q5_K, tier_amd.Q6_K])
+@pytest.mark.parametrize("t", [tier_amd.Q8_0, tier_amd.Q5_0, tier_amd.Q4_K, tier_amd.Q5_K, tier_amd.Q6_K,
+                               tier_amd.Q4_0, tier_amd.Q4_1, tier_amd.Q5_1])
 @pytest.mark.parametrize("N,K", [(1, 256), (13, 512), (7, 768), (65, 2304)])
 def test_gemv_ragged_shapes(gpu, t, N, K):
     """Row counts that do not fill a wave or a block; one super-block rows; K not a multiple of 512."""
@@ -121,6 +122,24 @@ def test_gemv_dense_rows(gpu, wtype, N, K):
     hip.synchronize()
     y = Y.download(np.float32, N)
     assert oracle.rel_fro(y, wf.astype(np.float64) @ x.astype(np.float64)) <= TOL
+
+
+@pytest.mark.parametrize("wtype", [tier_amd.F32, tier_amd.F16, tier_amd.BF16])
+def test_gemv_q_on_dense_rows(gpu, wtype):
+    """gemv_q over q_val's dense cases takes the dense-row kernel: the same bits as tiermm_gemv."""
+    rng = np.random.default_rng(70 + wtype)
+    N, K = 77, 1032
+    w = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
+    bits = {tier_amd.F32: w, tier_amd.F16: oracle.f2h(w), tier_amd.BF16: oracle.f2bf(w)}[wtype].reshape(N, K)
+    x = rng.standard_normal(K).astype(np.float32)
+    W, X, Y1, Y2 = hip.to_device(bits), hip.to_device(x), hip.DeviceBuffer(N * 4), hip.DeviceBuffer(N * 4)
+    tier_amd.gemv_q(W.ptr, wtype, tier_amd.q_row_bytes(wtype, K), X.ptr, Y1.ptr, N, K)
+    tier_amd.gemv(W.ptr, wtype, X.ptr, Y2.ptr, N, K)
+    hip.synchronize()
+    y1, y2 = Y1.download(np.float32, N), Y2.download(np.float32, N)
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+    wf = oracle.dequant(np.ascontiguousarray(bits).view(np.uint8).reshape(N, -1), wtype, K)
+    assert oracle.rel_fro(y1, wf.reshape(N, K).astype(np.float64) @ x.astype(np.float64)) <= TOL
 
 
 def test_gemv_from_a_tq_base(gpu, tmp_path):

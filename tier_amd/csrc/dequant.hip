@@ -1,4 +1,5 @@
-// dequant.hip -- tiermm_dequant: quantized rows -> fp32 / fp16 / bf16 (dq_k<T>, tier.cpp:293-298).
+// dequant.hip -- tiermm_dequant: quantized or dense rows -> fp32 / fp16 / bf16 (dq_k<T>,
+// tier.cpp:293-298).
 //
 // One thread decodes 8 consecutive outputs of a row and writes them with one
 // 16-byte store (fp16/bf16) or two (fp32): the kernel is bound by the output
@@ -56,15 +57,24 @@ int launch_dequant(const void* W, size_t rb, int cols, size_t r0, size_t nrows, 
 
 // Shared argument checks for a quantized weight: type handled, rb consistent,
 // alignment of the row bytes the decoders assume.
+bool gpu_type(int qtype) {
+  switch (qtype) {
+    case QT_F32: case QT_F16: case QT_BF16: case QT_Q4_0: case QT_Q4_1: case QT_Q5_0: case QT_Q5_1:
+    case QT_Q8_0: case QT_Q4_K: case QT_Q5_K: case QT_Q6_K: return true;
+    default: return false;
+  }
+}
+
 int check_qweight(const char* who, const void* W, int qtype, size_t rb, int cols) {
   const BlockInfo* bi = block_info(qtype);
-  if (!bi || (qtype != QT_Q8_0 && qtype != QT_Q5_0 && qtype != QT_Q4_K && qtype != QT_Q5_K && qtype != QT_Q6_K))
-    return set_error(TIERMM_UNSUPPORTED, "%s: type %d is not handled on the GPU", who, qtype);
-  if (cols <= 0 || cols % bi->elems)
-    return set_error(TIERMM_UNSUPPORTED, "%s: %d columns are not whole %s blocks", who, cols, bi->name);
+  if (!bi || !gpu_type(qtype)) return set_error(TIERMM_UNSUPPORTED, "%s: type %d is not handled on the GPU", who, qtype);
+  // the kernels decode 8 consecutive elements of one row at a time
+  const int whole = bi->elems > 8 ? bi->elems : 8;
+  if (cols <= 0 || cols % whole)
+    return set_error(TIERMM_UNSUPPORTED, "%s: %d columns are not whole %s blocks of %d", who, cols, bi->name, whole);
   if (rb != (size_t)cols / bi->elems * bi->bytes)
     return set_error(TIERMM_EINVAL, "%s: rb %zu does not match %d %s columns", who, rb, cols, bi->name);
-  const size_t align = (qtype == QT_Q4_K || qtype == QT_Q5_K) ? 16 : 2;
+  const size_t align = (qtype == QT_Q4_K || qtype == QT_Q5_K) ? 16 : qtype == QT_F32 ? 4 : 2;
   if (!W || ((uintptr_t)W % align) || (rb % align))
     return set_error(TIERMM_EINVAL, "%s: weight rows must be %zu-byte aligned", who, align);
   return TIERMM_OK;
@@ -72,13 +82,9 @@ int check_qweight(const char* who, const void* W, int qtype, size_t rb, int cols
 
 // Whole rows to fp16 for the quantized GEMM (dq_launch<tier_fp16>, tier.cpp:515).
 int dequant_f16_rows(const void* W, int qtype, size_t rb, int cols, size_t nrows, uint16_t* out, hipStream_t s) {
-  switch (qtype) {
-    case QT_Q8_0: return launch_dequant<QT_Q8_0>(W, rb, cols, 0, nrows, out, TIERMM_OUT_F16, s);
-    case QT_Q5_0: return launch_dequant<QT_Q5_0>(W, rb, cols, 0, nrows, out, TIERMM_OUT_F16, s);
-    case QT_Q4_K: return launch_dequant<QT_Q4_K>(W, rb, cols, 0, nrows, out, TIERMM_OUT_F16, s);
-    case QT_Q5_K: return launch_dequant<QT_Q5_K>(W, rb, cols, 0, nrows, out, TIERMM_OUT_F16, s);
-    default: return launch_dequant<QT_Q6_K>(W, rb, cols, 0, nrows, out, TIERMM_OUT_F16, s);
-  }
+  return with_qtype(qtype, [&](auto qt) {
+    return launch_dequant<decltype(qt)::value>(W, rb, cols, 0, nrows, out, TIERMM_OUT_F16, s);
+  });
 }
 
 }  // namespace tiermm
@@ -94,11 +100,7 @@ extern "C" int tiermm_dequant(const void* W, int qtype, size_t rb, int cols, siz
   if (nrows && (!out || ((uintptr_t)out % 16)))
     return set_error(TIERMM_EINVAL, "tiermm_dequant: output must be 16-byte aligned");
   hipStream_t s = (hipStream_t)stream;
-  switch (qtype) {
-    case QT_Q8_0: return launch_dequant<QT_Q8_0>(W, rb, cols, r0, nrows, out, out_dtype, s);
-    case QT_Q5_0: return launch_dequant<QT_Q5_0>(W, rb, cols, r0, nrows, out, out_dtype, s);
-    case QT_Q4_K: return launch_dequant<QT_Q4_K>(W, rb, cols, r0, nrows, out, out_dtype, s);
-    case QT_Q5_K: return launch_dequant<QT_Q5_K>(W, rb, cols, r0, nrows, out, out_dtype, s);
-    default: return launch_dequant<QT_Q6_K>(W, rb, cols, r0, nrows, out, out_dtype, s);
-  }
+  return with_qtype(qtype, [&](auto qt) {
+    return launch_dequant<decltype(qt)::value>(W, rb, cols, r0, nrows, out, out_dtype, s);
+  });
 }

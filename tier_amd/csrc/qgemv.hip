@@ -169,13 +169,15 @@ constexpr int kQ4kMaxK = 14336;  // equals the limit in qgemv_q4k.hip
 
 int qgemv_dispatch(const void* W, int qtype, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
   switch (qtype) {
-    case QT_Q8_0: return launch_generic<QT_Q8_0>(W, rb, x, y, N, K, s);
-    case QT_Q5_0: return launch_generic<QT_Q5_0>(W, rb, x, y, N, K, s);
+    // dense rows (gemv_q over q_val's F32/F16/BF16 cases): the dense-row kernel
+    case QT_F32: return launch_dense<TIERMM_F32>(W, x, y, N, K, s);
+    case QT_F16: return launch_dense<TIERMM_F16>(W, x, y, N, K, s);
+    case QT_BF16: return launch_dense<TIERMM_BF16>(W, x, y, N, K, s);
     case QT_Q4_K:  // MFMA kernels up to kQ4kMaxK (x digits in LDS); beyond, the generic kernel
       if (K <= 8192 && (N + 15) / 16 >= 640) return qgemv_q4k_ws(W, rb, x, y, N, K, s);
       return K <= kQ4kMaxK ? qgemv_q4k(W, rb, x, y, N, K, s) : launch_generic<QT_Q4_K>(W, rb, x, y, N, K, s);
-    case QT_Q5_K: return launch_generic<QT_Q5_K>(W, rb, x, y, N, K, s);
-    default: return launch_generic<QT_Q6_K>(W, rb, x, y, N, K, s);
+    default:
+      return with_qtype(qtype, [&](auto qt) { return launch_generic<decltype(qt)::value>(W, rb, x, y, N, K, s); });
   }
 }
 
@@ -191,6 +193,8 @@ extern "C" int tiermm_qgemv(const void* W, int qtype, size_t rb, const float* x,
   if (N == 0) return TIERMM_OK;
   if (K > kMaxK) return set_error(TIERMM_UNSUPPORTED, "tiermm_qgemv: K=%d above %d", K, kMaxK);
   if (!x || !y || ((uintptr_t)x % 16)) return set_error(TIERMM_EINVAL, "tiermm_qgemv: x must be 16-byte aligned");
+  if ((qtype == QT_F32 || qtype == QT_F16 || qtype == QT_BF16) && ((uintptr_t)W % 16))
+    return set_error(TIERMM_EINVAL, "tiermm_qgemv: dense rows must start 16-byte aligned");
   return qgemv_dispatch(W, qtype, rb, x, y, N, K, (hipStream_t)stream);
 }
 

@@ -1,9 +1,10 @@
 // tm_device.h -- device helpers shared by the gfx950 kernels: fp16/bf16
 // conversion, aligned loads and the exact per-block decoders.
 //
-// Exactness: for Q8_0, Q5_0, Q4_K, Q5_K and Q6_K every product in q_val
+// Exactness: for every block type decoded here every product in q_val
 // (quant.h:59-121) is exact in fp32 (at most 11+7+5 significant bits), so the
-// only fp32 rounding is the final subtraction of the K-quants with a minimum.
+// only fp32 rounding is the final addition of a minimum (Q4_1, Q5_1) or its
+// subtraction (Q4_K, Q5_K), and a fused multiply-add rounds that sum alike.
 // The decoders below therefore give the reference's fp32 value bit for bit
 // whatever the compiler fuses.  fp32 -> fp16 uses v_cvt_f16_f32 (round to
 // nearest even, fp16 denormals kept by the default MODE), matching tier_fp16.
@@ -12,6 +13,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "tm_host.h"
 
@@ -100,6 +102,86 @@ struct Dec<QT_Q5_0> {  // quant.h:66 -- 22-byte blocks: d, qh u32, 16 bytes of n
 };
 
 template <>
+struct Dec<QT_Q4_0> {  // quant.h:64 -- 18-byte blocks: d, 16 bytes of nibbles (low half first)
+  static constexpr int BLK = 32, BYTES = 18;
+  __device__ static void run(const uint8_t* row, int c, float v[8]) {
+    const uint8_t* b = row + (size_t)(c >> 5) * 18;
+    const int i0 = c & 31;
+    const float d = h2f(ld_u16(b));
+    const uint2 q = ld_u64_a2(b + 2 + (i0 & 15));
+    const int sh = i0 < 16 ? 0 : 4;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = d * (float)((int)((byte_at(q, k) >> sh) & 15u) - 8);
+  }
+};
+
+template <>
+struct Dec<QT_Q4_1> {  // quant.h:65 -- 20-byte blocks: d, m, 16 bytes of nibbles
+  static constexpr int BLK = 32, BYTES = 20;
+  __device__ static void run(const uint8_t* row, int c, float v[8]) {
+    const uint8_t* b = row + (size_t)(c >> 5) * 20;
+    const int i0 = c & 31;
+    const float d = h2f(ld_u16(b)), m = h2f(ld_u16(b + 2));
+    const uint2 q = ld_u64_a2(b + 4 + (i0 & 15));
+    const int sh = i0 < 16 ? 0 : 4;
+    // d*v is exact (11 x 4 bits), so a fused multiply-add rounds as d*v + m does
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = d * (float)((byte_at(q, k) >> sh) & 15u) + m;
+  }
+};
+
+template <>
+struct Dec<QT_Q5_1> {  // quant.h:67 -- 24-byte blocks: d, m, qh u32, 16 bytes of nibbles
+  static constexpr int BLK = 32, BYTES = 24;
+  __device__ static void run(const uint8_t* row, int c, float v[8]) {
+    const uint8_t* b = row + (size_t)(c >> 5) * 24;
+    const int i0 = c & 31;
+    const float d = h2f(ld_u16(b)), m = h2f(ld_u16(b + 2));
+    const uint32_t qh = ld_u32_a2(b + 4);
+    const uint2 q = ld_u64_a2(b + 8 + (i0 & 15));
+    const int sh = i0 < 16 ? 0 : 4;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t nib = ((byte_at(q, k) >> sh) & 15u) | (((qh >> (i0 + k)) & 1u) << 4);
+      v[k] = d * (float)nib + m;
+    }
+  }
+};
+
+// Dense rows (quant.h:61-63): 8 elements at a 4-byte (fp32) or 2-byte aligned address.
+template <>
+struct Dec<QT_F32> {
+  static constexpr int BLK = 1, BYTES = 4;
+  __device__ static void run(const uint8_t* row, int c, float v[8]) {
+    const float* p = (const float*)row + c;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = p[k];
+  }
+};
+
+template <>
+struct Dec<QT_F16> {
+  static constexpr int BLK = 1, BYTES = 2;
+  __device__ static void run(const uint8_t* row, int c, float v[8]) {
+    const uint2 a = ld_u64_a2(row + 2 * (size_t)c), b = ld_u64_a2(row + 2 * (size_t)c + 8);
+    const uint32_t w[4] = {a.x, a.y, b.x, b.y};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = h2f((w[k >> 1] >> (16 * (k & 1))) & 0xffffu);
+  }
+};
+
+template <>
+struct Dec<QT_BF16> {
+  static constexpr int BLK = 1, BYTES = 2;
+  __device__ static void run(const uint8_t* row, int c, float v[8]) {
+    const uint2 a = ld_u64_a2(row + 2 * (size_t)c), b = ld_u64_a2(row + 2 * (size_t)c + 8);
+    const uint32_t w[4] = {a.x, a.y, b.x, b.y};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = __uint_as_float((k & 1) ? (w[k >> 1] & 0xffff0000u) : (w[k >> 1] << 16));
+  }
+};
+
+template <>
 struct Dec<QT_Q4_K> {  // quant.h:83-84 -- 144-byte super-blocks
   static constexpr int BLK = 256, BYTES = 144;
   __device__ static void run(const uint8_t* row, int c, float v[8]) {
@@ -154,6 +236,25 @@ struct Dec<QT_Q6_K> {  // quant.h:88-90 -- 210-byte super-blocks (2-byte aligned
     }
   }
 };
+
+// Calls f(std::integral_constant<int, QT>{}) for the GPU-decoded type `qtype`;
+// the caller has already refused every other type.
+template <class F>
+__host__ auto with_qtype(int qtype, F&& f) {
+  switch (qtype) {
+    case QT_F32: return f(std::integral_constant<int, QT_F32>{});
+    case QT_F16: return f(std::integral_constant<int, QT_F16>{});
+    case QT_BF16: return f(std::integral_constant<int, QT_BF16>{});
+    case QT_Q4_0: return f(std::integral_constant<int, QT_Q4_0>{});
+    case QT_Q4_1: return f(std::integral_constant<int, QT_Q4_1>{});
+    case QT_Q5_0: return f(std::integral_constant<int, QT_Q5_0>{});
+    case QT_Q5_1: return f(std::integral_constant<int, QT_Q5_1>{});
+    case QT_Q8_0: return f(std::integral_constant<int, QT_Q8_0>{});
+    case QT_Q4_K: return f(std::integral_constant<int, QT_Q4_K>{});
+    case QT_Q5_K: return f(std::integral_constant<int, QT_Q5_K>{});
+    default: return f(std::integral_constant<int, QT_Q6_K>{});
+  }
+}
 
 // Hand-issued vector memory for the kernels that stream through LDS: the
 // compiler's wait insertion cannot follow global->LDS loads (it falls back to
