@@ -68,8 +68,14 @@ __global__ __launch_bounds__(256) void qgemm_q4k_x3ref(const QArgs p) {
   const uint32_t lds0 = lds_addr(lds);
 
   int grp = 0;  // the group of this workgroup (uniform scan over the tile prefix)
-  while (grp + 1 < p.ngroups && (int)blockIdx.x >= p.tile0[grp + 1]) ++grp;
-  const int tile = (int)blockIdx.x - p.tile0[grp];
+  // One GEMM: workgroups go round-robin over the 8 XCDs, so XCD x is given the
+  // x-th eighth of the tile sequence (M-block major), a few M-blocks whose x rows
+  // stay in that XCD's L2 while its N tiles stream past.
+  int b = (int)blockIdx.x;
+  const int nt_all = p.tile0[p.ngroups];
+  if (p.ngroups == 1 && (nt_all & 7) == 0) b = (b & 7) * (nt_all >> 3) + (b >> 3);
+  while (grp + 1 < p.ngroups && b >= p.tile0[grp + 1]) ++grp;
+  const int tile = b - p.tile0[grp];
   const int ntn = (p.N + BN - 1) / BN;
   const int tm = tile / ntn, tn = tile % ntn;
   const int m0 = tm * QBM, n0 = tn * BN;
