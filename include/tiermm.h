@@ -57,10 +57,19 @@ enum {
   TIERMM_Q5_0 = 6,
   TIERMM_Q5_1 = 7,
   TIERMM_Q8_0 = 8,
+  TIERMM_Q2_K = 10,
+  TIERMM_Q3_K = 11,
   TIERMM_Q4_K = 12,
   TIERMM_Q5_K = 13,
   TIERMM_Q6_K = 14,
-  TIERMM_BF16 = 30
+  TIERMM_IQ4_NL = 20,
+  TIERMM_IQ4_XS = 23,
+  TIERMM_BF16 = 30,
+  TIERMM_TQ1_0 = 34,
+  TIERMM_TQ2_0 = 35,
+  TIERMM_MXFP4 = 39,
+  TIERMM_NF4 = 200,
+  TIERMM_FP4 = 201
 };
 
 /* element type of a dequantized output (dq_k<T>, tier.cpp:294: float, tier_fp16, hip_bfloat16) */
@@ -100,8 +109,10 @@ int tiermm_q_row_bytes(int qtype, int cols, size_t* rb);
 /* dq_k<T> / dq_launch (tier.cpp:293-298): for i < nrows*cols,
  * out[i] = T(q_val(W + (r0 + i/cols)*rb, qtype, i%cols)), T = fp32, fp16
  * (round to nearest even, subnormals kept, as tier_fp16) or bf16 (RNE, as
- * hip_bfloat16).  qtype in {F32, F16, BF16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q4_K,
- * Q5_K, Q6_K}, cols a multiple of 8 and of the block.
+ * hip_bfloat16).  qtype: every q_val type but the lattice-grid IQ2_*, IQ3_* and
+ * IQ1_* families -- F32, F16, BF16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K,
+ * Q5_K, Q6_K, IQ4_NL, IQ4_XS, TQ1_0, TQ2_0, MXFP4, NF4, FP4; cols a multiple of 8
+ * and of the block.
  * Bit-exact with the reference's q_val for finite block scales. */
 int tiermm_dequant(const void* W, int qtype, size_t rb, int cols, size_t r0, size_t nrows,
                    void* out, int out_dtype, tiermm_stream_t stream);
@@ -255,9 +266,9 @@ int tiermm_tq_write(const char* path, int n, const char* const* names, const int
                     const int* cols, const void* const* data, const double* errs, int nmeta,
                     const char* const* keys, const char* const* values);
 
-/* q_val (quant.h:59-121) on the host: out[r*cols + c] for nrows rows of rb bytes,
- * types F32, F16, BF16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K, Q6_K (host
- * memory; the comparison behind tier --tq-check, tier.cpp:2749-2765). */
+/* q_val (quant.h:59-121) on the host: out[r*cols + c] for nrows rows of rb bytes
+ * of any GPU type of tiermm_dequant (host memory; the comparison behind
+ * tier --tq-check, tier.cpp:2749-2765). */
 int tiermm_dequant_host(const void* W, int qtype, size_t rb, int cols, size_t nrows, float* out);
 
 /* Type of one projection under a quantization recipe (tier.cpp:2701-2713, the

@@ -27,6 +27,7 @@ REF_PATH = os.path.join(HERE, "_ref", "libtqref.so")
 
 F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, BF16 = (
     0, 1, 2, 3, 6, 7, 8, 10, 11, 12, 13, 14, 30)
+IQ4_NL, IQ4_XS, TQ1_0, TQ2_0, MXFP4, NF4, FP4 = 20, 23, 34, 35, 39, 200, 201
 OUT_F32, OUT_F16, OUT_BF16 = 0, 1, 2
 
 _u8p = ctypes.POINTER(ctypes.c_uint8)
@@ -236,13 +237,20 @@ def ref_gemv_threads(W: np.ndarray, qtype: int, x: np.ndarray, N: int, K: int, n
     return y
 
 
-def random_blocks(rng: np.random.Generator, qtype: int, nblocks: int) -> np.ndarray:
-    """Random block bytes with finite fp16 scale fields ~N(0,0.02), as check_quant.py:31-48 builds them."""
+def random_blocks(rng: np.random.Generator, qtype: int, nblocks: int, moderate: bool = False) -> np.ndarray:
+    """Random block bytes with finite fp16 scale fields ~N(0,0.02), as check_quant.py:31-48 builds them;
+    NF4/FP4 get an fp32 absmax ~N(0,0.02).  MXFP4's exponent byte is any byte (2^127 * 12 overflows, as
+    in the reference), or with moderate=True one in [110, 130] for products that must stay finite."""
     be, bb = block(qtype)
     b = rng.integers(0, 256, size=(nblocks, bb), dtype=np.uint8)
     halfs = {Q4_0: [0], Q4_1: [0, 2], Q5_0: [0], Q5_1: [0, 2], Q8_0: [0], Q2_K: [80, 82], Q3_K: [108],
-             Q4_K: [0, 2], Q5_K: [0, 2], Q6_K: [208]}.get(qtype, [])
+             Q4_K: [0, 2], Q5_K: [0, 2], Q6_K: [208], IQ4_NL: [0], IQ4_XS: [0], TQ1_0: [52],
+             TQ2_0: [64]}.get(qtype, [])
     for o in halfs:
         h = (rng.standard_normal(nblocks) * 0.02).astype(np.float16).view(np.uint8).reshape(nblocks, 2)
         b[:, o:o + 2] = h
+    if qtype in (NF4, FP4):
+        b[:, 0:4] = (rng.standard_normal(nblocks) * 0.02).astype(np.float32).view(np.uint8).reshape(nblocks, 4)
+    if qtype == MXFP4 and moderate:
+        b[:, 0] = rng.integers(110, 131, size=nblocks, dtype=np.uint8)
     return b

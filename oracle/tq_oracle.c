@@ -107,7 +107,29 @@ static void kq_scale_min(int s, const uint8_t* q, int* sc, int* mn) {
   }
 }
 
-/* One element of a quantized row (quant.h:59-121, the types this path uses). */
+/* The 16-level maps of the non-uniform 4-bit types.  These values define the
+ * formats (the reference keeps them in quant_tables.h and quant.h:50-57) and must
+ * be reproduced exactly.  Pinned: tests compare every code with oracle/_ref. */
+/* IQ4_NL / IQ4_XS levels (ggml's kvalues_iq4nl), times the block scale */
+static const int8_t kIQ4[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+/* MXFP4: an E2M1 code (sign, 2-bit exponent, 1-bit mantissa) as an integer twice its
+ * value, so that the block scale 2^(e-128) gives code * 2^(e-127); code 8 is +0. */
+static int mxfp4_level(int v) {
+  const int e = (v >> 1) & 3, m = v & 1;
+  const int twice = e == 0 ? m : (2 + m) << (e - 1);
+  return (v & 8) ? -twice : twice;
+}
+/* NF4: the 16 normal-quantile levels of bitsandbytes' NF4 code. */
+static const float kNF4[16] = {-1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
+                               -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
+                               0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f,
+                               0.33791524171829224f, 0.44070982933044434f, 0.5626170039176941f,
+                               0.7229568362236023f, 1.0f};
+/* FP4: bitsandbytes' FP4 code (E2M1 magnitudes over 6, code 1 the 1/192 subnormal, bit 3 the sign) */
+static const float kFP4[16] = {0.0f, 0.0052083333f, 0.6666667f, 1.0f, 0.33333334f, 0.5f, 0.16666667f, 0.25f,
+                               -0.0f, -0.0052083333f, -0.6666667f, -1.0f, -0.33333334f, -0.5f, -0.16666667f, -0.25f};
+
+/* One element of a quantized row (quant.h:59-121). */
 float orc_q_val(const uint8_t* row, int type, int col) {
   switch (type) {
     case ORC_F32: return u2f(rd32(row + (size_t)col * 4));
@@ -139,6 +161,24 @@ float orc_q_val(const uint8_t* row, int type, int col) {
       const int v = ((b[8 + i % 16] >> (i < 16 ? 0 : 4)) & 15) | (int)(((rd32(b + 4) >> i) & 1u) << 4);
       return fp16_at(b) * (float)v + fp16_at(b + 2);
     }
+    case ORC_IQ4_NL: { /* quant.h:69: d @0, qs[16] @2 as Q4_0, the nibble maps through kIQ4 */
+      const uint8_t* b = row + (size_t)(col / 32) * 18;
+      const int i = col % 32, v = (b[2 + i % 16] >> (i < 16 ? 0 : 4)) & 15;
+      return fp16_at(b) * (float)kIQ4[v];
+    }
+    case ORC_MXFP4: { /* quant.h:70-71: E8M0 exponent byte @0, qs[16] @1 */
+      const uint8_t* b = row + (size_t)(col / 32) * 17;
+      const int i = col % 32, v = (b[1 + i % 16] >> (i < 16 ? 0 : 4)) & 15;
+      return ldexpf(1.0f, (int)b[0] - 128) * (float)mxfp4_level(v);
+    }
+    case ORC_NF4:
+    case ORC_FP4: { /* quant.h:72-73: fp32 absmax @0, 32 bytes of nibbles @4, even element high */
+      const uint8_t* b = row + (size_t)(col / 64) * 36;
+      const int i = col % 64;
+      const uint8_t y = b[4 + i / 2];
+      const int v = (i & 1) ? (y & 15) : (y >> 4);
+      return (type == ORC_NF4 ? kNF4[v] : kFP4[v]) * u2f(rd32(b));
+    }
     default: break;
   }
   const int i = col % 256; /* position inside a 256-element super-block */
@@ -169,6 +209,46 @@ float orc_q_val(const uint8_t* row, int type, int col) {
       const int hi2 = (b[128 + 32 * half128 + r % 32] >> (2 * (r / 32))) & 3;
       const int q = (lo4 | (hi2 << 4)) - 32;
       return (fp16_at(b + 208) * (float)(int8_t)b[192 + i / 16]) * (float)q;
+    }
+    case ORC_Q2_K: { /* quant.h:76-77: scales[16] @0 (low nibble scale, high min), qs[64] @16, d @80, dmin @82 */
+      const uint8_t* b = row + (size_t)(col / 256) * 84;
+      const int q = (b[16 + 32 * (i / 128) + i % 32] >> (2 * ((i % 128) / 32))) & 3;
+      const uint8_t sc = b[i / 16];
+      return (fp16_at(b + 80) * (float)(sc & 15)) * (float)q - fp16_at(b + 82) * (float)(sc >> 4);
+    }
+    case ORC_Q3_K: { /* quant.h:78-80: hmask[32] @0, qs[64] @32, 6-bit scales in 12 bytes @96, d @108 */
+      const uint8_t* b = row + (size_t)(col / 256) * 110;
+      const uint8_t* s = b + 96;
+      const int j = i / 16;
+      const int low = j < 8 ? (s[j] & 15) : (s[j - 8] >> 4);
+      const int high = (s[8 + j % 4] >> (2 * (j / 4))) & 3;
+      const int sc = (low | (high << 4)) - 32;
+      const int ql = (b[32 + 32 * (i / 128) + i % 32] >> (2 * ((i % 128) / 32))) & 3;
+      const int hbit = (b[i % 32] >> (i / 32)) & 1; /* a clear bit subtracts 4 */
+      return (fp16_at(b + 108) * (float)sc) * (float)(ql - (hbit ? 0 : 4));
+    }
+    case ORC_IQ4_XS: { /* quant.h:92-94: d @0, high scale bits u16 @2, low nibbles [4] @4, qs[128] @8 */
+      const uint8_t* b = row + (size_t)(col / 256) * 136;
+      const int j = i / 32;
+      const int low = (b[4 + j / 2] >> (4 * (j % 2))) & 15, high = (rd16(b + 2) >> (2 * j)) & 3;
+      const int sc = (low | (high << 4)) - 32;
+      const int v = (b[8 + 16 * j + i % 16] >> (4 * ((i % 32) / 16))) & 15;
+      return (fp16_at(b) * (float)sc) * (float)kIQ4[v];
+    }
+    case ORC_TQ2_0: { /* quant.h:116: 2-bit codes qs[64] @0, d @64; value d * (code - 1) */
+      const uint8_t* b = row + (size_t)(col / 256) * 66;
+      const int q = (b[32 * (i / 128) + i % 32] >> (2 * ((i % 128) / 32))) & 3;
+      return fp16_at(b + 64) * (float)(q - 1);
+    }
+    case ORC_TQ1_0: { /* quant.h:117-119: 5 trits per byte in qs[48] @0, 4 per byte in qh[4] @48, d @52 */
+      const uint8_t* b = row + (size_t)(col / 256) * 54;
+      static const int pow3[5] = {1, 3, 9, 27, 81};
+      uint8_t x; /* the byte times 3^k keeps trit k in its top bits (mod 256) */
+      if (i < 160) x = (uint8_t)(b[i % 32] * pow3[i / 32]);
+      else if (i < 240) x = (uint8_t)(b[32 + (i - 160) % 16] * pow3[(i - 160) / 16]);
+      else x = (uint8_t)(b[48 + (i - 240) % 4] * pow3[(i - 240) / 4]);
+      const int trit = ((int)x * 3) >> 8;
+      return fp16_at(b + 52) * (float)(trit - 1);
     }
     default: return 0.f;
   }

@@ -24,7 +24,8 @@ extern "C" {
 enum {
   ORC_F32 = 0, ORC_F16 = 1, ORC_Q4_0 = 2, ORC_Q4_1 = 3, ORC_Q5_0 = 6, ORC_Q5_1 = 7,
   ORC_Q8_0 = 8, ORC_Q2_K = 10, ORC_Q3_K = 11, ORC_Q4_K = 12, ORC_Q5_K = 13,
-  ORC_Q6_K = 14, ORC_BF16 = 30
+  ORC_Q6_K = 14, ORC_IQ4_NL = 20, ORC_IQ4_XS = 23, ORC_BF16 = 30, ORC_TQ1_0 = 34,
+  ORC_TQ2_0 = 35, ORC_MXFP4 = 39, ORC_NF4 = 200, ORC_FP4 = 201
 };
 /* output dtypes of the dequant (dq_k<T>, tier.cpp:294): float, tier_fp16, hip_bfloat16 */
 enum { ORC_OUT_F32 = 0, ORC_OUT_F16 = 1, ORC_OUT_BF16 = 2 };
@@ -49,10 +50,14 @@ void orc_f2bf_n(const float* x, uint16_t* b, size_t n);
  * Pinned: numpy reference rounding in tests (random + boundary inputs). */
 uint16_t orc_f2bf(float f);
 
-/* Scalar dequant of one element, quant.h:59-121 (types Q8_0, Q4_0, Q4_1, Q5_0,
- * Q5_1, Q4_K, Q5_K, Q6_K, F32, F16, BF16).  Returns 0 for other types, as
- * q_val does.  Pinned: golden vectors written by oracle/_ref (the reference's
- * own q_val) and closed-form special cases in tests/test_oracle.py. */
+/* Scalar dequant of one element, quant.h:59-121: every type except the
+ * lattice-grid IQ2_*, IQ3_* and IQ1_* families (Q8_0, Q4_0, Q4_1, Q5_0, Q5_1,
+ * Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS, TQ1_0, TQ2_0, MXFP4, NF4, FP4,
+ * F32, F16, BF16); 0 for those, where q_val reads its grids.  Pinned: the
+ * reference's golden vectors (Q4_0..Q6_K) and closed-form special cases in
+ * tests/test_oracle.py; every type on random blocks, and the types without
+ * golden vectors on every payload byte value, against oracle/_ref (the
+ * reference's own q_val); MXFP4's levels against E2M1 by definition. */
 float orc_q_val(const uint8_t* row, int type, int col);
 
 /* dq_k<T> / dq_launch (tier.cpp:293-298): out[i] = T(q_val(W+(r0+i/cols)*rb, type, i%cols))

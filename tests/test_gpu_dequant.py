@@ -145,3 +145,25 @@ def test_dequant_dense_rows(gpu, t):
     for out in OUTS.values():
         got = _run(gpu, blocks, t, K, out[0])
         assert np.array_equal(got, _expect(blocks, t, K, out[0]))
+
+
+TABLED = {"q2_K": tier_amd.Q2_K, "q3_K": tier_amd.Q3_K, "iq4_nl": tier_amd.IQ4_NL, "iq4_xs": tier_amd.IQ4_XS,
+          "tq1_0": tier_amd.TQ1_0, "tq2_0": tier_amd.TQ2_0, "mxfp4": tier_amd.MXFP4, "nf4": tier_amd.NF4,
+          "fp4": tier_amd.FP4}
+
+
+@pytest.mark.parametrize("name", list(TABLED))
+@pytest.mark.parametrize("outname", list(OUTS))
+def test_dequant_more_types_bit_exact(gpu, name, outname):
+    """q_val's other closed-form and 16-level types (quant.h:69-73, 76-80, 92-94, 116-119), every byte
+    value in the payload, against the oracle (itself pinned to the reference build)."""
+    t, out = TABLED[name], OUTS[outname][0]
+    be, bb = oracle.block(t)
+    rng = np.random.default_rng(90 + t)
+    blocks = oracle.random_blocks(rng, t, 512)
+    if t == tier_amd.MXFP4:
+        blocks[:4, 0] = [0, 1, 2, 254]  # subnormal, smallest normal and near-overflow scales
+    cols = be * 64
+    got = _run(gpu, blocks.reshape(512 * bb // tier_amd.q_row_bytes(t, cols), -1), t, cols, out)
+    want = _expect(blocks, t, cols, out)
+    assert np.array_equal(got, want)

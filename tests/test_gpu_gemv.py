@@ -52,13 +52,15 @@ def test_gemv_config_shapes(gpu, name, t, N, K):
 
 
 @pytest.mark.parametrize("t", [tier_amd.Q8_0, tier_amd.Q5_0, tier_amd.Q4_K, tier_amd.Q5_K, tier_amd.Q6_K,
-                               tier_amd.Q4_0, tier_amd.Q4_1, tier_amd.Q5_1])
+                               tier_amd.Q4_0, tier_amd.Q4_1, tier_amd.Q5_1, tier_amd.Q2_K, tier_amd.Q3_K,
+                               tier_amd.IQ4_NL, tier_amd.IQ4_XS, tier_amd.TQ1_0, tier_amd.TQ2_0, tier_amd.MXFP4,
+                               tier_amd.NF4, tier_amd.FP4])
 @pytest.mark.parametrize("N,K", [(1, 256), (13, 512), (7, 768), (65, 2304)])
 def test_gemv_ragged_shapes(gpu, t, N, K):
     """Row counts that do not fill a wave or a block; one super-block rows; K not a multiple of 512."""
     rng = np.random.default_rng(N * 1000 + K + t)
     be, _ = oracle.block(t)
-    blocks = oracle.random_blocks(rng, t, N * (K // be)).reshape(N, -1)
+    blocks = oracle.random_blocks(rng, t, N * (K // be), moderate=True).reshape(N, -1)
     x = rng.standard_normal(K).astype(np.float32)
     y = _gemv(blocks, t, x, N, K)
     assert oracle.rel_fro(y, oracle.gemv_f64(blocks, t, x, N, K)) <= TOL

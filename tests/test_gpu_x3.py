@@ -216,7 +216,8 @@ def test_qgemm_f32_mode(gpu, name, t, M, N, K):
     assert oracle.rel_fro(got, x.astype(np.float64) @ wf.astype(np.float64).T) <= BAR
 
 
-@pytest.mark.parametrize("t", [tier_amd.Q4_0, tier_amd.Q4_1, tier_amd.Q5_1, tier_amd.F32, tier_amd.F16, tier_amd.BF16])
+@pytest.mark.parametrize("t", [tier_amd.Q4_0, tier_amd.Q4_1, tier_amd.Q5_1, tier_amd.F32, tier_amd.F16, tier_amd.BF16,
+                               tier_amd.Q3_K, tier_amd.IQ4_XS, tier_amd.NF4])
 @pytest.mark.parametrize("mode", [tier_amd.MODE_X3REF, tier_amd.MODE_F32])
 def test_qgemm_more_types(gpu, t, mode):
     """The legacy 32-blocks and dense rows through tiermm_qgemm, both semantics, against fp64."""
@@ -227,7 +228,7 @@ def test_qgemm_more_types(gpu, t, mode):
         bits = {tier_amd.F32: w, tier_amd.F16: oracle.f2h(w), tier_amd.BF16: oracle.f2bf(w)}[t]
         blocks = np.ascontiguousarray(bits).view(np.uint8).reshape(N, -1)
     else:
-        blocks = oracle.random_blocks(rng, t, N * K // 32).reshape(N, -1)
+        blocks = oracle.random_blocks(rng, t, N * K // oracle.block(t)[0]).reshape(N, -1)
     x = activations(M, K, seed=81)
     W, X, Y = hip.to_device(blocks), hip.to_device(x), hip.DeviceBuffer(M * N * 4)
     tier_amd.qgemm(W.ptr, t, tier_amd.q_row_bytes(t, K), X.ptr, Y.ptr, M, N, K, mode=mode)

@@ -30,10 +30,15 @@ def test_f2h_matches_reference_golden(golden):
     assert np.array_equal(oracle.f2h(g["f32"]), g["f2h"])
 
 
+# types without golden vectors in the reference's tests: pinned against the reference build
+MORE = {"q2_K": oracle.Q2_K, "q3_K": oracle.Q3_K, "iq4_nl": oracle.IQ4_NL, "iq4_xs": oracle.IQ4_XS,
+        "tq1_0": oracle.TQ1_0, "tq2_0": oracle.TQ2_0, "mxfp4": oracle.MXFP4, "nf4": oracle.NF4, "fp4": oracle.FP4}
+
+
 @pytest.mark.skipif(not oracle.ref_available(), reason="oracle/_ref not built (no reference checkout)")
-@pytest.mark.parametrize("name", list(NAMES))
+@pytest.mark.parametrize("name", list(NAMES) + list(MORE))
 def test_dequant_matches_reference_build(name):
-    t = NAMES[name]
+    t = NAMES[name] if name in NAMES else MORE[name]
     rng = np.random.default_rng(1000 + t)
     be, bb = oracle.block(t)
     cols = 2048
@@ -311,3 +316,35 @@ def test_x3s_product_within_bound():
     Y = oracle.x3s_product_f64(xh, xl, ex, wh, wl, ew)
     ref = X.astype(np.float64) @ W.astype(np.float64).T
     assert oracle.rel_fro(Y, ref) < 2.0 ** -21
+
+
+@pytest.mark.skipif(not oracle.ref_available(), reason="oracle/_ref not built (no reference checkout)")
+@pytest.mark.parametrize("name", list(MORE))
+def test_more_types_every_code_against_reference_build(name):
+    """Every byte value in every position class: blocks whose payload bytes run through 0..255."""
+    t = MORE[name]
+    be, bb = oracle.block(t)
+    rng = np.random.default_rng(77)
+    blocks = oracle.random_blocks(rng, t, 256)
+    scale = {oracle.Q2_K: (80, 84), oracle.Q3_K: (108, 110), oracle.IQ4_NL: (0, 2), oracle.IQ4_XS: (0, 2),
+             oracle.TQ1_0: (52, 54), oracle.TQ2_0: (64, 66), oracle.MXFP4: (0, 1), oracle.NF4: (0, 4),
+             oracle.FP4: (0, 4)}[t]
+    for j in range(bb):
+        if not scale[0] <= j < scale[1]:
+            blocks[:, j] = np.arange(256, dtype=np.uint8)  # block k holds byte value k everywhere else
+    got = oracle.dequant(blocks, t, be * 256 // be * be)
+    want = oracle.ref_dequant(blocks, t, be * 256 // be * be)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_mxfp4_levels_are_twice_e2m1():
+    """MXFP4 element = 2^(e-127) * E2M1(code): the oracle's doubled levels over the 2^(e-128) scale."""
+    e2m1 = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0]
+    for e in (1, 100, 127, 128, 150):
+        b = np.zeros((1, 17), np.uint8)
+        b[0, 0] = e
+        b[0, 1:9] = np.array([c | ((c + 8) << 4) for c in range(8)], np.uint8)  # codes c and c+8
+        v = oracle.dequant(b, oracle.MXFP4, 32)[0]
+        for c in range(8):
+            assert v[c] == np.float32(2.0 ** (e - 127) * e2m1[c])
+            assert v[16 + c] == np.float32(-(2.0 ** (e - 127)) * e2m1[c])

@@ -181,7 +181,9 @@ def test_tq_check_metrics(tmp_path):
     assert tq.check(model, base3, say=lambda s: None) == 2
 
 
-@pytest.mark.parametrize("t", [tier_amd.Q8_0, tier_amd.Q5_0, tier_amd.Q4_K, tier_amd.Q5_K, tier_amd.Q6_K])
+@pytest.mark.parametrize("t", [tier_amd.Q8_0, tier_amd.Q5_0, tier_amd.Q4_K, tier_amd.Q5_K, tier_amd.Q6_K,
+                               tier_amd.Q2_K, tier_amd.Q3_K, tier_amd.IQ4_NL, tier_amd.IQ4_XS, tier_amd.TQ1_0,
+                               tier_amd.TQ2_0, tier_amd.MXFP4, tier_amd.NF4, tier_amd.FP4])
 def test_host_dequant_matches_oracle_on_random_blocks(t):
     import oracle
     rng = np.random.default_rng(100 + t)

@@ -60,7 +60,8 @@ int launch_dequant(const void* W, size_t rb, int cols, size_t r0, size_t nrows, 
 bool gpu_type(int qtype) {
   switch (qtype) {
     case QT_F32: case QT_F16: case QT_BF16: case QT_Q4_0: case QT_Q4_1: case QT_Q5_0: case QT_Q5_1:
-    case QT_Q8_0: case QT_Q4_K: case QT_Q5_K: case QT_Q6_K: return true;
+    case QT_Q8_0: case QT_Q2_K: case QT_Q3_K: case QT_Q4_K: case QT_Q5_K: case QT_Q6_K: case QT_IQ4_NL:
+    case QT_IQ4_XS: case QT_TQ1_0: case QT_TQ2_0: case QT_MXFP4: case QT_NF4: case QT_FP4: return true;
     default: return false;
   }
 }
@@ -74,7 +75,10 @@ int check_qweight(const char* who, const void* W, int qtype, size_t rb, int cols
     return set_error(TIERMM_UNSUPPORTED, "%s: %d columns are not whole %s blocks of %d", who, cols, bi->name, whole);
   if (rb != (size_t)cols / bi->elems * bi->bytes)
     return set_error(TIERMM_EINVAL, "%s: rb %zu does not match %d %s columns", who, rb, cols, bi->name);
-  const size_t align = (qtype == QT_Q4_K || qtype == QT_Q5_K) ? 16 : qtype == QT_F32 ? 4 : 2;
+  const size_t align = (qtype == QT_Q4_K || qtype == QT_Q5_K)                          ? 16
+                       : (qtype == QT_F32 || qtype == QT_Q2_K || qtype == QT_NF4 || qtype == QT_FP4) ? 4
+                       : qtype == QT_MXFP4                                                    ? 1
+                                                                                             : 2;
   if (!W || ((uintptr_t)W % align) || (rb % align))
     return set_error(TIERMM_EINVAL, "%s: weight rows must be %zu-byte aligned", who, align);
   return TIERMM_OK;

@@ -1,10 +1,13 @@
 // host_dequant.cpp -- q_val on the host, for the tools that compare a quantized
 // base with its source (the --tq-check metrics) without a GPU.
 //
-// Element values follow q_val (quant.h:59-121) for the types with closed forms:
-// F32, F16, BF16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K, Q6_K.  Compiled
-// without floating-point contraction, so (d*sc)*v - dmin*m rounds exactly as
-// the reference's expression does (every product is exact; one rounding).
+// Element values follow q_val (quant.h:59-121) for every type except the
+// lattice-grid IQ2/IQ3/IQ1 families: F32, F16, BF16, Q4_0, Q4_1, Q5_0, Q5_1,
+// Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS, TQ1_0, TQ2_0, MXFP4, NF4,
+// FP4.  Compiled without floating-point contraction, so (d*sc)*v - dmin*m rounds
+// exactly as the reference's expression does (every product is exact; one
+// rounding).
+#include <cmath>
 #include <cstdint>
 #include <cstring>
 
@@ -52,6 +55,22 @@ void scale_min(int j, const uint8_t* q, int& sc, int& mn) {  // 6-bit pairs, qua
   }
 }
 
+// Levels of the non-uniform 4-bit codes (formats fixed by their definitions).
+const int8_t kIq4[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};  // IQ4_NL, IQ4_XS
+const float kNf4[16] = {-1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
+                        -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
+                        0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
+                        0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};  // bitsandbytes NF4
+const float kFp4[16] = {0.0f, 0.0052083333f, 0.6666667f, 1.0f, 0.33333334f, 0.5f, 0.16666667f, 0.25f,
+                        -0.0f, -0.0052083333f, -0.6666667f, -1.0f, -0.33333334f, -0.5f, -0.16666667f, -0.25f};  // bitsandbytes FP4
+// MXFP4: E2M1 code as an integer twice its value (code 8 is +0)
+int mxfp4_twice(int v) {
+  const int e = (v >> 1) & 3, m = v & 1, t = e == 0 ? m : (2 + m) << (e - 1);
+  return (v & 8) ? -t : t;
+}
+// 2^(e-128) for the E8M0 byte e (the MXFP4 block scale, halved for the doubled levels)
+float e8m0_half(int e) { return std::ldexp(1.0f, e - 128); }
+
 float value(const uint8_t* row, int type, int col) {
   switch (type) {
     case QT_F32: return u2f(rd32(row + (size_t)col * 4));
@@ -82,6 +101,61 @@ float value(const uint8_t* row, int type, int col) {
     case QT_Q8_0: {
       const uint8_t* b = row + (size_t)(col >> 5) * 34;
       return f16(rd16(b)) * (float)(int8_t)b[2 + (col & 31)];
+    }
+    case QT_IQ4_NL: {
+      const uint8_t* b = row + (size_t)(col >> 5) * 18;
+      const int i = col & 31, v = (b[2 + (i & 15)] >> (4 * (i >> 4))) & 15;
+      return f16(rd16(b)) * (float)kIq4[v];
+    }
+    case QT_MXFP4: {
+      const uint8_t* b = row + (size_t)(col >> 5) * 17;
+      const int i = col & 31, v = (b[1 + (i & 15)] >> (4 * (i >> 4))) & 15;
+      return e8m0_half(b[0]) * (float)mxfp4_twice(v);
+    }
+    case QT_NF4:
+    case QT_FP4: {
+      const uint8_t* b = row + (size_t)(col >> 6) * 36;
+      const int i = col & 63;
+      const uint8_t y = b[4 + (i >> 1)];
+      const int v = (i & 1) ? (y & 15) : (y >> 4);
+      return (type == QT_NF4 ? kNf4[v] : kFp4[v]) * u2f(rd32(b));
+    }
+    case QT_Q2_K: {
+      const uint8_t* b = row + (size_t)(col >> 8) * 84;
+      const int i = col & 255, q = (b[16 + (i >> 7) * 32 + (i & 31)] >> (2 * ((i & 127) >> 5))) & 3;
+      const uint8_t sc = b[i >> 4];
+      return (f16(rd16(b + 80)) * (float)(sc & 15)) * (float)q - f16(rd16(b + 82)) * (float)(sc >> 4);
+    }
+    case QT_Q3_K: {
+      const uint8_t* b = row + (size_t)(col >> 8) * 110;
+      const int i = col & 255, j = i >> 4;
+      const uint8_t* s = b + 96;
+      const int sc = ((j < 8 ? (s[j] & 15) : (s[j - 8] >> 4)) | (((s[8 + (j & 3)] >> (2 * (j >> 2))) & 3) << 4)) - 32;
+      const int ql = (b[32 + (i >> 7) * 32 + (i & 31)] >> (2 * ((i & 127) >> 5))) & 3;
+      const int sub = ((b[i & 31] >> (i >> 5)) & 1) ? 0 : 4;
+      return (f16(rd16(b + 108)) * (float)sc) * (float)(ql - sub);
+    }
+    case QT_IQ4_XS: {
+      const uint8_t* b = row + (size_t)(col >> 8) * 136;
+      const int i = col & 255, j = i >> 5;
+      const int sc = (((b[4 + (j >> 1)] >> (4 * (j & 1))) & 15) | (((rd16(b + 2) >> (2 * j)) & 3) << 4)) - 32;
+      const int v = (b[8 + j * 16 + (i & 15)] >> (4 * ((i & 31) >> 4))) & 15;
+      return (f16(rd16(b)) * (float)sc) * (float)kIq4[v];
+    }
+    case QT_TQ2_0: {
+      const uint8_t* b = row + (size_t)(col >> 8) * 66;
+      const int i = col & 255, q = (b[(i >> 7) * 32 + (i & 31)] >> (2 * ((i & 127) >> 5))) & 3;
+      return f16(rd16(b + 64)) * (float)(q - 1);
+    }
+    case QT_TQ1_0: {
+      const uint8_t* b = row + (size_t)(col >> 8) * 54;
+      const int i = col & 255;
+      static const int p3[5] = {1, 3, 9, 27, 81};
+      uint8_t x;
+      if (i < 160) x = (uint8_t)(b[i & 31] * p3[i >> 5]);
+      else if (i < 240) x = (uint8_t)(b[32 + ((i - 160) & 15)] * p3[(i - 160) >> 4]);
+      else x = (uint8_t)(b[48 + ((i - 240) & 3)] * p3[(i - 240) >> 2]);
+      return f16(rd16(b + 52)) * (float)((((int)x * 3) >> 8) - 1);
     }
     case QT_Q4_K: {
       const uint8_t* b = row + (size_t)(col >> 8) * 144;
@@ -117,7 +191,8 @@ float value(const uint8_t* row, int type, int col) {
 extern "C" int tiermm_dequant_host(const void* W, int qtype, size_t rb, int cols, size_t nrows, float* out) {
   switch (qtype) {
     case QT_F32: case QT_F16: case QT_BF16: case QT_Q4_0: case QT_Q4_1: case QT_Q5_0: case QT_Q5_1:
-    case QT_Q8_0: case QT_Q4_K: case QT_Q5_K: case QT_Q6_K: break;
+    case QT_Q8_0: case QT_Q2_K: case QT_Q3_K: case QT_Q4_K: case QT_Q5_K: case QT_Q6_K: case QT_IQ4_NL:
+    case QT_IQ4_XS: case QT_TQ1_0: case QT_TQ2_0: case QT_MXFP4: case QT_NF4: case QT_FP4: break;
     default: return set_error(TIERMM_UNSUPPORTED, "tiermm_dequant_host: type %d", qtype);
   }
   const BlockInfo* b = block_info(qtype);

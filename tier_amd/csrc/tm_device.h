@@ -237,6 +237,163 @@ struct Dec<QT_Q6_K> {  // quant.h:88-90 -- 210-byte super-blocks (2-byte aligned
   }
 };
 
+// Levels of the non-uniform 4-bit codes (formats fixed by their definitions).
+__device__ constexpr int8_t kIq4Levels[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+__device__ constexpr float kNf4Levels[16] = {
+    -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f, -0.28444138169288635f,
+    -0.18477343022823334f, -0.09105003625154495f, 0.0f, 0.07958029955625534f, 0.16093020141124725f,
+    0.24611230194568634f, 0.33791524171829224f, 0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f,
+    1.0f};  // bitsandbytes NF4
+__device__ constexpr float kFp4Levels[16] = {0.0f, 0.0052083333f, 0.6666667f, 1.0f, 0.33333334f, 0.5f,
+                                             0.16666667f, 0.25f, -0.0f, -0.0052083333f, -0.6666667f, -1.0f,
+                                             -0.33333334f, -0.5f, -0.16666667f, -0.25f};  // bitsandbytes FP4
+
+__device__ __forceinline__ uint32_t ld_u32(const uint8_t* p) { return *(const uint32_t*)p; }
+__device__ __forceinline__ uint32_t byte_of(uint32_t w, int k) { return (w >> (8 * k)) & 255u; }
+
+template <>
+struct Dec<QT_IQ4_NL> {  // quant.h:69 -- 18-byte blocks: d, 16 bytes of nibbles mapped through the IQ4 levels
+  static constexpr int BLK = 32, BYTES = 18;
+  __device__ static void run(const uint8_t* row, int c, float v[8]) {
+    const uint8_t* b = row + (size_t)(c >> 5) * 18;
+    const int i0 = c & 31;
+    const float d = h2f(ld_u16(b));
+    const uint2 q = ld_u64_a2(b + 2 + (i0 & 15));
+    const int sh = i0 < 16 ? 0 : 4;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = d * (float)kIq4Levels[(byte_at(q, k) >> sh) & 15u];
+  }
+};
+
+template <>
+struct Dec<QT_MXFP4> {  // quant.h:70-71 -- 17-byte blocks: E8M0 exponent, 16 bytes of E2M1 nibbles
+  static constexpr int BLK = 32, BYTES = 17;
+  __device__ static void run(const uint8_t* row, int c, float v[8]) {
+    const uint8_t* b = row + (size_t)(c >> 5) * 17;  // blocks are byte aligned: byte loads
+    const int i0 = c & 31, e = b[0];
+    const float scale = __builtin_ldexpf(1.0f, e - 128);  // 2^(e-127) over the doubled levels
+    const int sh = i0 < 16 ? 0 : 4;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int code = (b[1 + (i0 & 15) + k] >> sh) & 15, ex = (code >> 1) & 3, m = code & 1;
+      const int twice = ex == 0 ? m : (2 + m) << (ex - 1);
+      v[k] = scale * (float)((code & 8) ? -twice : twice);
+    }
+  }
+};
+
+template <int QT>
+struct DecBnb {  // quant.h:72-73 -- 36-byte blocks of 64: fp32 absmax, 32 bytes of nibbles (even element high)
+  static constexpr int BLK = 64, BYTES = 36;
+  __device__ static void run(const uint8_t* row, int c, float v[8]) {
+    const uint8_t* b = row + (size_t)(c >> 6) * 36;
+    const float a = __uint_as_float(ld_u32(b));
+    const uint32_t w = ld_u32(b + 4 + ((c & 63) >> 1));
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t y = byte_of(w, k >> 1), code = (k & 1) ? (y & 15u) : (y >> 4);
+      v[k] = (QT == QT_NF4 ? kNf4Levels[code] : kFp4Levels[code]) * a;
+    }
+  }
+};
+template <>
+struct Dec<QT_NF4> : DecBnb<QT_NF4> {};
+template <>
+struct Dec<QT_FP4> : DecBnb<QT_FP4> {};
+
+template <>
+struct Dec<QT_Q2_K> {  // quant.h:76-77 -- 84-byte super-blocks: nibble scale/min pairs, 2-bit codes, d, dmin
+  static constexpr int BLK = 256, BYTES = 84;
+  __device__ static void run(const uint8_t* row, int c, float v[8]) {
+    const uint8_t* b = row + (size_t)(c >> 8) * 84;
+    const int i0 = c & 255;
+    const uint32_t sc = b[i0 >> 4];
+    const float dsc = h2f(ld_u16(b + 80)) * (float)(sc & 15u), dm = h2f(ld_u16(b + 82)) * (float)(sc >> 4);
+    const uint8_t* q = b + 16 + (i0 >> 7) * 32 + (i0 & 31);
+    const uint32_t q0 = ld_u32(q), q1 = ld_u32(q + 4);
+    const int sh = 2 * ((i0 & 127) >> 5);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = dsc * (float)((byte_of(k < 4 ? q0 : q1, k & 3) >> sh) & 3u) - dm;
+  }
+};
+
+template <>
+struct Dec<QT_Q3_K> {  // quant.h:78-80 -- 110-byte super-blocks: high-bit mask, 2-bit codes, 6-bit scales, d
+  static constexpr int BLK = 256, BYTES = 110;
+  __device__ static void run(const uint8_t* row, int c, float v[8]) {
+    const uint8_t* b = row + (size_t)(c >> 8) * 110;
+    const int i0 = c & 255, j = i0 >> 4;
+    const uint8_t* s = b + 96;
+    const int sc = ((j < 8 ? (s[j] & 15) : (s[j - 8] >> 4)) | (((s[8 + (j & 3)] >> (2 * (j >> 2))) & 3) << 4)) - 32;
+    const float ds = h2f(ld_u16(b + 108)) * (float)sc;
+    const uint2 ql = ld_u64_a2(b + 32 + (i0 >> 7) * 32 + (i0 & 31));
+    const uint2 hm = ld_u64_a2(b + (i0 & 31));
+    const int sh = 2 * ((i0 & 127) >> 5), hb = i0 >> 5;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int q = (int)((byte_at(ql, k) >> sh) & 3u) - (((byte_at(hm, k) >> hb) & 1u) ? 0 : 4);
+      v[k] = ds * (float)q;
+    }
+  }
+};
+
+template <>
+struct Dec<QT_IQ4_XS> {  // quant.h:92-94 -- 136-byte super-blocks: d, 6-bit scales, nibbles mapped through the IQ4 levels
+  static constexpr int BLK = 256, BYTES = 136;
+  __device__ static void run(const uint8_t* row, int c, float v[8]) {
+    const uint8_t* b = row + (size_t)(c >> 8) * 136;
+    const int i0 = c & 255, j = i0 >> 5;
+    const int sc = (((b[4 + (j >> 1)] >> (4 * (j & 1))) & 15) | (((ld_u16(b + 2) >> (2 * j)) & 3) << 4)) - 32;
+    const float ds = h2f(ld_u16(b)) * (float)sc;  // 11 + 6 bits: exact, and times a 7-bit level still exact
+    const uint2 q = ld_u64_a2(b + 8 + j * 16 + (i0 & 15));
+    const int sh = 4 * ((i0 & 31) >> 4);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = ds * (float)kIq4Levels[(byte_at(q, k) >> sh) & 15u];
+  }
+};
+
+template <>
+struct Dec<QT_TQ2_0> {  // quant.h:116 -- 66-byte super-blocks: 2-bit codes, d; value d * (code - 1)
+  static constexpr int BLK = 256, BYTES = 66;
+  __device__ static void run(const uint8_t* row, int c, float v[8]) {
+    const uint8_t* b = row + (size_t)(c >> 8) * 66;
+    const int i0 = c & 255;
+    const float d = h2f(ld_u16(b + 64));
+    const uint2 q = ld_u64_a2(b + (i0 >> 7) * 32 + (i0 & 31));
+    const int sh = 2 * ((i0 & 127) >> 5);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = d * (float)((int)((byte_at(q, k) >> sh) & 3u) - 1);
+  }
+};
+
+template <>
+struct Dec<QT_TQ1_0> {  // quant.h:117-119 -- 54-byte super-blocks: base-3 packed trits, d; value d * (trit - 1)
+  static constexpr int BLK = 256, BYTES = 54;
+  __device__ static void run(const uint8_t* row, int c, float v[8]) {
+    const uint8_t* b = row + (size_t)(c >> 8) * 54;
+    const int i0 = c & 255;
+    const float d = h2f(ld_u16(b + 52));
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int i = i0 + k;
+      int byte, mul;  // the byte times 3^t keeps trit t in its top bits (mod 256)
+      if (i < 160) {
+        byte = b[i & 31];
+        mul = i >> 5;
+      } else if (i < 240) {
+        byte = b[32 + ((i - 160) & 15)];
+        mul = (i - 160) >> 4;
+      } else {
+        byte = b[48 + ((i - 240) & 3)];
+        mul = (i - 240) >> 2;
+      }
+      const int p3 = mul == 0 ? 1 : mul == 1 ? 3 : mul == 2 ? 9 : mul == 3 ? 27 : 81;
+      const uint32_t x = (uint32_t)(byte * p3) & 255u;
+      v[k] = d * (float)((int)((x * 3u) >> 8) - 1);
+    }
+  }
+};
+
 // Calls f(std::integral_constant<int, QT>{}) for the GPU-decoded type `qtype`;
 // the caller has already refused every other type.
 template <class F>
@@ -252,6 +409,15 @@ __host__ auto with_qtype(int qtype, F&& f) {
     case QT_Q8_0: return f(std::integral_constant<int, QT_Q8_0>{});
     case QT_Q4_K: return f(std::integral_constant<int, QT_Q4_K>{});
     case QT_Q5_K: return f(std::integral_constant<int, QT_Q5_K>{});
+    case QT_Q2_K: return f(std::integral_constant<int, QT_Q2_K>{});
+    case QT_Q3_K: return f(std::integral_constant<int, QT_Q3_K>{});
+    case QT_IQ4_NL: return f(std::integral_constant<int, QT_IQ4_NL>{});
+    case QT_IQ4_XS: return f(std::integral_constant<int, QT_IQ4_XS>{});
+    case QT_TQ1_0: return f(std::integral_constant<int, QT_TQ1_0>{});
+    case QT_TQ2_0: return f(std::integral_constant<int, QT_TQ2_0>{});
+    case QT_MXFP4: return f(std::integral_constant<int, QT_MXFP4>{});
+    case QT_NF4: return f(std::integral_constant<int, QT_NF4>{});
+    case QT_FP4: return f(std::integral_constant<int, QT_FP4>{});
     default: return f(std::integral_constant<int, QT_Q6_K>{});
   }
 }

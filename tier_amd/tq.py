@@ -23,7 +23,8 @@ from . import _L, _check, q_info
 
 # block geometry by type name (quant.h:26-30)
 _TYPES = {"F32": 0, "F16": 1, "BF16": 30, "Q4_0": 2, "Q4_1": 3, "Q5_0": 6, "Q5_1": 7, "Q8_0": 8, "Q2_K": 10,
-          "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
+          "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "IQ4_NL": 20, "IQ4_XS": 23, "TQ1_0": 34, "TQ2_0": 35,
+          "MXFP4": 39, "NF4": 200, "FP4": 201}
 
 
 _NAMES = {v: k for k, v in _TYPES.items()}
