@@ -133,6 +133,18 @@ def test_workspace_sizes():
     assert tier_amd.qgemm_ws_bytes(tier_amd.Q4_K, 512, 5120, 5120) == 3 * 512 * 5120 * 2
     # other types stage fp16 W in the workspace as well
     assert tier_amd.qgemm_ws_bytes(tier_amd.Q6_K, 512, 5120, 5120) == 5120 * 5120 * 2 + 3 * 512 * 5120 * 2
+    # routed experts: 256-row tiles that fill the chip stage the fp16 weights of
+    # up to 64 experts (1 GiB at most); few or mostly empty tiles keep one expert's
+    E, N, K = 64, 1408, 2048
+    full = [512 * e for e in range(E + 1)]
+    planes = 3 * full[-1] * K * 2
+    assert tier_amd.qgemm_grouped_ws_bytes([tier_amd.Q5_0] * E, full, N, K) == planes + 64 * N * K * 2
+    assert tier_amd.qgemm_grouped_ws_bytes([tier_amd.Q5_0] * E, full, 14336, 5120) == \
+        planes // K * 5120 + (1 << 30) // (14336 * 5120 * 2) * 14336 * 5120 * 2
+    sparse = [100 * e for e in range(E + 1)]  # 100 rows per 256-row tile
+    assert tier_amd.qgemm_grouped_ws_bytes([tier_amd.Q5_0] * E, sparse, N, K) == \
+        3 * sparse[-1] * K * 2 + N * K * 2
+    assert tier_amd.qgemm_grouped_ws_bytes([tier_amd.Q4_K] * E, sparse, N, K) == 3 * sparse[-1] * K * 2
 
 
 def _mats(n_layers, no_v=()):

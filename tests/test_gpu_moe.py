@@ -82,3 +82,41 @@ def test_grouped_gemm_and_combine(gpu, t, N, K):
             p = token_pairs[tt, j]
             ref[tt] += float(pair_w[p]) * ref_s[p]
     assert oracle.rel_fro(out, ref) <= BAR
+
+
+@pytest.mark.parametrize("with_ws", [False, True])
+def test_grouped_big_tiles_mixed_types(gpu, with_ws):
+    """Routed rows that fill the chip with 256-row tiles (the grouped 256x320 path):
+    70 experts (two chunks of at most 64), four weight types in one call, an empty
+    expert, a one-row expert and ragged row counts."""
+    rng = np.random.default_rng(70)
+    E, N, K = 70, 640, 256
+    types = [tier_amd.Q4_K, tier_amd.Q5_0, tier_amd.Q8_0, tier_amd.Q6_K]
+    counts = rng.integers(260, 330, E)
+    counts[3], counts[11], counts[40] = 0, 1, 257
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    P = int(offsets[-1])
+    qt = [types[e % 4] for e in range(E)]
+    blocks = [oracle.random_blocks(rng, qt[e], N * (K // oracle.block(qt[e])[0])).reshape(N, -1) for e in range(E)]
+    xs = activations(P, K, seed=71)
+    dW = [hip.to_device(b) for b in blocks]
+    X, Y = hip.to_device(xs), hip.DeviceBuffer(P * N * 4)
+    rbs = [tier_amd.q_row_bytes(q, K) for q in qt]
+    ws = wsb = None
+    if with_ws:
+        wsb = tier_amd.qgemm_grouped_ws_bytes(qt, offsets.tolist(), N, K)
+        assert wsb >= 3 * P * K * 2 + 64 * N * K * 2  # planes + one chunk of fp16 experts
+        ws = hip.DeviceBuffer(wsb)
+    tier_amd.qgemm_grouped([w.ptr for w in dW], qt, rbs, X.ptr, offsets.tolist(), Y.ptr, N, K,
+                           ws=ws.ptr if ws else None, ws_bytes=wsb or 0)
+    hip.synchronize()
+    ys = Y.download(np.float32, P * N).reshape(P, N)
+    ref = np.empty((P, N))
+    for e in range(E):
+        a, b = offsets[e], offsets[e + 1]
+        w16 = oracle.h2f(oracle.dequant(blocks[e], qt[e], K, oracle.OUT_F16)).reshape(N, K).astype(np.float64)
+        ref[a:b] = xs[a:b].astype(np.float64) @ w16.T
+    for e in (11, 40, 69):  # per expert as well: a misplaced row or group shows here
+        a, b = offsets[e], offsets[e + 1]
+        assert oracle.rel_fro(ys[a:b], ref[a:b]) <= BAR, e
+    assert oracle.rel_fro(ys, ref) <= BAR

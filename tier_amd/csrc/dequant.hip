@@ -53,6 +53,32 @@ int launch_dequant(const void* W, size_t rb, int cols, size_t r0, size_t nrows, 
   return TIERMM_OK;
 }
 
+// Several weights of one type and shape to fp16 in one launch: blockIdx.y picks
+// the weight (routed experts before their grouped GEMM).
+constexpr int DQ_GROUP = 64;
+struct DqGroup {
+  const uint8_t* W[DQ_GROUP];
+  uint16_t* out[DQ_GROUP];
+};
+
+template <int QT>
+__global__ __launch_bounds__(256) void dequant_f16_group_kernel(const DqGroup g, size_t rb, int cols, size_t n8) {
+  const uint8_t* W = g.W[blockIdx.y];
+  uint16_t* out = g.out[blockIdx.y];
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x; t < n8; t += stride) {
+    const size_t e = t * 8;
+    const size_t row = e / (size_t)cols;
+    const int col = (int)(e - row * (size_t)cols);
+    float v[8];
+    Dec<QT>::run(W + row * rb, col, v);
+    uint32_t p[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) p[k] = f2h(v[2 * k]) | (f2h(v[2 * k + 1]) << 16);
+    *(uint4*)(out + e) = make_uint4(p[0], p[1], p[2], p[3]);
+  }
+}
+
 }  // namespace
 
 // Shared argument checks for a quantized weight: type handled, rb consistent,
@@ -88,6 +114,27 @@ int check_qweight(const char* who, const void* W, int qtype, size_t rb, int cols
 int dequant_f16_rows(const void* W, int qtype, size_t rb, int cols, size_t nrows, uint16_t* out, hipStream_t s) {
   return with_qtype(qtype, [&](auto qt) {
     return launch_dequant<decltype(qt)::value>(W, rb, cols, 0, nrows, out, TIERMM_OUT_F16, s);
+  });
+}
+
+// n (<= 64) weights of one type, each nrows x cols, to fp16 rows at out[i].
+int dequant_f16_group(const void* const* W, uint16_t* const* out, int n, int qtype, size_t rb, int cols,
+                      size_t nrows, hipStream_t s) {
+  if (n <= 0) return TIERMM_OK;
+  if (n > DQ_GROUP) return set_error(TIERMM_EINVAL, "dequant_f16_group: %d weights (max %d)", n, DQ_GROUP);
+  const size_t n8 = nrows * (size_t)cols / 8;
+  if (n8 == 0) return TIERMM_OK;
+  DqGroup g{};
+  for (int i = 0; i < n; ++i) {
+    g.W[i] = (const uint8_t*)W[i];
+    g.out[i] = out[i];
+  }
+  const size_t want = (n8 + 255) / 256;
+  const dim3 grid((unsigned)(want < 2048 ? want : 2048), (unsigned)n);
+  return with_qtype(qtype, [&](auto qt) -> int {
+    dequant_f16_group_kernel<decltype(qt)::value><<<grid, 256, 0, s>>>(g, rb, cols, n8);
+    TM_LAUNCH_CHECK("dequant_f16_group: launch");
+    return TIERMM_OK;
   });
 }
 

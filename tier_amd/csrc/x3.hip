@@ -26,6 +26,8 @@ namespace tiermm {
 
 int check_qweight(const char* who, const void* W, int qtype, size_t rb, int cols);
 int dequant_f16_rows(const void* W, int qtype, size_t rb, int cols, size_t nrows, uint16_t* out, hipStream_t s);
+int dequant_f16_group(const void* const* W, uint16_t* const* out, int n, int qtype, size_t rb, int cols,
+                      size_t nrows, hipStream_t s);
 int qgemm_q4k_fused(const void* W, size_t rb, const uint16_t* xparts, size_t xs, float* Y, int ldy, int M, int N, int K,
                     float beta, int cus, hipStream_t s, const char* who);
 int qgemm_q4k_fused_groups(const void* const* W, const int* row0, const int* rows, int n, size_t rb,
@@ -311,43 +313,59 @@ __global__ __launch_bounds__(256) void gemm_x3_kernel(const X3Args p) {
 }
 
 // ------------------------------------------------------ big-tile GEMM core
-// Same products as gemm_x3_kernel on a 256 x 320 workgroup tile: 8 waves (4
-// along M x 2 along N), each 64 x 160 = 2 x 5 blocks of 32x32, K step 32.  The
-// operand tiles reach LDS by global_load_lds_dwordx4 (no register staging),
-// double-buffered: after the barrier that publishes stage k, the loads of
-// stage k+1 go out into the other buffer, then stage k is multiplied.  A row of
-// 32 halfs is four 16-byte chunks, chunk c stored at slot c ^ ((row >> 2) & 3):
-// a fragment read (16 consecutive rows, one chunk) then touches 16 distinct
-// 16-byte bank groups.  Per k-substep a wave reads 2*NA + 5*NB fragments for
-// 30 MFMAs (x3-2x2), which keeps LDS below half its bandwidth at full MFMA rate.
-constexpr int XB_M = 256, XB_N = 320, XB_WM = 2, XB_WN = 5;
+// Same products as gemm_x3_kernel on a 256-row workgroup tile of 8 waves, K step
+// 32, in two shapes: 256 x 320 (4 waves along M x 2 along N, each 64 x 160 =
+// 2 x 5 blocks of 32x32) and 256 x 352 (8 waves along M, each 32 x 352 = 1 x 11
+// blocks), the second for the N that 352 covers with less padding (1408 =
+// 4 x 352, 2048 in 6 x 352 against 7 x 320).  Consecutive waves go along N
+// first, so the waves whose rows all lie past M (a routed expert's last tile)
+// sit on different SIMDs and skip their MFMAs.  The operand tiles reach LDS by
+// global_load_lds_dwordx4 (no register staging), double-buffered: after the
+// barrier that publishes stage k, the loads of stage k+1 go out into the other
+// buffer, then stage k is multiplied.  A row of 32 halfs is four 16-byte
+// chunks, chunk c stored at slot c ^ ((row >> 2) & 3): a fragment read (16
+// consecutive rows, one chunk) then touches 16 distinct 16-byte bank groups.
+// Per k-substep a wave reads NA*WM + NB*WN fragments for 3*WM*WN MFMAs (11 for
+// 30 in the 320 shape, 14 for 33 in the 352 shape, x3-ref), which keeps LDS
+// below half its bandwidth at full MFMA rate.
+constexpr int XB_M = 256;
+template <int TN>
+struct XbShape;
+template <>
+struct XbShape<320> {
+  static constexpr int WAVES_N = 2, WM = 2, WN = 5;
+};
+template <>
+struct XbShape<352> {
+  static constexpr int WAVES_N = 1, WM = 1, WN = 11;
+};
 
-template <int MODE>
-__global__ __launch_bounds__(512) void gemm_x3_big(const X3Args p) {
+// One 256 x TN output tile t of the problem p (t < ceil(M/256) * ceil(N/TN)).
+template <int MODE, int TN>
+__device__ __forceinline__ void x3_big_tile(const X3Args& p, int t) {
   using Md = X3Mode<MODE>;
-  constexpr int NA = Md::NA, NB = Md::NB;
-  constexpr int A_PART = XB_M * 64, B_PART = XB_N * 64;  // bytes of one part per stage
+  using Sh = XbShape<TN>;
+  constexpr int NA = Md::NA, NB = Md::NB, WM = Sh::WM, WN = Sh::WN, WAVES_N = Sh::WAVES_N;
+  constexpr int A_PART = XB_M * 64, B_PART = TN * 64;  // bytes of one part per stage
   constexpr int STAGE = NA * A_PART + NB * B_PART;
-  constexpr int A_INST = XB_M * 64 / 1024, B_INST = XB_N * 64 / 1024;  // 1 KiB loads per part
+  constexpr int A_INST = XB_M * 64 / 1024, B_INST = TN * 64 / 1024;  // 1 KiB loads per part
   constexpr int NINST = NA * A_INST + NB * B_INST;
   constexpr int PER_WAVE = (NINST + 7) / 8;
+  static_assert(WM * 32 * (8 / WAVES_N) == XB_M && WN * 32 * WAVES_N == TN, "wave grid covers the tile");
   extern __shared__ __attribute__((aligned(16))) uint16_t lds_h[];
   uint8_t* lds = (uint8_t*)lds_h;
 
-  // Tile order: workgroups go round-robin over the 8 XCDs, so XCD x gets the
-  // x-th eighth of the tile sequence; the sequence walks groups of 4 tile rows
-  // column by column, so an XCD's share is a compact block (4 x 8 tiles at
-  // config 2) and its L2 holds few distinct operand panels.
-  const int ntm = (p.M + XB_M - 1) / XB_M, ntn = (p.N + XB_N - 1) / XB_N, nt = ntm * ntn;
-  int t = blockIdx.x;
-  if ((nt & 7) == 0) t = (t & 7) * (nt >> 3) + (t >> 3);
+  // The tile sequence walks groups of 4 tile rows column by column.
+  const int ntm = (p.M + XB_M - 1) / XB_M, ntn = (p.N + TN - 1) / TN;
   constexpr int GM = 4;
   const int grp = t / (GM * ntn), first = grp * GM, gm = min(GM, ntm - first);
   const int tin = t - grp * GM * ntn;
   const int tm = first + tin % gm, tn = tin / gm;
-  const int m0 = tm * XB_M, n0 = tn * XB_N;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave & 3, wn = wave >> 2;
+  const int m0 = tm * XB_M, n0 = tn * TN;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  const bool live = m0 + wm * WM * 32 < p.M;  // some of the wave's rows exist
   const uint32_t lds0 = lds_addr(lds);
 
   // DMA of stage kt into buffer buf: instruction t = wave + 8u covers 16 rows
@@ -387,11 +405,11 @@ __global__ __launch_bounds__(512) void gemm_x3_big(const X3Args p) {
       if (wave + 8 * u < NINST) dma16(gsrc[u] + k0, lds0 + buf * STAGE + loff[u]);
   };
 
-  float16v acc[XB_WM][XB_WN];
+  float16v acc[WM][WN];
 #pragma unroll
-  for (int i = 0; i < XB_WM; ++i)
+  for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int j = 0; j < XB_WN; ++j)
+    for (int j = 0; j < WN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
@@ -406,55 +424,57 @@ __global__ __launch_bounds__(512) void gemm_x3_big(const X3Args p) {
     vm_wait<0>();
     __syncthreads();  // stage kt is in LDS for every wave; buffer kt+1 is free
     if (kt + 1 < nk) issue(kt + 1, (kt + 1) & 1);
+    if (!live) continue;
     const uint8_t* s = lds + (kt & 1) * STAGE;
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
       const uint32_t co = kk ? cofs1 : cofs0;
       // all fragments of the substep first, then the MFMAs product-major, so
-      // consecutive MFMAs on one accumulator are XB_WM*XB_WN apart
-      half8 af[NA][XB_WM], bf[NB][XB_WN];
+      // consecutive MFMAs on one accumulator are WM*WN apart
+      half8 af[NA][WM], bf[NB][WN];
 #pragma unroll
       for (int q = 0; q < NA; ++q)
 #pragma unroll
-        for (int i = 0; i < XB_WM; ++i)
-          af[q][i] = *(const half8*)(s + q * A_PART + (wm * 64 + i * 32) * 64 + co);
+        for (int i = 0; i < WM; ++i)
+          af[q][i] = *(const half8*)(s + q * A_PART + (wm * WM * 32 + i * 32) * 64 + co);
 #pragma unroll
       for (int q = 0; q < NB; ++q)
 #pragma unroll
-        for (int j = 0; j < XB_WN; ++j)
-          bf[q][j] = *(const half8*)(s + NA * A_PART + q * B_PART + (wn * 160 + j * 32) * 64 + co);
+        for (int j = 0; j < WN; ++j)
+          bf[q][j] = *(const half8*)(s + NA * A_PART + q * B_PART + (wn * WN * 32 + j * 32) * 64 + co);
       if constexpr (MODE != X3_2X2) {  // lo, mid, hi times the weight (tier.cpp:940, 918)
 #pragma unroll
         for (int pa = 2; pa >= 0; --pa)
 #pragma unroll
-          for (int j = 0; j < XB_WN; ++j)
+          for (int j = 0; j < WN; ++j)
 #pragma unroll
-            for (int i = 0; i < XB_WM; ++i)
+            for (int i = 0; i < WM; ++i)
               acc[i][j] = mfma16<MODE>(af[pa][i], bf[0][j], acc[i][j]);
       } else {  // hi*hi + hi*lo + lo*hi
         constexpr int PA[3] = {0, 0, 1}, PB[3] = {0, 1, 0};
 #pragma unroll
         for (int pr = 0; pr < 3; ++pr)
 #pragma unroll
-          for (int j = 0; j < XB_WN; ++j)
+          for (int j = 0; j < WN; ++j)
 #pragma unroll
-            for (int i = 0; i < XB_WM; ++i)
+            for (int i = 0; i < WM; ++i)
               acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[PA[pr]][i], bf[PB[pr]][j], acc[i][j], 0, 0, 0);
       }
     }
   }
+  if (!live) return;
 
   // epilogue: register r of lane l holds row 8*(r/4) + 4*(l/32) + r%4, column l%32
 #pragma unroll
-  for (int i = 0; i < XB_WM; ++i)
+  for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int j = 0; j < XB_WN; ++j) {
-      const int col = n0 + wn * 160 + j * 32 + (lane & 31);
+    for (int j = 0; j < WN; ++j) {
+      const int col = n0 + wn * WN * 32 + j * 32 + (lane & 31);
       if (col >= p.N) continue;
       const int eb = p.bexp ? p.bexp[col] : 0;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int row = m0 + wm * WM * 32 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         if (row >= p.M) continue;
         float v = acc[i][j][r];
         if (p.aexp || p.bexp) v = ldexpf(v, -((p.aexp ? p.aexp[row] : 0) + eb));
@@ -465,20 +485,92 @@ __global__ __launch_bounds__(512) void gemm_x3_big(const X3Args p) {
     }
 }
 
-template <int MODE>
-int launch_x3_big(const X3Args& a, hipStream_t s, const char* who) {
-  using Md = X3Mode<MODE>;
-  const int nt = ((a.M + XB_M - 1) / XB_M) * ((a.N + XB_N - 1) / XB_N);
-  constexpr size_t lds = 2 * (size_t)(Md::NA * XB_M + Md::NB * XB_N) * 64;
+template <int MODE, int TN>
+__global__ __launch_bounds__(512) void gemm_x3_big(const X3Args p) {
+  // Workgroups go round-robin over the 8 XCDs, so XCD x gets the x-th eighth of
+  // the tile sequence: a compact block of tiles (4 x 8 at 4096 x 5120) whose
+  // operand panels its L2 holds.
+  const int nt = ((p.M + XB_M - 1) / XB_M) * ((p.N + TN - 1) / TN);
+  int t = blockIdx.x;
+  if ((nt & 7) == 0) t = (t & 7) * (nt >> 3) + (t >> 3);
+  x3_big_tile<MODE, TN>(p, t);
+}
+
+// Grouped problems (routed experts): group g multiplies rows [row0[g], row0[g] +
+// rows[g]) of the A planes with its own B[g] (N x K, ldb = K) into the same rows
+// of C; its tiles are [tile0[g], tile0[g+1]) of the tile sequence.
+constexpr int X3G = 64;
+struct X3Groups {
+  int n;
+  int tile0[X3G + 1];
+  int row0[X3G];
+  int rows[X3G];
+  const uint16_t* B[X3G];
+};
+
+template <int MODE, int TN>
+__global__ __launch_bounds__(512) void gemm_x3_big_grouped(const X3Args p, const X3Groups g) {
+  // XCD x (workgroups b = x mod 8) takes the x-th contiguous share of the tile
+  // sequence, so an expert's tiles share one L2
+  const int nt = g.tile0[g.n], q8 = nt >> 3, r8 = nt & 7, x = (int)blockIdx.x & 7;
+  const int b = x * q8 + min(x, r8) + ((int)blockIdx.x >> 3);
+  int grp = 0;
+  while (grp + 1 < g.n && b >= g.tile0[grp + 1]) ++grp;
+  X3Args q = p;
+  for (int k = 0; k < 3; ++k)
+    if (q.A[k]) q.A[k] += (size_t)g.row0[grp] * p.lda;
+  q.B[0] = g.B[grp];
+  q.M = g.rows[grp];
+  q.C = p.C + (size_t)g.row0[grp] * p.ldc;
+  x3_big_tile<MODE, TN>(q, b - g.tile0[grp]);
+}
+
+// Tile width for N: 352 where it pads N less than 320 does.
+int big_tn(int N) {
+  const long p352 = (long)((N + 351) / 352) * 352, p320 = (long)((N + 319) / 320) * 320;
+  return p352 < p320 ? 352 : 320;
+}
+
+template <int MODE, int TN>
+constexpr size_t big_lds() {
+  return 2 * (size_t)(X3Mode<MODE>::NA * XB_M + X3Mode<MODE>::NB * TN) * 64;
+}
+
+template <int MODE, int TN>
+int launch_x3_big_tn(const X3Args& a, hipStream_t s, const char* who) {
+  constexpr size_t lds = big_lds<MODE, TN>();
   static_assert(lds <= 160 * 1024, "LDS budget");
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)gemm_x3_big<MODE>, hipFuncAttributeMaxDynamicSharedMemorySize,
+    hipError_t e = hipFuncSetAttribute((const void*)gemm_x3_big<MODE, TN>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                        (int)lds);
     if (e != hipSuccess) return hip_fail(e, who);
     attr_set = true;
   }
-  gemm_x3_big<MODE><<<nt, 512, lds, s>>>(a);
+  const int nt = ((a.M + XB_M - 1) / XB_M) * ((a.N + TN - 1) / TN);
+  gemm_x3_big<MODE, TN><<<nt, 512, lds, s>>>(a);
+  TM_LAUNCH_CHECK(who);
+  return TIERMM_OK;
+}
+
+template <int MODE>
+int launch_x3_big(const X3Args& a, hipStream_t s, const char* who) {
+  return big_tn(a.N) == 352 ? launch_x3_big_tn<MODE, 352>(a, s, who) : launch_x3_big_tn<MODE, 320>(a, s, who);
+}
+
+// g.tile0 counts tiles of width TN.
+template <int MODE, int TN>
+int launch_x3_big_grouped(const X3Args& a, const X3Groups& g, hipStream_t s, const char* who) {
+  constexpr size_t lds = big_lds<MODE, TN>();
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)gemm_x3_big_grouped<MODE, TN>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return hip_fail(e, who);
+    attr_set = true;
+  }
+  if (g.tile0[g.n] == 0) return TIERMM_OK;
+  gemm_x3_big_grouped<MODE, TN><<<g.tile0[g.n], 512, lds, s>>>(a, g);
   TM_LAUNCH_CHECK(who);
   return TIERMM_OK;
 }
@@ -501,7 +593,10 @@ int launch_x3(const X3Args& a, hipStream_t s, const char* who) {
 }
 
 // Tiles of the 256x320 kernel: it pays off once they occupy most of the CUs.
-long big_tiles(int M, int N) { return (long)((M + XB_M - 1) / XB_M) * ((N + XB_N - 1) / XB_N); }
+long big_tiles(int M, int N) {
+  const int tn = big_tn(N);
+  return (long)((M + XB_M - 1) / XB_M) * ((N + tn - 1) / tn);
+}
 
 int check_nt(const char* who, int M, int N, int K) {
   if (M < 0 || N < 0 || K < 0) return set_error(TIERMM_EINVAL, "%s: negative size", who);
@@ -510,6 +605,25 @@ int check_nt(const char* who, int M, int N, int K) {
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// Routed experts through the grouped 256x320 launch: the number of experts whose
+// fp16 weights are decoded at once (at most 64 and 1 GiB), or 0 when the experts'
+// 256-row tiles do not fill the chip or are mostly empty rows.
+int big_group_chunk(const int* offs, int n_experts, int N, int K) {
+  long tiles = 0, rows = 0, cap = 0;
+  for (int e = 0; e < n_experts; ++e) {
+    const int Me = offs[e + 1] - offs[e];
+    if (Me <= 0) continue;
+    tiles += big_tiles(Me, N);
+    rows += Me;
+    cap += (long)((Me + XB_M - 1) / XB_M) * XB_M;
+  }
+  if (tiles < 192 || 2 * rows < cap) return 0;
+  const size_t per = al256((size_t)N * K * sizeof(uint16_t));
+  return (int)std::max<size_t>(1, std::min<size_t>(X3G, (size_t(1) << 30) / per));
+}
 
 }  // namespace
 
@@ -696,7 +810,6 @@ int tiermm_x3_rows_bf16(const uint16_t* W, const float* x, float* y, int M, int 
   return x3_rows_impl(W, x, y, M, K, N, ldo, ws, ws_bytes, stream, true, "tiermm_x3_rows_bf16");
 }
 
-static size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 size_t tiermm_qgemm_ws_bytes(int qtype, int M, int N, int K, int mode) {
   if (mode == TIERMM_MODE_F32)  // fp32 W, its two-part split, and x's
@@ -775,9 +888,12 @@ size_t tiermm_qgemm_grouped_ws_bytes(const int* qtype_e, const int* expert_offse
     }
     return need;
   }
-  // x3-ref: the three fp16 planes of all routed rows, plus one expert's fp16 W for
-  // the experts that are not decoded inside the GEMM
+  // x3-ref: the three fp16 planes of all routed rows, plus the fp16 weights of a
+  // chunk of experts (grouped 256x320 launch) or of one expert at a time (the
+  // experts that are not decoded inside the GEMM)
   const size_t P = n_experts > 0 ? (size_t)expert_offsets[n_experts] : 0;
+  const int chunk = n_experts > 0 ? big_group_chunk(expert_offsets, n_experts, N, K) : 0;
+  if (chunk) return al256(3 * P * K * sizeof(uint16_t)) + chunk * al256((size_t)N * K * sizeof(uint16_t));
   bool staged = false;
   for (int e = 0; e < n_experts; ++e) {
     const int Me = expert_offsets[e + 1] - expert_offsets[e];
@@ -826,6 +942,48 @@ int tiermm_qgemm_grouped(const void* const* W_e, const int* qtype_e, const size_
   uint16_t* w16 = (uint16_t*)((uint8_t*)w + al256(3 * pk * sizeof(uint16_t)));
   st = split3_launch(X_sorted, parts, pk, pk, TIERMM_HML, s);
   if (st) return st;
+  const int chunk = big_group_chunk(expert_offsets, n_experts, N, K);
+  if (chunk) {  // fp16 weights of up to `chunk` experts, then one grouped launch over their tiles
+    const size_t per = al256((size_t)N * K * sizeof(uint16_t));
+    X3Args a{};
+    a.A[0] = parts; a.A[1] = parts + pk; a.A[2] = parts + 2 * pk;
+    a.lda = K; a.ldb = K; a.C = Y_sorted; a.ldc = N; a.N = N; a.K = K;
+    std::vector<int> ex;
+    for (int e = 0; e < n_experts; ++e)
+      if (expert_offsets[e + 1] > expert_offsets[e]) ex.push_back(e);
+    for (size_t c0 = 0; c0 < ex.size(); c0 += chunk) {
+      const int n = (int)std::min<size_t>(chunk, ex.size() - c0);
+      X3Groups g{};
+      g.n = n;
+      for (int i = 0; i < n; ++i) {
+        const int e = ex[c0 + i];
+        g.row0[i] = expert_offsets[e];
+        g.rows[i] = expert_offsets[e + 1] - expert_offsets[e];
+        g.B[i] = (const uint16_t*)((uint8_t*)w16 + i * per);
+        g.tile0[i + 1] = g.tile0[i] + (int)big_tiles(g.rows[i], N);
+      }
+      // one decode launch per weight type in the chunk
+      std::vector<char> done(n, 0);
+      for (int i = 0; i < n; ++i) {
+        if (done[i]) continue;
+        const int qt = qtype_e[ex[c0 + i]];
+        std::vector<const void*> src;
+        std::vector<uint16_t*> dst;
+        for (int j = i; j < n; ++j)
+          if (!done[j] && qtype_e[ex[c0 + j]] == qt) {
+            done[j] = 1;
+            src.push_back(W_e[ex[c0 + j]]);
+            dst.push_back((uint16_t*)g.B[j]);
+          }
+        st = dequant_f16_group(src.data(), dst.data(), (int)src.size(), qt, rb_e[ex[c0 + i]], K, (size_t)N, s);
+        if (st) return st;
+      }
+      st = big_tn(N) == 352 ? launch_x3_big_grouped<X3_REF, 352>(a, g, s, who)
+                            : launch_x3_big_grouped<X3_REF, 320>(a, g, s, who);
+      if (st) return st;
+    }
+    return TIERMM_OK;
+  }
   int cus = 0;
   st = device_cus(&cus);
   if (st) return st;
