@@ -66,6 +66,39 @@ def test_gemv_ragged_shapes(gpu, t, N, K):
     assert oracle.rel_fro(y, oracle.gemv_f64(blocks, t, x, N, K)) <= TOL
 
 
+@pytest.mark.parametrize("t", [tier_amd.Q8_0, tier_amd.Q4_0, tier_amd.Q4_1, tier_amd.Q5_0, tier_amd.Q5_1])
+@pytest.mark.parametrize("N,K", [(300, 14336), (9, 16384), (1029, 8192), (4100, 4096)])
+def test_gemv_block32_rows_in_lds(gpu, t, N, K):
+    """The 32-element block types staged whole in LDS: one row per wave above 80 KiB a
+    workgroup (K = 8192 .. 16384), two below; a partial last workgroup."""
+    rng = np.random.default_rng(N + K + t)
+    be, _ = oracle.block(t)
+    blocks = oracle.random_blocks(rng, t, N * (K // be)).reshape(N, -1)
+    x = rng.standard_normal(K).astype(np.float32)
+    y = _gemv(blocks, t, x, N, K)
+    assert oracle.rel_fro(y, oracle.gemv_f64(blocks, t, x, N, K)) <= TOL
+
+
+@pytest.mark.parametrize("t", [tier_amd.Q8_0, tier_amd.Q5_1])
+def test_gemv_block32_unaligned_rows(gpu, t):
+    """Weights at an address that is not 16-byte aligned take the per-element kernel;
+    both kernels meet the bar on the same rows."""
+    N, K = 200, 4096
+    rng = np.random.default_rng(t)
+    be, _ = oracle.block(t)
+    blocks = oracle.random_blocks(rng, t, N * (K // be)).reshape(N, -1)
+    x = rng.standard_normal(K).astype(np.float32)
+    rb = tier_amd.q_row_bytes(t, K)
+    W = hip.DeviceBuffer(blocks.nbytes + 16).upload(blocks, offset=2)
+    X, Y = hip.to_device(x), hip.DeviceBuffer(N * 4)
+    tier_amd.gemv_q(W.ptr + 2, t, rb, X.ptr, Y.ptr, N, K)
+    hip.synchronize()
+    want = oracle.gemv_f64(blocks, t, x, N, K)
+    y_off = Y.download(np.float32, N)
+    assert oracle.rel_fro(y_off, want) <= TOL
+    assert oracle.rel_fro(_gemv(blocks, t, x, N, K), want) <= TOL
+
+
 @pytest.mark.parametrize("N,K", [(10250, 4352), (10240, 256), (10256, 8192), (10240, 1280)])
 def test_gemv_q4k_tall_ragged(gpu, N, K):
     """Tall q4_K matrices (the producer-wave kernel): a partial last row tile, K halves of

@@ -70,25 +70,26 @@ __device__ __forceinline__ void prep_half(int s, int h, const float (&v)[16], ui
 // wave's K range re-read the last valid 16 bytes of the row segment, so the
 // number of loads is fixed.  When the stage is not a whole number of 1 KiB
 // loads, the last load runs on the lanes that still have bytes to bring.
-template <int GS>
+template <int GS, int SBB = SB_BYTES>
 struct Stage {
-  static constexpr int GRP = GS * SB_BYTES;               // bytes of one row's group
+  static constexpr int GRP = GS * SBB;                    // bytes of one row's group
   static constexpr int BYTES = 16 * GRP;                  // one stage
   static constexpr int NLD = (BYTES + 1023) / 1024;       // loads per stage
   static constexpr int LAST = (BYTES - (NLD - 1) * 1024) / 16;  // lanes of the last load
 };
 
-template <int GS>
-__device__ __forceinline__ void load_group(const uint8_t* base0, size_t rb, const int (&roff)[Stage<GS>::NLD],
-                                           const int (&coff)[Stage<GS>::NLD], int lane, int grp, int nsb,
+template <int GS, int SBB = SB_BYTES>
+__device__ __forceinline__ void load_group(const uint8_t* base0, size_t rb, const int (&roff)[Stage<GS, SBB>::NLD],
+                                           const int (&coff)[Stage<GS, SBB>::NLD], int lane, int grp, int nsb,
                                            uint32_t stage) {
-  constexpr int NLD = Stage<GS>::NLD;
+  using St = Stage<GS, SBB>;
+  constexpr int NLD = St::NLD;
   const int valid = min(GS, nsb - GS * grp);
-  const int lastb = valid > 0 ? SB_BYTES * valid - 16 : 0;
-  const uint8_t* b = base0 + (size_t)max(0, min(grp, (nsb - 1) / GS)) * Stage<GS>::GRP;
+  const int lastb = valid > 0 ? SBB * valid - 16 : 0;
+  const uint8_t* b = base0 + (size_t)max(0, min(grp, (nsb - 1) / GS)) * St::GRP;
 #pragma unroll
   for (int j = 0; j < NLD; ++j)
-    if (j < NLD - 1 || Stage<GS>::LAST == 64 || lane < Stage<GS>::LAST)
+    if (j < NLD - 1 || St::LAST == 64 || lane < St::LAST)
       dma16(b + (size_t)roff[j] * rb + min(coff[j], lastb), stage + j * 1024);
 }
 
@@ -134,6 +135,120 @@ __device__ __forceinline__ float q4k_superblock(const uint8_t* hp, int g, const 
   acc = fmaf(d, u, acc);
   return fmaf(-dmin, m, acc);
 }
+
+// Q5_K super-block (176 bytes: d, dmin, scales as Q4_K, qh[32], qs[128]; quant.h:49,
+// 85-86): the Q4_K arithmetic with the fifth bit of each weight from qh.  Element
+// 64j + l of the low (high) nibbles of qs[32j + l] takes bit 2j (2j+1) of qh[l];
+// lane group g's chunks g and g+4 cover l = 16(g&1) + [0,16), so its 16 qh bytes
+// serve all four MFMAs, with bits s0, s0+1, s0+4, s0+5 for s0 = 2(g>>1).
+// Weights reach 31: the digit combination rounds once (relative 2^-24).
+__device__ __forceinline__ float q5k_superblock(const uint8_t* hp, int g, const uint8_t* a0p, const uint8_t* a1p,
+                                                const float* mtp, float acc) {
+  const u32x4 H = *(const u32x4*)hp;
+  const u32x4 Qh = *(const u32x4*)(hp + 16 + 16 * (g & 1));
+  const u32x4 cA = *(const u32x4*)(hp + 48 + 16 * g);
+  const u32x4 cB = *(const u32x4*)(hp + 112 + 16 * g);
+  const i32x4 A0 = *(const i32x4*)(a0p), A1 = *(const i32x4*)(a1p + XQ_T);
+  const i32x4 A2 = *(const i32x4*)(a0p + 2 * XQ_T), A3 = *(const i32x4*)(a1p + 3 * XQ_T);
+  const int s0 = 2 * (g >> 1);
+  i32x4 B0, B1, B2, B3;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t qs = Qh[w] >> s0;  // bit s0 of each byte at bit 0
+    B0[w] = (int)((cA[w] & 0x0f0f0f0fu) | ((qs << 4) & 0x10101010u));
+    B1[w] = (int)(((cA[w] >> 4) & 0x0f0f0f0fu) | ((qs << 3) & 0x10101010u));
+    B2[w] = (int)((cB[w] & 0x0f0f0f0fu) | (qs & 0x10101010u));
+    B3[w] = (int)(((cB[w] >> 4) & 0x0f0f0f0fu) | ((qs >> 1) & 0x10101010u));
+  }
+  const i32x4 z = {0, 0, 0, 0};
+  i32x4 Ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, z, 0, 0, 0);
+  Ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, Ca, 0, 0, 0);
+  i32x4 Cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(A2, B2, z, 0, 0, 0);
+  Cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(A3, B3, Cb, 0, 0, 0);
+  // |C| <= 32*31*128: the halves stay exact in int32
+  const float Da = fmaf((float)(Ca[3] * 256 + Ca[2]), 65536.f, (float)(Ca[1] * 256 + Ca[0]));
+  const float Db = fmaf((float)(Cb[3] * 256 + Cb[2]), 65536.f, (float)(Cb[1] * 256 + Cb[0]));
+  const float4 mt = *(const float4*)mtp;
+  const int sh = 8 * g;
+  const uint32_t hy = H[1], hz = H[2], hw = H[3];
+  const int sca = (hy >> sh) & 63, mna = (hz >> sh) & 63;
+  const int scb = ((hw >> sh) & 15) | (((hy >> (sh + 6)) & 3) << 4);
+  const int mnb = ((hw >> (sh + 4)) & 15) | (((hz >> (sh + 6)) & 3) << 4);
+  const float d = h2f(H[0] & 0xffffu), dmin = h2f(H[0] >> 16);
+  const float u = fmaf((float)scb * mt.y, Db, (float)sca * mt.x * Da);
+  const float m = fmaf((float)mnb, mt.w, (float)mna * mt.z);
+  acc = fmaf(d, u, acc);
+  return fmaf(-dmin, m, acc);
+}
+
+// Q8_0 in groups of eight blocks (272 bytes = 256 weights, 16-byte multiple),
+// the "super-block" of the MFMA GEMV (quant.h:68).  Sub-block s is block s: its
+// scale d at byte 34s, its 32 int8 weights at 34s + 2.  For MFMA t lane group g
+// supplies weights 16(g&1) + [0,16) of block 4(t>>1) + 2(g>>1) + (t&1), whose
+// bytes sit 2 (t even) or 0 (t odd) past a dword boundary; Ca ends with block
+// g's digit dots, Cb with block 4+g's.
+__device__ __forceinline__ float q8_group(const uint8_t* hp, int g, const uint8_t* a0p, const uint8_t* a1p,
+                                          const float* mtp, float acc) {
+  i32x4 B[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int blk = 4 * (t >> 1) + 2 * (g >> 1) + (t & 1);
+    const uint32_t* q = (const uint32_t*)(hp + 34 * blk + 16 * (g & 1) + ((t & 1) ? 2 : 0));
+    if (t & 1) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) B[t][w] = (int)q[w];
+    } else {
+      uint32_t v[5];
+#pragma unroll
+      for (int w = 0; w < 5; ++w) v[w] = q[w];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) B[t][w] = (int)__builtin_amdgcn_alignbyte(v[w + 1], v[w], 2);
+    }
+  }
+  const i32x4 A0 = *(const i32x4*)(a0p), A1 = *(const i32x4*)(a1p + XQ_T);
+  const i32x4 A2 = *(const i32x4*)(a0p + 2 * XQ_T), A3 = *(const i32x4*)(a1p + 3 * XQ_T);
+  const i32x4 z = {0, 0, 0, 0};
+  i32x4 Ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B[0], z, 0, 0, 0);
+  Ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B[1], Ca, 0, 0, 0);
+  i32x4 Cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(A2, B[2], z, 0, 0, 0);
+  Cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(A3, B[3], Cb, 0, 0, 0);
+  // |C| <= 32*127*128 < 2^19: the int32 halves are exact, their conversion rounds once
+  const float Da = fmaf((float)(Ca[3] * 256 + Ca[2]), 65536.f, (float)(Ca[1] * 256 + Ca[0]));
+  const float Db = fmaf((float)(Cb[3] * 256 + Cb[2]), 65536.f, (float)(Cb[1] * 256 + Cb[0]));
+  const float4 mt = *(const float4*)mtp;
+  const float da = h2f(*(const uint16_t*)(hp + 34 * g)), db = h2f(*(const uint16_t*)(hp + 34 * (4 + g)));
+  acc = fmaf(da * mt.x, Da, acc);
+  return fmaf(db * mt.y, Db, acc);
+}
+
+// Per-format pieces of the MFMA GEMV: bytes per 256 weights and the 16-row
+// super-block step.
+template <int QT>
+struct MfmaFmt;
+template <>
+struct MfmaFmt<QT_Q4_K> {
+  static constexpr int SBB = 144;
+  __device__ static float step(const uint8_t* hp, int g, const uint8_t* a0p, const uint8_t* a1p, const float* mtp,
+                               float acc) {
+    return q4k_superblock(hp, g, a0p, a1p, mtp, acc);
+  }
+};
+template <>
+struct MfmaFmt<QT_Q5_K> {
+  static constexpr int SBB = 176;
+  __device__ static float step(const uint8_t* hp, int g, const uint8_t* a0p, const uint8_t* a1p, const float* mtp,
+                               float acc) {
+    return q5k_superblock(hp, g, a0p, a1p, mtp, acc);
+  }
+};
+template <>
+struct MfmaFmt<QT_Q8_0> {
+  static constexpr int SBB = 272;
+  __device__ static float step(const uint8_t* hp, int g, const uint8_t* a0p, const uint8_t* a1p, const float* mtp,
+                               float acc) {
+    return q8_group(hp, g, a0p, a1p, mtp, acc);
+  }
+};
 
 }  // namespace
 }  // namespace tiermm

@@ -1,5 +1,10 @@
 // qgemv.hip -- tiermm_qgemv: decode-time (M=1) dequant-GEMV, gemv_q (tier.cpp:299-306).
 //
+// Kernel per type: Q4_K, Q5_K and Q8_0 run on int8 MFMA (qgemv_q4k.hip,
+// qgemv_q4k_ws.hip); Q4_0/Q4_1/Q5_0/Q5_1 (and Q8_0 rows the MFMA kernel does not
+// take) on the staged kernel below; every other type, and rows either kernel
+// does not take, on the generic kernel.
+//
 // Generic kernel (every type): the block stages x in LDS once; each wave
 // owns R consecutive rows and its lanes walk the row in 8-element chunks
 // (lane-strided, like gemv_q's k += warpSize loop but 8 wide), decoding each
@@ -63,6 +68,174 @@ int launch_generic(const void* W, size_t rb, const float* x, float* y, int N, in
   qgemv_generic<QT, R><<<grid, 256, (size_t)K * 4, s>>>((const uint8_t*)W, rb, x, y, N, K);
   TM_LAUNCH_CHECK("tiermm_qgemv: launch");
   return TIERMM_OK;
+}
+
+// ------------------------------------------------------ staged block GEMV
+// The 32-element block types whose two-block unit is a whole number of dwords
+// (q8_0 68 B, q4_0 36, q4_1 40, q5_0 44, q5_1 48), rows 16-byte aligned.  A
+// workgroup of 4 waves owns RW = 4R consecutive rows, which are one contiguous
+// byte range of W: it copies them into LDS with global_load_lds_dwordx4 (1 KiB
+// per instruction, every byte read once, all loads issued up front) while it
+// copies x into LDS, padded 4 floats per 64 so that the lanes' 64-float units
+// start on distinct banks.  Lane l of a wave then takes the units u = l, l + 64,
+// ... (elements [64u, 64u + 64)) of the wave's R rows: 16 ds_read_b128 of x, DW
+// dwords of each row, decoded in registers.  Per block the integer values are
+// summed against x in fp32 and scaled once: d * sum(q * x) (+ m * sum(x)), the
+// same products as gemv_q's sum of q_val * x (tier.cpp:299-306) in another
+// order, within fp32 rounding of it.
+template <int QT>
+struct U2;
+template <>
+struct U2<QT_Q8_0> {  // quant.h:68
+  static constexpr int B = 34, QS = 2, M = -1, QH = -1;
+};
+template <>
+struct U2<QT_Q4_0> {  // quant.h:64
+  static constexpr int B = 18, QS = 2, M = -1, QH = -1, OFF = 8;
+};
+template <>
+struct U2<QT_Q4_1> {  // quant.h:65
+  static constexpr int B = 20, QS = 4, M = 2, QH = -1, OFF = 0;
+};
+template <>
+struct U2<QT_Q5_0> {  // quant.h:66
+  static constexpr int B = 22, QS = 6, M = -1, QH = 2, OFF = 16;
+};
+template <>
+struct U2<QT_Q5_1> {  // quant.h:67
+  static constexpr int B = 24, QS = 8, M = 2, QH = 4, OFF = 0;
+};
+
+// byte / halfword / word at byte offset i (a compile-time constant once unrolled)
+// of the dwords w; halfwords and words sit at even offsets in these layouts
+template <int NW>
+__device__ __forceinline__ uint32_t ubyte(const uint32_t (&w)[NW], int i) { return (w[i >> 2] >> (8 * (i & 3))) & 255u; }
+template <int NW>
+__device__ __forceinline__ int sbyte(const uint32_t (&w)[NW], int i) { return (int)(w[i >> 2] << (24 - 8 * (i & 3))) >> 24; }
+template <int NW>
+__device__ __forceinline__ uint32_t uhalf(const uint32_t (&w)[NW], int i) { return (w[i >> 2] >> (8 * (i & 3))) & 0xffffu; }
+template <int NW>
+__device__ __forceinline__ uint32_t uword(const uint32_t (&w)[NW], int i) {
+  return (i & 3) ? (w[i >> 2] >> 16) | (w[(i >> 2) + 1] << 16) : w[i >> 2];
+}
+
+// sum over the unit's 64 elements of q_val * x; sx[b] = sum of block b's x
+template <int QT, int NW>
+__device__ __forceinline__ float unit_dot(const uint32_t (&w)[NW], const float (&xv)[64], const float (&sx)[2]) {
+  using T = U2<QT>;
+  float acc = 0.f;
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const int o = T::B * b;
+    float sq = 0.f;
+    if constexpr (QT == QT_Q8_0) {
+#pragma unroll
+      for (int j = 0; j < 32; ++j) sq = fmaf((float)sbyte(w, o + T::QS + j), xv[32 * b + j], sq);
+    } else {
+      uint32_t qh = 0;
+      if constexpr (T::QH >= 0) qh = uword(w, o + T::QH);
+#pragma unroll
+      for (int j = 0; j < 32; ++j) {
+        int q = (int)((ubyte(w, o + T::QS + (j & 15)) >> (j < 16 ? 0 : 4)) & 15u);
+        if constexpr (T::QH >= 0) q |= (int)(((qh >> j) & 1u) << 4);
+        sq = fmaf((float)(q - T::OFF), xv[32 * b + j], sq);
+      }
+    }
+    acc = fmaf(h2f(uhalf(w, o)), sq, acc);
+    if constexpr (T::M >= 0) acc = fmaf(h2f(uhalf(w, o + T::M)), sx[b], acc);
+  }
+  return acc;
+}
+
+template <int QT, int R>
+__global__ __launch_bounds__(256) void qgemv_staged(const uint8_t* __restrict__ W, size_t rb, const float* __restrict__ x,
+                                                    float* __restrict__ y, int N, int K, uint32_t wbytes) {
+  constexpr int UB = 2 * U2<QT>::B, NW = UB / 4, RW = 4 * R;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int row0 = blockIdx.x * RW;
+  // the workgroup's rows: bytes [row0 * rb, (row0 + rows) * rb) of W; a lane past
+  // them re-reads the last 16 bytes into the slack after the image
+  const uint32_t total = (uint32_t)min(RW, N - row0) * (uint32_t)rb;
+  const uint8_t* g0 = W + (size_t)row0 * rb;
+  const uint32_t l0 = lds_addr(smem);
+  const int ni = (int)((total + 1023) / 1024);
+  for (int i = wave; i < ni; i += 4) {
+    const uint32_t off = (uint32_t)i * 1024 + 16 * lane;
+    dma16(g0 + min(off, total - 16), l0 + (uint32_t)i * 1024);
+  }
+  float* xs = (float*)(smem + wbytes);
+  for (int i = tid * 4; i < K; i += 1024) *(float4*)&xs[i + (i >> 6) * 4] = *(const float4*)&x[i];
+  vm_wait<0>();
+  __syncthreads();
+
+  const int U = K / 64;
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.f;
+  for (int u = lane; u < U; u += 64) {
+    float xv[64];
+    const float* xp = xs + 68 * u;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float4 t = *(const float4*)(xp + 4 * i);
+      xv[4 * i] = t.x; xv[4 * i + 1] = t.y; xv[4 * i + 2] = t.z; xv[4 * i + 3] = t.w;
+    }
+    float sx[2] = {0.f, 0.f};
+    if constexpr (U2<QT>::M >= 0) {
+#pragma unroll
+      for (int j = 0; j < 32; ++j) {
+        sx[0] += xv[j];
+        sx[1] += xv[32 + j];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint32_t* wp = (const uint32_t*)(smem + (size_t)(wave * R + r) * rb + (size_t)UB * u);
+      uint32_t w[NW];
+#pragma unroll
+      for (int i = 0; i < NW; ++i) w[i] = wp[i];
+      acc[r] += unit_dot<QT>(w, xv, sx);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const float v = wave_sum(acc[r]);
+    const int row = row0 + wave * R + r;
+    if (lane == 0 && row < N) y[row] = v;
+  }
+}
+
+// LDS of the staged kernel: the rows (whole KiB) plus padded x.
+size_t staged_lds(size_t rb, int K, int R) { return (4 * R * rb + 1023) / 1024 * 1024 + (size_t)K / 64 * 68 * 4; }
+
+template <int QT>
+int launch_staged(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
+  // two rows per wave while two workgroups fit a CU, else one
+  const int R = staged_lds(rb, K, 2) <= 80 * 1024 ? 2 : 1;
+  const size_t lds = staged_lds(rb, K, R);
+  const uint32_t wbytes = (uint32_t)((4 * R * rb + 1023) / 1024 * 1024);
+  const unsigned grid = (unsigned)((N + 4 * R - 1) / (4 * R));
+  static bool attr_set = false;
+  if (!attr_set) {
+    for (auto f : {(const void*)qgemv_staged<QT, 1>, (const void*)qgemv_staged<QT, 2>}) {
+      hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+      if (e != hipSuccess) return hip_fail(e, "tiermm_qgemv");
+    }
+    attr_set = true;
+  }
+  if (R == 2)
+    qgemv_staged<QT, 2><<<grid, 256, lds, s>>>((const uint8_t*)W, rb, x, y, N, K, wbytes);
+  else
+    qgemv_staged<QT, 1><<<grid, 256, lds, s>>>((const uint8_t*)W, rb, x, y, N, K, wbytes);
+  TM_LAUNCH_CHECK("tiermm_qgemv: launch");
+  return TIERMM_OK;
+}
+
+// The staged kernel takes the shape: 64-element units, rows and base 16-byte
+// aligned, and one workgroup's rows plus x within the LDS.
+bool staged_fits(const void* W, size_t rb, int K) {
+  return K % 64 == 0 && rb % 16 == 0 && ((uintptr_t)W % 16) == 0 && staged_lds(rb, K, 1) <= 160 * 1024;
 }
 
 // ------------------------------------------------------- dense-row GEMV
@@ -165,6 +338,8 @@ int launch_dense(const void* W, const float* x, float* y, int N, int K, hipStrea
 
 int qgemv_q4k(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s);
 int qgemv_q4k_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s);
+bool qgemv_mfma_fits(const void* W, int qtype, size_t rb, int K);
+int qgemv_mfma(const void* W, int qtype, size_t rb, const float* x, float* y, int N, int K, hipStream_t s);
 constexpr int kQ4kMaxK = 14336;  // equals the limit in qgemv_q4k.hip
 
 int qgemv_dispatch(const void* W, int qtype, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
@@ -176,6 +351,25 @@ int qgemv_dispatch(const void* W, int qtype, size_t rb, const float* x, float* y
     case QT_Q4_K:  // MFMA kernels up to kQ4kMaxK (x digits in LDS); beyond, the generic kernel
       if (K <= 8192 && (N + 15) / 16 >= 640) return qgemv_q4k_ws(W, rb, x, y, N, K, s);
       return K <= kQ4kMaxK ? qgemv_q4k(W, rb, x, y, N, K, s) : launch_generic<QT_Q4_K>(W, rb, x, y, N, K, s);
+    case QT_Q8_0:  // int8 MFMA kernel; rows that do not fit it staged whole in LDS
+      if (qgemv_mfma_fits(W, qtype, rb, K)) return qgemv_mfma(W, qtype, rb, x, y, N, K, s);
+      if (staged_fits(W, rb, K)) return launch_staged<QT_Q8_0>(W, rb, x, y, N, K, s);
+      return launch_generic<QT_Q8_0>(W, rb, x, y, N, K, s);
+    case QT_Q5_K:
+      if (qgemv_mfma_fits(W, qtype, rb, K)) return qgemv_mfma(W, qtype, rb, x, y, N, K, s);
+      return launch_generic<QT_Q5_K>(W, rb, x, y, N, K, s);
+    case QT_Q4_0:
+      if (staged_fits(W, rb, K)) return launch_staged<QT_Q4_0>(W, rb, x, y, N, K, s);
+      return launch_generic<QT_Q4_0>(W, rb, x, y, N, K, s);
+    case QT_Q4_1:
+      if (staged_fits(W, rb, K)) return launch_staged<QT_Q4_1>(W, rb, x, y, N, K, s);
+      return launch_generic<QT_Q4_1>(W, rb, x, y, N, K, s);
+    case QT_Q5_0:
+      if (staged_fits(W, rb, K)) return launch_staged<QT_Q5_0>(W, rb, x, y, N, K, s);
+      return launch_generic<QT_Q5_0>(W, rb, x, y, N, K, s);
+    case QT_Q5_1:
+      if (staged_fits(W, rb, K)) return launch_staged<QT_Q5_1>(W, rb, x, y, N, K, s);
+      return launch_generic<QT_Q5_1>(W, rb, x, y, N, K, s);
     default:
       return with_qtype(qtype, [&](auto qt) { return launch_generic<decltype(qt)::value>(W, rb, x, y, N, K, s); });
   }

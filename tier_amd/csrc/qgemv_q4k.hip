@@ -1,4 +1,5 @@
-// qgemv_q4k.hip -- Q4_K decode GEMV on int8 MFMA (the north-star path).
+// qgemv_q4k.hip -- Q4_K decode GEMV on int8 MFMA (the north-star path), and
+// Q5_K / Q8_0 on the same kernel (their per-super-block step in q4k_mfma.h).
 //
 // y[n] = sum_k q_val(W_n, k) * x[k] for Q4_K rows (gemv_q, tier.cpp:299-306),
 // reorganised so the bulk of the work runs on v_mfma_i32_16x16x64_i8:
@@ -47,12 +48,14 @@ namespace {
 // STAGES groups in flight per wave; XP x half-sub-blocks per thread at most;
 // XK the largest K (sizes the x-digit LDS object -- a static object of its own,
 // so the compiler can tell it apart from the DMA ring).
-template <int RT, int KS, int GS, int STAGES, int XP, int XK>
+template <int QT, int RT, int KS, int GS, int STAGES, int XP, int XK>
 __global__ __launch_bounds__(64 * RT * KS) void qgemv_q4k_mfma(const uint8_t* __restrict__ W, size_t rb,
                                                             const float* __restrict__ x, float* __restrict__ y,
                                                             int N, int K) {
+  using F = MfmaFmt<QT>;
+  using St = Stage<GS, F::SBB>;
   constexpr int NT = 64 * RT * KS;
-  constexpr int GRP = Stage<GS>::GRP, SBYTES = Stage<GS>::BYTES, NLD = Stage<GS>::NLD;
+  constexpr int GRP = St::GRP, SBYTES = St::BYTES, NLD = St::NLD;
   extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // RT*KS*STAGES*SBYTES + RT*KS*64
   __shared__ __attribute__((aligned(16))) uint8_t xlds[xq_bytes(XK)];
   const int nsb_all = K >> 8;
@@ -69,7 +72,7 @@ __global__ __launch_bounds__(64 * RT * KS) void qgemv_q4k_mfma(const uint8_t* __
   // per-lane DMA source: row (clamped to N-1) and byte within the group image
   const int rbase = min(row0, N - 1);                  // a tile past N re-reads row N-1
   const int rmax = min(15, N - 1 - rbase);
-  const uint8_t* base0 = W + (size_t)rbase * rb + (size_t)sbk * SB_BYTES;
+  const uint8_t* base0 = W + (size_t)rbase * rb + (size_t)sbk * F::SBB;
   int roff[NLD], coff[NLD];
 #pragma unroll
   for (int j = 0; j < NLD; ++j) {
@@ -94,7 +97,7 @@ __global__ __launch_bounds__(64 * RT * KS) void qgemv_q4k_mfma(const uint8_t* __
   }
 #pragma unroll
   for (int p = 0; p < STAGES - 1; ++p)
-    load_group<GS>(base0, rb, roff, coff, lane, p, nsb, ring_lds + p * SBYTES);
+    load_group<GS, F::SBB>(base0, rb, roff, coff, lane, p, nsb, ring_lds + p * SBYTES);
   vm_wait<NLD * (STAGES - 1)>();  // x has landed; the weight groups stay in flight
 #pragma unroll
   for (int j = 0; j < XP; ++j)
@@ -128,14 +131,14 @@ __global__ __launch_bounds__(64 * RT * KS) void qgemv_q4k_mfma(const uint8_t* __
   float acc = 0.f;
 
   auto superblock = [&](const uint8_t* st, int i, int sb) __attribute__((always_inline)) {
-    acc = q4k_superblock(st + n * GRP + i * SB_BYTES, g, xlds + aoff[0] + (uint32_t)sb * astep[0],
+    acc = F::step(st + n * GRP + i * F::SBB, g, xlds + aoff[0] + (uint32_t)sb * astep[0],
                          xlds + aoff[1] + (uint32_t)sb * astep[1], meta + (sbk + sb) * 16 + g * 4, acc);
   };
 
   for (int grp = 0; grp < ngrp; ++grp) {
     // keep STAGES-1 groups in flight: issue group grp+STAGES-1 (a clamped re-read
     // past the end keeps the count of outstanding loads fixed), then wait for grp
-    load_group<GS>(base0, rb, roff, coff, lane, grp + STAGES - 1, nsb,
+    load_group<GS, F::SBB>(base0, rb, roff, coff, lane, grp + STAGES - 1, nsb,
                    ring_lds + ((grp + STAGES - 1) % STAGES) * SBYTES);
     vm_wait<NLD * (STAGES - 1)>();  // group grp has landed in its stage
     const uint8_t* st = myring + (grp % STAGES) * SBYTES;
@@ -167,21 +170,21 @@ __global__ __launch_bounds__(64 * RT * KS) void qgemv_q4k_mfma(const uint8_t* __
   }
 }
 
-template <int RT, int KS, int GS, int STAGES, int XP, int XK>
+template <int QT, int RT, int KS, int GS, int STAGES, int XP, int XK>
 int launch(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
-  constexpr size_t lds = (size_t)RT * KS * (STAGES * Stage<GS>::BYTES + 64);  // plus the static x digits
+  constexpr size_t lds = (size_t)RT * KS * (STAGES * Stage<GS, MfmaFmt<QT>::SBB>::BYTES + 64);  // plus the static x digits
   static_assert(xq_bytes(XK) + lds <= 160 * 1024, "LDS budget");
   static_assert(XK / 16 <= 64 * RT * KS * XP, "x preparation: one thread per 16 elements");
   const int tiles = (N + 15) / 16;
   const unsigned grid = (unsigned)((tiles + RT - 1) / RT);
   static bool attr_set = false;  // dynamic LDS above 64 KiB is opted into once per instantiation
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)qgemv_q4k_mfma<RT, KS, GS, STAGES, XP, XK>,
+    hipError_t e = hipFuncSetAttribute((const void*)qgemv_q4k_mfma<QT, RT, KS, GS, STAGES, XP, XK>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return hip_fail(e, "tiermm_qgemv: q4_K LDS attribute");
     attr_set = true;
   }
-  qgemv_q4k_mfma<RT, KS, GS, STAGES, XP, XK><<<grid, 64 * RT * KS, lds, s>>>((const uint8_t*)W, rb, x, y, N, K);
+  qgemv_q4k_mfma<QT, RT, KS, GS, STAGES, XP, XK><<<grid, 64 * RT * KS, lds, s>>>((const uint8_t*)W, rb, x, y, N, K);
   TM_LAUNCH_CHECK("tiermm_qgemv: q4_K launch");
   return TIERMM_OK;
 }
@@ -194,12 +197,41 @@ constexpr int kQ4kMaxK = 14336;
 int qgemv_q4k(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
   if (K > kQ4kMaxK) return set_error(TIERMM_UNSUPPORTED, "tiermm_qgemv: q4_K K=%d above %d", K, kQ4kMaxK);
   const int tiles = (N + 15) / 16;
+  if (tiles <= 256 && K <= 5120) return launch<QT_Q4_K, 1, 4, 1, 3, 2, 5120>(W, rb, x, y, N, K, s);
   // Two row tiles x two K-halves per workgroup; the x digits are sized for the
   // smallest K class that holds K, which leaves room for more workgroups per CU.
-  if (K <= 5120) return launch<2, 2, 2, 3, 2, 5120>(W, rb, x, y, N, K, s);
-  if (K <= 8192) return launch<2, 2, 2, 3, 2, 8192>(W, rb, x, y, N, K, s);
-  if (tiles >= 640) return launch<4, 1, 4, 2, 4, 14336>(W, rb, x, y, N, K, s);
-  return launch<2, 2, 4, 2, 4, 14336>(W, rb, x, y, N, K, s);
+  if (K <= 5120) return launch<QT_Q4_K, 2, 2, 2, 3, 2, 5120>(W, rb, x, y, N, K, s);
+  if (K <= 8192) return launch<QT_Q4_K, 2, 2, 2, 3, 2, 8192>(W, rb, x, y, N, K, s);
+  if (tiles >= 640) return launch<QT_Q4_K, 4, 1, 4, 2, 4, 14336>(W, rb, x, y, N, K, s);
+  return launch<QT_Q4_K, 2, 2, 4, 2, 4, 14336>(W, rb, x, y, N, K, s);
+}
+
+// Q5_K (176-byte super-blocks) and Q8_0 (groups of eight 34-byte blocks) on the
+// same kernel: K a multiple of 256 up to kQ4kMaxK, rows and base 16-byte aligned.
+bool qgemv_mfma_fits(const void* W, int qtype, size_t rb, int K) {
+  return (qtype == QT_Q5_K || qtype == QT_Q8_0) && K % 256 == 0 && K <= kQ4kMaxK && rb % 16 == 0 &&
+         ((uintptr_t)W % 16) == 0;
+}
+
+int qgemv_mfma(const void* W, int qtype, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
+  const int tiles = (N + 15) / 16;
+  // at most one row tile per CU: one tile per workgroup, K in four parts (q8_0
+  // 4096x4096: 5.7 against 7.6 us with two tiles x two parts per workgroup)
+  if (tiles <= 256 && K <= 5120) {
+    if (qtype == QT_Q5_K) return launch<QT_Q5_K, 1, 4, 1, 3, 2, 5120>(W, rb, x, y, N, K, s);
+    return launch<QT_Q8_0, 1, 4, 1, 3, 2, 5120>(W, rb, x, y, N, K, s);
+  }
+  if (qtype == QT_Q5_K) {
+    if (K <= 5120) return launch<QT_Q5_K, 2, 2, 2, 3, 2, 5120>(W, rb, x, y, N, K, s);
+    if (K <= 8192) return launch<QT_Q5_K, 2, 2, 2, 3, 2, 8192>(W, rb, x, y, N, K, s);
+    if (tiles >= 640) return launch<QT_Q5_K, 4, 1, 4, 2, 4, 14336>(W, rb, x, y, N, K, s);
+    return launch<QT_Q5_K, 2, 2, 4, 2, 4, 14336>(W, rb, x, y, N, K, s);
+  }
+  // one 272-byte group per stage row keeps two workgroups on a CU up to K = 5120
+  if (K <= 5120) return launch<QT_Q8_0, 2, 2, 1, 3, 2, 5120>(W, rb, x, y, N, K, s);
+  if (K <= 8192) return launch<QT_Q8_0, 2, 2, 1, 3, 2, 8192>(W, rb, x, y, N, K, s);
+  if (tiles >= 640) return launch<QT_Q8_0, 4, 1, 2, 2, 4, 14336>(W, rb, x, y, N, K, s);
+  return launch<QT_Q8_0, 2, 2, 2, 2, 4, 14336>(W, rb, x, y, N, K, s);
 }
 
 }  // namespace tiermm
