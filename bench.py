@@ -356,7 +356,9 @@ def main() -> int:
         for name, qt, N, K in (("q4_K_5120x5120_m1", tier_amd.Q4_K, 5120, 5120),
                                ("q4_K_14336x5120_m1", tier_amd.Q4_K, 14336, 5120),
                                ("q4_K_5120x14336_m1", tier_amd.Q4_K, 5120, 14336),
-                               ("q8_0_4096x4096_m1", tier_amd.Q8_0, 4096, 4096)):
+                               ("q8_0_4096x4096_m1", tier_amd.Q8_0, 4096, 4096),
+                               ("q5_K_5120x14336_m1", tier_amd.Q5_K, 5120, 14336),
+                               ("q6_K_5120x14336_m1", tier_amd.Q6_K, 5120, 14336)):
             log(f"bench: {name}")
             c = GemvCase(tier_amd, hip, qt, N, K, seed=N + K)
             km = time_launches(hip, stream, lambda i: c.launch(tier_amd, i, stream), reps, warm)

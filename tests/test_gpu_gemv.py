@@ -79,6 +79,23 @@ def test_gemv_block32_rows_in_lds(gpu, t, N, K):
     assert oracle.rel_fro(y, oracle.gemv_f64(blocks, t, x, N, K)) <= TOL
 
 
+@pytest.mark.parametrize("N,K", [(8, 256), (24, 768), (40, 5120), (1000, 2304), (1024, 4096), (10240, 5120),
+                                 (2000, 14336), (10240, 8192), (10240, 14336)])
+def test_gemv_q6k_mfma(gpu, N, K):
+    """Q6_K on int8 MFMA: 210-byte super-blocks leave rows at every even shift in
+    their 16-byte window; one to four K parts per row tile; every launch shape."""
+    rng = np.random.default_rng(N + K)
+    t = tier_amd.Q6_K
+    blocks = oracle.random_blocks(rng, t, N * (K // 256)).reshape(N, -1)
+    x = rng.standard_normal(K).astype(np.float32)
+    y = _gemv(blocks, t, x, N, K)
+    assert oracle.rel_fro(y, oracle.gemv_f64(blocks, t, x, N, K)) <= TOL
+    # per row as well: a row read at a wrong shift stands out
+    want = oracle.gemv_f64(blocks, t, x, N, K)
+    err = np.abs(y - want) / np.maximum(np.abs(want), 1e-3 * np.abs(want).max())
+    assert err.max() <= 1e-4
+
+
 @pytest.mark.parametrize("t", [tier_amd.Q8_0, tier_amd.Q5_1])
 def test_gemv_block32_unaligned_rows(gpu, t):
     """Weights at an address that is not 16-byte aligned take the per-element kernel;
@@ -99,7 +116,20 @@ def test_gemv_block32_unaligned_rows(gpu, t):
     assert oracle.rel_fro(_gemv(blocks, t, x, N, K), want) <= TOL
 
 
-@pytest.mark.parametrize("N,K", [(10250, 4352), (10240, 256), (10256, 8192), (10240, 1280)])
+@pytest.mark.parametrize("t", [tier_amd.Q5_K, tier_amd.Q8_0])
+@pytest.mark.parametrize("N,K", [(10250, 5120), (10256, 8192), (10240, 14336), (5000, 7936), (3000, 14336)])
+def test_gemv_mfma_tall(gpu, t, N, K):
+    """q5_K / q8_0 on the int8-MFMA kernel with more row tiles than CUs (eight waves a
+    workgroup) and ragged row counts, at each K class."""
+    rng = np.random.default_rng(N + K + t)
+    be, _ = oracle.block(t)
+    blocks = oracle.random_blocks(rng, t, N * (K // be)).reshape(N, -1)
+    x = rng.standard_normal(K).astype(np.float32)
+    y = _gemv(blocks, t, x, N, K)
+    assert oracle.rel_fro(y, oracle.gemv_f64(blocks, t, x, N, K)) <= TOL
+
+
+@pytest.mark.parametrize("N,K", [(10250, 4352), (10240, 256), (10256, 8192), (10240, 1280), (10250, 14336)])
 def test_gemv_q4k_tall_ragged(gpu, N, K):
     """Tall q4_K matrices (the producer-wave kernel): a partial last row tile, K halves of
     unequal super-block counts (17 = 8 + 9), a half with no super-block (K = 256)."""

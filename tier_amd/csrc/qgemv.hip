@@ -1,7 +1,7 @@
 // qgemv.hip -- tiermm_qgemv: decode-time (M=1) dequant-GEMV, gemv_q (tier.cpp:299-306).
 //
-// Kernel per type: Q4_K, Q5_K and Q8_0 run on int8 MFMA (qgemv_q4k.hip,
-// qgemv_q4k_ws.hip); Q4_0/Q4_1/Q5_0/Q5_1 (and Q8_0 rows the MFMA kernel does not
+// Kernel per type: Q4_K, Q5_K, Q6_K and Q8_0 run on int8 MFMA (qgemv_q4k.hip,
+// qgemv_q4k_ws.hip, qgemv_q6k.hip); Q4_0/Q4_1/Q5_0/Q5_1 (and Q8_0 rows the MFMA kernel does not
 // take) on the staged kernel below; every other type, and rows either kernel
 // does not take, on the generic kernel.
 //
@@ -339,6 +339,8 @@ int launch_dense(const void* W, const float* x, float* y, int N, int K, hipStrea
 int qgemv_q4k(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s);
 int qgemv_q4k_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s);
 bool qgemv_mfma_fits(const void* W, int qtype, size_t rb, int K);
+bool qgemv_q6k_fits(const void* W, size_t rb, int N, int K);
+int qgemv_q6k(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s);
 int qgemv_mfma(const void* W, int qtype, size_t rb, const float* x, float* y, int N, int K, hipStream_t s);
 constexpr int kQ4kMaxK = 14336;  // equals the limit in qgemv_q4k.hip
 
@@ -358,6 +360,9 @@ int qgemv_dispatch(const void* W, int qtype, size_t rb, const float* x, float* y
     case QT_Q5_K:
       if (qgemv_mfma_fits(W, qtype, rb, K)) return qgemv_mfma(W, qtype, rb, x, y, N, K, s);
       return launch_generic<QT_Q5_K>(W, rb, x, y, N, K, s);
+    case QT_Q6_K:
+      if (qgemv_q6k_fits(W, rb, N, K)) return qgemv_q6k(W, rb, x, y, N, K, s);
+      return launch_generic<QT_Q6_K>(W, rb, x, y, N, K, s);
     case QT_Q4_0:
       if (staged_fits(W, rb, K)) return launch_staged<QT_Q4_0>(W, rb, x, y, N, K, s);
       return launch_generic<QT_Q4_0>(W, rb, x, y, N, K, s);

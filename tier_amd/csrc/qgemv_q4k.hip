@@ -194,16 +194,20 @@ int launch(const void* W, size_t rb, const float* x, float* y, int N, int K, hip
 // Largest K handled (the x digits of the whole row stay in LDS).
 constexpr int kQ4kMaxK = 14336;
 
+// Launch shapes by measurement (MI355X; 200 launches over rotated copies).  At
+// most one row tile per CU: one tile per workgroup, K in four parts (q8_0
+// 4096x4096: 5.7 against 8.0 us).  Many row tiles: eight waves per workgroup
+// (q5_K 13824x5120: 11.7 against 15.1 us; q8_0 14336x14336: 41.5 against 46.6 us).
 int qgemv_q4k(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
   if (K > kQ4kMaxK) return set_error(TIERMM_UNSUPPORTED, "tiermm_qgemv: q4_K K=%d above %d", K, kQ4kMaxK);
   const int tiles = (N + 15) / 16;
-  if (tiles <= 256 && K <= 5120) return launch<QT_Q4_K, 1, 4, 1, 3, 2, 5120>(W, rb, x, y, N, K, s);
-  // Two row tiles x two K-halves per workgroup; the x digits are sized for the
-  // smallest K class that holds K, which leaves room for more workgroups per CU.
-  if (K <= 5120) return launch<QT_Q4_K, 2, 2, 2, 3, 2, 5120>(W, rb, x, y, N, K, s);
+  if (K <= 5120) {
+    if (tiles <= 256) return launch<QT_Q4_K, 1, 4, 1, 3, 2, 5120>(W, rb, x, y, N, K, s);
+    return launch<QT_Q4_K, 2, 2, 2, 3, 2, 5120>(W, rb, x, y, N, K, s);
+  }
   if (K <= 8192) return launch<QT_Q4_K, 2, 2, 2, 3, 2, 8192>(W, rb, x, y, N, K, s);
-  if (tiles >= 640) return launch<QT_Q4_K, 4, 1, 4, 2, 4, 14336>(W, rb, x, y, N, K, s);
-  return launch<QT_Q4_K, 2, 2, 4, 2, 4, 14336>(W, rb, x, y, N, K, s);
+  if (tiles >= 640) return launch<QT_Q4_K, 4, 1, 4, 2, 4, 14336>(W, rb, x, y, N, K, s);  // 24.2 against 25.5 us
+  return launch<QT_Q4_K, 2, 4, 2, 2, 2, 14336>(W, rb, x, y, N, K, s);
 }
 
 // Q5_K (176-byte super-blocks) and Q8_0 (groups of eight 34-byte blocks) on the
@@ -215,22 +219,29 @@ bool qgemv_mfma_fits(const void* W, int qtype, size_t rb, int K) {
 
 int qgemv_mfma(const void* W, int qtype, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
   const int tiles = (N + 15) / 16;
-  // at most one row tile per CU: one tile per workgroup, K in four parts (q8_0
-  // 4096x4096: 5.7 against 7.6 us with two tiles x two parts per workgroup)
-  if (tiles <= 256 && K <= 5120) {
-    if (qtype == QT_Q5_K) return launch<QT_Q5_K, 1, 4, 1, 3, 2, 5120>(W, rb, x, y, N, K, s);
-    return launch<QT_Q8_0, 1, 4, 1, 3, 2, 5120>(W, rb, x, y, N, K, s);
-  }
   if (qtype == QT_Q5_K) {
-    if (K <= 5120) return launch<QT_Q5_K, 2, 2, 2, 3, 2, 5120>(W, rb, x, y, N, K, s);
-    if (K <= 8192) return launch<QT_Q5_K, 2, 2, 2, 3, 2, 8192>(W, rb, x, y, N, K, s);
-    if (tiles >= 640) return launch<QT_Q5_K, 4, 1, 4, 2, 4, 14336>(W, rb, x, y, N, K, s);
-    return launch<QT_Q5_K, 2, 2, 4, 2, 4, 14336>(W, rb, x, y, N, K, s);
+    if (K <= 5120) {
+      if (tiles <= 256) return launch<QT_Q5_K, 1, 4, 1, 3, 2, 5120>(W, rb, x, y, N, K, s);
+      if (tiles < 640) return launch<QT_Q5_K, 2, 4, 1, 2, 2, 5120>(W, rb, x, y, N, K, s);
+      return launch<QT_Q5_K, 4, 2, 2, 2, 2, 5120>(W, rb, x, y, N, K, s);
+    }
+    if (K <= 8192) {
+      if (tiles < 640) return launch<QT_Q5_K, 2, 2, 2, 3, 2, 8192>(W, rb, x, y, N, K, s);
+      return launch<QT_Q5_K, 4, 2, 2, 2, 2, 8192>(W, rb, x, y, N, K, s);
+    }
+    if (tiles >= 640) return launch<QT_Q5_K, 4, 2, 1, 2, 2, 14336>(W, rb, x, y, N, K, s);
+    return launch<QT_Q5_K, 2, 4, 2, 2, 2, 14336>(W, rb, x, y, N, K, s);
   }
-  // one 272-byte group per stage row keeps two workgroups on a CU up to K = 5120
-  if (K <= 5120) return launch<QT_Q8_0, 2, 2, 1, 3, 2, 5120>(W, rb, x, y, N, K, s);
-  if (K <= 8192) return launch<QT_Q8_0, 2, 2, 1, 3, 2, 8192>(W, rb, x, y, N, K, s);
-  if (tiles >= 640) return launch<QT_Q8_0, 4, 1, 2, 2, 4, 14336>(W, rb, x, y, N, K, s);
+  if (K <= 5120) {
+    if (tiles <= 256) return launch<QT_Q8_0, 1, 4, 1, 3, 2, 5120>(W, rb, x, y, N, K, s);
+    if (tiles < 640) return launch<QT_Q8_0, 2, 2, 1, 3, 2, 5120>(W, rb, x, y, N, K, s);
+    return launch<QT_Q8_0, 4, 2, 2, 2, 2, 5120>(W, rb, x, y, N, K, s);
+  }
+  if (K <= 8192) {
+    if (tiles < 640) return launch<QT_Q8_0, 2, 2, 1, 3, 2, 8192>(W, rb, x, y, N, K, s);
+    return launch<QT_Q8_0, 4, 2, 1, 2, 2, 8192>(W, rb, x, y, N, K, s);
+  }
+  if (tiles >= 640) return launch<QT_Q8_0, 4, 2, 1, 2, 2, 14336>(W, rb, x, y, N, K, s);
   return launch<QT_Q8_0, 2, 2, 2, 2, 4, 14336>(W, rb, x, y, N, K, s);
 }
 
