@@ -7,17 +7,18 @@
 // them.
 //
 // Tiling: a workgroup owns BM=128 rows of X x BN rows of W (BN in 64..128, a
-// multiple of 16 picked per shape so the tile count fills the CUs); 4 waves,
-// wave w the X rows [32w, 32w+32) against all BN columns, on
-// v_mfma_f32_16x16x32_f16 (2 x BN/16 blocks per wave).  K advances 32 per
-// stage (one q4_K sub-block):
-//   * the three x parts (pre-split, HML planes) reach LDS by
-//     global_load_lds_dwordx4, double-buffered;
-//   * thread (r, h) of the first 2*BN decodes elements [16h, 16h+16) of the
-//     sub-block of W row r: its raw header and 16 qs bytes are loaded two stages
-//     ahead into registers, decoded exactly as q_val (d*sc*q - dmin*m, one
-//     rounding), rounded to fp16 (v_cvt, RNE) and stored in the other B buffer
-//     while the current stage's MFMAs run.
+// multiple of 16 picked per shape so the tile count fills the CUs); 8 waves, two
+// per SIMD: wave w the X rows [32(w%4), 32(w%4)+32) against the 16-column blocks
+// j = 2jj + w/4 (every other block), on v_mfma_f32_16x16x32_f16.  K advances 32
+// per stage (one q4_K sub-block):
+//   * the three x parts (pre-split, HML planes) and the raw weight bytes reach
+//     LDS by global_load_lds_dwordx4;
+//   * thread (r, h) of waves 4..7 decodes elements [16h, 16h+16) of the
+//     sub-block of W row r from the raw bytes, exactly as q_val (d*sc*q -
+//     dmin*m, one rounding), rounds to fp16 (v_cvt, RNE) and stores them in the
+//     other B buffer while the current stage's MFMAs run.  Waves 0..3 only
+//     multiply, so each SIMD has one wave with MFMAs to issue while the other
+//     decodes or waits on LDS.
 // LDS rows hold 32 halfs as four 16-byte chunks, chunk c at slot
 // c ^ ((row >> 2) & 3), so the fragment reads (16 rows x 4 chunks) hit
 // distinct bank groups.
@@ -55,8 +56,8 @@ struct QArgs {
 __device__ __forceinline__ uint32_t swz(int row, int chunk) { return (uint32_t)(row * 64 + ((chunk ^ ((row >> 2) & 3)) * 16)); }
 
 template <int BN>
-__global__ __launch_bounds__(256) void qgemm_q4k_x3ref(const QArgs p) {
-  constexpr int NB = BN / 16;
+__global__ __launch_bounds__(512) void qgemm_q4k_x3ref(const QArgs p) {
+  constexpr int NB = BN / 16, NBW = (NB + 1) / 2;  // blocks in the tile, per wave
   constexpr int BPART = BN * 64;
   constexpr int XSTAGE = 3 * XPART;
   constexpr int BOFF = XRING * XSTAGE;                 // the two B buffers follow the x ring
@@ -83,21 +84,23 @@ __global__ __launch_bounds__(256) void qgemm_q4k_x3ref(const QArgs p) {
   const uint16_t* Xg = p.X + (size_t)p.row0[grp] * p.K;
   float* Yg = p.Y + (size_t)p.row0[grp] * p.ldy;
   const uint8_t* Wg = p.W[grp];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 3, wn = wave >> 2;
 
-  // x DMA: 3 parts x 8 loads of 16 rows per stage, 6 per wave
-  const uint16_t* xsrc[6];
-  uint32_t xoff[6];
+  // x DMA: 3 parts x 8 loads of 16 rows per stage, 3 per wave
+  const uint16_t* xsrc[3];
+  uint32_t xoff[3];
 #pragma unroll
-  for (int u = 0; u < 6; ++u) {
-    const int t = wave + 4 * u, part = t >> 3, ch = t & 7;
+  for (int u = 0; u < 3; ++u) {
+    const int t = wave + 8 * u, part = t >> 3, ch = t & 7;
     const int row = ch * 16 + (lane >> 2), slot = lane & 3;
     xsrc[u] = Xg + part * p.xs + (size_t)min(m0 + row, M - 1) * p.K + 8 * (slot ^ ((row >> 2) & 3));
     xoff[u] = (uint32_t)(part * XPART + ch * 1024);
   }
   auto issue_x = [&](int kt) __attribute__((always_inline)) {
 #pragma unroll
-    for (int u = 0; u < 6; ++u) dma16(xsrc[u] + kt * QBK, lds0 + (kt % XRING) * XSTAGE + xoff[u]);
+    for (int u = 0; u < 3; ++u) dma16(xsrc[u] + kt * QBK, lds0 + (kt % XRING) * XSTAGE + xoff[u]);
   };
 
   // Raw weight bytes of a stage, per W row r: the super-block header and the two
@@ -107,14 +110,14 @@ __global__ __launch_bounds__(256) void qgemm_q4k_x3ref(const QArgs p) {
   // wave-uniform LDS address: its lanes past RAWB land in the slot's padding,
   // and whole loads past the image write a junk KiB, so that every wave issues
   // the same number of loads.
-  constexpr int RAWI = (NRI + 3) / 4;  // raw loads per wave per stage
-  constexpr int GRPL = 6 + RAWI;       // loads per wave per stage
+  constexpr int RAWI = (NRI + 7) / 8;  // raw loads per wave per stage
+  constexpr int GRPL = 3 + RAWI;       // loads per wave per stage
   const int nk = p.K / QBK;
   const uint8_t* rsrc[RAWI];
   int rkind[RAWI];
 #pragma unroll
   for (int u = 0; u < RAWI; ++u) {
-    const int f = (wave + 4 * u) * 1024 + lane * 16;
+    const int f = (wave + 8 * u) * 1024 + lane * 16;
     const int r = min(f / 48, BN - 1), c = (f % 48) >> 4;
     rsrc[u] = Wg + (size_t)min(n0 + r, p.N - 1) * p.rb;
     rkind[u] = c;
@@ -124,18 +127,20 @@ __global__ __launch_bounds__(256) void qgemm_q4k_x3ref(const QArgs p) {
     const int sb = kt >> 3, s = kt & 7;
 #pragma unroll
     for (int u = 0; u < RAWI; ++u) {
-      const int ii = wave + 4 * u, c = rkind[u];
+      const int ii = wave + 8 * u, c = rkind[u];
       const uint8_t* g = rsrc[u] + (size_t)sb * 144 + (c == 0 ? 0 : 16 + 32 * (s >> 1) + 16 * (c - 1));
       const uint32_t dst = ii < NRI ? (uint32_t)(RAWOFF + (kt % XRING) * RAWS + ii * 1024) : (uint32_t)JUNK;
       dma16(g, lds0 + dst);
     }
   };
 
-  // decode: thread (r, h) turns elements [16h, 16h+16) of W row r into fp16
-  // (threads past 2*BN repeat row BN-1 and store to the junk KiB, so the code has
-  // no branch and the scheduler can interleave it with the MFMAs)
-  const int dr = min(tid >> 1, BN - 1), dh = tid & 1;
-  const bool dec = tid < 2 * BN;
+  // decode: thread (r, h) of waves 4..7 turns elements [16h, 16h+16) of W row r
+  // into fp16 (threads past 2*BN repeat row BN-1 and store to the junk KiB, so a
+  // decoding wave has no divergent branch)
+  const int dt = tid - 256;
+  const int dr = min(max(dt, 0) >> 1, BN - 1), dh = tid & 1;
+  const bool dwave = wave >= 4;  // wave-uniform
+  const bool dec = dt >= 0 && dt < 2 * BN;
   auto decode = [&](int kt, uint32_t (&o)[8]) __attribute__((always_inline)) {
     const int s = kt & 7;
     const uint8_t* raw = lds + RAWOFF + (kt % XRING) * RAWS + dr * 48;
@@ -164,11 +169,11 @@ __global__ __launch_bounds__(256) void qgemm_q4k_x3ref(const QArgs p) {
     *(u32x4*)(bt + swz(r, 2 * dh + 1)) = u32x4{o[4], o[5], o[6], o[7]};
   };
 
-  float4v acc[2][NB];
+  float4v acc[2][NBW];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < NB; ++j) acc[i][j] = float4v{0.f, 0.f, 0.f, 0.f};
+    for (int jj = 0; jj < NBW; ++jj) acc[i][jj] = float4v{0.f, 0.f, 0.f, 0.f};
 
   // fragment offsets: lane l reads row (l%16) of a 16-row block, chunk l/16
   const int fr = lane & 15, fc = lane >> 4;
@@ -185,7 +190,7 @@ __global__ __launch_bounds__(256) void qgemm_q4k_x3ref(const QArgs p) {
   }
   vm_wait<(XRING - 1) * GRPL>();  // raw(0)
   __syncthreads();
-  {
+  if (dwave) {
     uint32_t o[8];
     decode(0, o);
     store_b(0, o);
@@ -196,40 +201,43 @@ __global__ __launch_bounds__(256) void qgemm_q4k_x3ref(const QArgs p) {
     issue_raw(kt + XRING);
     issue_x(min(kt + XRING - 1, nk - 1));
     uint32_t o[8];
-    decode(min(kt + 1, nk - 1), o);  // stage kt+1 (its raw bytes came with group kt)
+    if (dwave) decode(min(kt + 1, nk - 1), o);  // stage kt+1 (its raw bytes came with group kt)
     const uint8_t* xs = lds + (kt % XRING) * XSTAGE;
     const uint8_t* bs = lds + BOFF + (kt & 1) * BPART;
-    half8 bf[NB];
+    half8 bf[NBW];
 #pragma unroll
-    for (int j = 0; j < NB; ++j) bf[j] = *(const half8*)(bs + j * 1024 + fo);
+    for (int jj = 0; jj < NBW; ++jj) bf[jj] = *(const half8*)(bs + min(2 * jj + wn, NB - 1) * 1024 + fo);
     // parts lo, mid, hi (tier.cpp:940) into one fp32 accumulator
 #pragma unroll
     for (int part = 2; part >= 0; --part) {
       half8 af[2];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) af[i] = *(const half8*)(xs + part * XPART + (wave * 32 + i * 16) * 64 + fo);
+      for (int i = 0; i < 2; ++i) af[i] = *(const half8*)(xs + part * XPART + (wm * 32 + i * 16) * 64 + fo);
 #pragma unroll
-      for (int j = 0; j < NB; ++j)
+      for (int jj = 0; jj < NBW; ++jj)
+        if ((NB & 1) == 0 || jj < NBW - 1 || wn == 0)  // odd NB: the last block is wave-column 0's
 #pragma unroll
-        for (int i = 0; i < 2; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+          for (int i = 0; i < 2; ++i)
+            acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[jj], acc[i][jj], 0, 0, 0);
     }
-    store_b((kt + 1) & 1, o);
+    if (dwave) store_b((kt + 1) & 1, o);
   }
   vm_wait<0>();  // drain the re-loads past the end
 
   // epilogue: register i of lane l holds row 4*(l/16) + i, column l%16 of a 16x16 block
 #pragma unroll
-  for (int j = 0; j < NB; ++j) {
+  for (int jj = 0; jj < NBW; ++jj) {
+    const int j = 2 * jj + wn;
     const int col = n0 + j * 16 + (lane & 15);
-    if (col >= p.N) continue;
+    if (j >= NB || col >= p.N) continue;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int row = m0 + wave * 32 + i * 16 + 4 * (lane >> 4) + r;
+        const int row = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + r;
         if (row >= M) continue;
         float* c = Yg + (size_t)row * p.ldy + col;
-        float v = acc[i][j][r];
+        float v = acc[i][jj][r];
         if (p.beta != 0.f) v = fmaf(p.beta, *c, v);
         *c = v;
       }
@@ -247,7 +255,7 @@ int launch_q(const QArgs& a, hipStream_t s, const char* who) {
     if (e != hipSuccess) return hip_fail(e, who);
     attr_set = true;
   }
-  qgemm_q4k_x3ref<BN><<<(unsigned)a.tile0[a.ngroups], 256, lds, s>>>(a);
+  qgemm_q4k_x3ref<BN><<<(unsigned)a.tile0[a.ngroups], 512, lds, s>>>(a);
   TM_LAUNCH_CHECK(who);
   return TIERMM_OK;
 }
