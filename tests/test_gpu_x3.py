@@ -17,11 +17,12 @@ pytestmark = pytest.mark.gpu
 BAR = 2.0 ** -20
 
 
-def test_split3_bit_exact(gpu):
+@pytest.mark.parametrize("tail", [5, 3])  # 70005 elements: per-element kernel; 70000: 8 per thread
+def test_split3_bit_exact(gpu, tail):
     rng = np.random.default_rng(11)
     x = np.concatenate([rng.uniform(-60000, 60000, 50000),
                         np.ldexp(rng.uniform(-1, 1, 20000), rng.integers(-40, 10, 20000)),
-                        [0.0, -0.0, 65504.0, 65520.0, 1e-30]]).astype(np.float32)
+                        [0.0, -0.0, 65504.0, 65520.0, 1e-30]]).astype(np.float32)[:70000 + (tail == 5) * 5]
     n = x.size
     X = hip.to_device(x)
     for order, stride in ((tier_amd.HML, n), (tier_amd.LMH, n + 40)):
@@ -35,9 +36,11 @@ def test_split3_bit_exact(gpu):
             assert np.array_equal(got[i * stride:i * stride + n], want[i * stride:i * stride + n]), (order, i)
 
 
-def test_x3s_split_bit_exact(gpu):
+@pytest.mark.parametrize("cols", [1000, 1001, 5120, 8192, 14336, 20000])
+def test_x3s_split_bit_exact(gpu, cols):
+    """Rows held in registers (cols a multiple of 4, up to 16384) and the two-pass kernel."""
     rng = np.random.default_rng(12)
-    v = (rng.standard_normal((9, 1000)) * np.array([0.02, 1, 1e-6, 300, 0, 1e4, 2e-5, 5, 1e-30])[:, None])
+    v = (rng.standard_normal((9, cols)) * np.array([0.02, 1, 1e-6, 300, 0, 1e4, 2e-5, 5, 1e-30])[:, None])
     v = v.astype(np.float32)
     rows, cols = v.shape
     S = hip.to_device(v)
@@ -253,6 +256,11 @@ def test_split3_bf16_bit_exact(gpu):
     rng = np.random.default_rng(23)
     x = np.concatenate([rng.standard_normal(5000).astype(np.float32) * 3,
                         np.array([0.0, -0.0, 1e-30, -7.5e4, 3.0e38], np.float32)])
+    _split3_bf16_case(x)                         # 5005 elements: the per-element kernel
+    _split3_bf16_case(np.concatenate([x[:4995], x[-5:]]))  # 5000: eight elements per thread
+
+
+def _split3_bf16_case(x):
     n = x.size
     X, P = hip.to_device(x), hip.DeviceBuffer(3 * n * 2)
     for order in (tier_amd.HML, tier_amd.LMH):

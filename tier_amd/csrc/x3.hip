@@ -68,6 +68,42 @@ __global__ __launch_bounds__(256) void split3_kernel(const float* __restrict__ x
   }
 }
 
+// The same split, 8 consecutive elements per thread: two 16-byte loads, one
+// 16-byte store per part (n, stride multiples of 8; x and parts 16-byte aligned).
+template <bool BF>
+__global__ __launch_bounds__(256) void split3_vec8_kernel(const float* __restrict__ x, uint16_t* __restrict__ parts,
+                                                          size_t n8, size_t stride, int order) {
+  const size_t step = (size_t)gridDim.x * blockDim.x;
+  auto to16 = [](float f) __attribute__((always_inline)) { return BF ? f2bf(f) : f2h(f); };
+  auto from16 = [](uint16_t u) __attribute__((always_inline)) {
+    return BF ? __uint_as_float((uint32_t)u << 16) : h2f(u);
+  };
+  uint16_t* ph = parts + (order == TIERMM_HML ? 0 : 2 * stride);
+  uint16_t* pm = parts + stride;
+  uint16_t* pl = parts + (order == TIERMM_HML ? 2 * stride : 0);
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += step) {
+    const float4 a = ((const float4*)x)[2 * i], b = ((const float4*)x)[2 * i + 1];
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    uint32_t h[4], m[4], l[4];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint16_t hh = to16(v[k]);
+      const float r = v[k] - from16(hh);
+      const uint16_t mm = to16(r);
+      const uint16_t ll = to16(r - from16(mm));
+      const int sh = 16 * (k & 1);
+      if (sh == 0) {
+        h[k >> 1] = hh; m[k >> 1] = mm; l[k >> 1] = ll;
+      } else {
+        h[k >> 1] |= (uint32_t)hh << 16; m[k >> 1] |= (uint32_t)mm << 16; l[k >> 1] |= (uint32_t)ll << 16;
+      }
+    }
+    ((uint4*)ph)[i] = make_uint4(h[0], h[1], h[2], h[3]);
+    ((uint4*)pm)[i] = make_uint4(m[0], m[1], m[2], m[3]);
+    ((uint4*)pl)[i] = make_uint4(l[0], l[1], l[2], l[3]);
+  }
+}
+
 __device__ __forceinline__ float block_max_256(float v, float* red) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
@@ -84,6 +120,45 @@ __device__ __forceinline__ int x3s_exp(float amax) {
   int ex;
   (void)frexpf(amax, &ex);
   return min(100, max(-100, 15 - ex));
+}
+
+// One pass over a row held in registers: 4 consecutive elements per thread and
+// step (cols a multiple of 4, at most 1024 * XR; rows 16-byte aligned).
+template <int XR>
+__global__ __launch_bounds__(256) void x3s_split_reg_kernel(const float* __restrict__ src, uint16_t* __restrict__ hi,
+                                                            uint16_t* __restrict__ lo, int32_t* __restrict__ exps,
+                                                            int cols) {
+  __shared__ float red[4];
+  const size_t base = (size_t)blockIdx.x * cols;
+  const int c4 = cols >> 2;
+  float4 v[XR];
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < XR; ++j) {
+    const int k = threadIdx.x + 256 * j;
+    v[j] = k < c4 ? ((const float4*)(src + base))[k] : make_float4(0.f, 0.f, 0.f, 0.f);
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+  }
+  amax = block_max_256(amax, red);
+  const int e = x3s_exp(amax);
+  const float sc = ldexpf(1.f, e);
+#pragma unroll
+  for (int j = 0; j < XR; ++j) {
+    const int k = threadIdx.x + 256 * j;
+    if (k >= c4) break;
+    const float f[4] = {v[j].x * sc, v[j].y * sc, v[j].z * sc, v[j].w * sc};
+    uint32_t h[2], l[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint16_t h0 = f2h(f[2 * q]), h1 = f2h(f[2 * q + 1]);
+      const uint16_t l0 = f2h(f[2 * q] - h2f(h0)), l1 = f2h(f[2 * q + 1] - h2f(h1));
+      h[q] = h0 | ((uint32_t)h1 << 16);
+      l[q] = l0 | ((uint32_t)l1 << 16);
+    }
+    ((uint2*)(hi + base))[k] = make_uint2(h[0], h[1]);
+    ((uint2*)(lo + base))[k] = make_uint2(l[0], l[1]);
+  }
+  if (threadIdx.x == 0) exps[blockIdx.x] = e;
 }
 
 __global__ __launch_bounds__(256) void x3s_split_kernel(const float* __restrict__ src, uint16_t* __restrict__ hi,
@@ -654,8 +729,31 @@ int x3ref_nt(const uint16_t* xparts, size_t stride, const uint16_t* W, int ldw, 
   return launch_x3<128, 128, X3_REF>(a, s, who);
 }
 
+// Rows held in registers where they fit (one read of the source), else two passes.
+void x3s_split_launch(const float* src, uint16_t* hi, uint16_t* lo, int32_t* exps, int rows, int cols, hipStream_t s) {
+  const bool vec = cols % 4 == 0 && ((uintptr_t)src & 15) == 0 && ((uintptr_t)hi & 7) == 0 && ((uintptr_t)lo & 7) == 0;
+  if (vec && cols <= 4096)
+    x3s_split_reg_kernel<4><<<rows, 256, 0, s>>>(src, hi, lo, exps, cols);
+  else if (vec && cols <= 8192)
+    x3s_split_reg_kernel<8><<<rows, 256, 0, s>>>(src, hi, lo, exps, cols);
+  else if (vec && cols <= 16384)
+    x3s_split_reg_kernel<16><<<rows, 256, 0, s>>>(src, hi, lo, exps, cols);
+  else
+    x3s_split_kernel<<<rows, 256, 0, s>>>(src, hi, lo, exps, cols);
+}
+
 int split3_launch(const float* x, uint16_t* parts, size_t n, size_t stride, int order, hipStream_t s, bool bf16 = false) {
   if (n == 0) return TIERMM_OK;
+  if (n % 8 == 0 && stride % 8 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)parts & 15) == 0) {
+    const size_t n8 = n / 8, want = (n8 + 255) / 256;
+    const unsigned grid = (unsigned)(want < 8192 ? want : 8192);
+    if (bf16)
+      split3_vec8_kernel<true><<<grid, 256, 0, s>>>(x, parts, n8, stride, order);
+    else
+      split3_vec8_kernel<false><<<grid, 256, 0, s>>>(x, parts, n8, stride, order);
+    TM_LAUNCH_CHECK("split3: launch");
+    return TIERMM_OK;
+  }
   const size_t want = (n + 255) / 256;
   const unsigned grid = (unsigned)(want < 16384 ? want : 16384);
   if (bf16)
@@ -695,7 +793,7 @@ int tiermm_x3s_split(const float* src, uint16_t* hi, uint16_t* lo, int32_t* exps
   if (rows < 0 || cols < 0) return set_error(TIERMM_EINVAL, "tiermm_x3s_split: negative size");
   if (rows == 0) return TIERMM_OK;
   if (!src || !hi || !lo || !exps) return set_error(TIERMM_EINVAL, "tiermm_x3s_split: null buffer");
-  x3s_split_kernel<<<rows, 256, 0, (hipStream_t)stream>>>(src, hi, lo, exps, cols);
+  x3s_split_launch(src, hi, lo, exps, rows, cols, (hipStream_t)stream);
   TM_LAUNCH_CHECK("tiermm_x3s_split: launch");
   return TIERMM_OK;
 }
@@ -849,9 +947,9 @@ int tiermm_qgemm(const void* W, int qtype, size_t rb, const float* X, float* Y, 
     int32_t* xexp = (int32_t*)b;
     st = tiermm_dequant(W, qtype, rb, K, 0, (size_t)N, wf, TIERMM_OUT_F32, stream);
     if (st) return st;
-    x3s_split_kernel<<<N, 256, 0, s>>>(wf, whi, wlo, wexp, K);
+    x3s_split_launch(wf, whi, wlo, wexp, N, K, s);
     TM_LAUNCH_CHECK("tiermm_qgemm: split W");
-    x3s_split_kernel<<<M, 256, 0, s>>>(X, xhi, xlo, xexp, K);
+    x3s_split_launch(X, xhi, xlo, xexp, M, K, s);
     TM_LAUNCH_CHECK("tiermm_qgemm: split x");
     X3Args a{};
     a.A[0] = xhi; a.A[1] = xlo; a.B[0] = whi; a.B[1] = wlo;
