@@ -325,6 +325,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the host baseline")
     ap.add_argument("--no-secondary", action="store_true", help="headline only")
+    ap.add_argument("--secondary", default="", help="comma-separated secondary names to run (default: all)")
     ap.add_argument("--cpu-seconds", type=float, default=3.0)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -351,6 +352,8 @@ def main() -> int:
     log(f"bench: q4_K GEMV {per * 1e3:.2f} us/step")
 
     secondary = {}
+    only = {n for n in args.secondary.split(",") if n}
+    want = lambda name: not args.no_secondary and (not only or name in only)  # noqa: E731
     if not args.no_secondary:
         reps, warm = max(20, args.steps // 4), 5
         for name, qt, N, K in (("q4_K_5120x5120_m1", tier_amd.Q4_K, 5120, 5120),
@@ -359,6 +362,8 @@ def main() -> int:
                                ("q8_0_4096x4096_m1", tier_amd.Q8_0, 4096, 4096),
                                ("q5_K_5120x14336_m1", tier_amd.Q5_K, 5120, 14336),
                                ("q6_K_5120x14336_m1", tier_amd.Q6_K, 5120, 14336)):
+            if not want(name):
+                continue
             log(f"bench: {name}")
             c = GemvCase(tier_amd, hip, qt, N, K, seed=N + K)
             km = time_launches(hip, stream, lambda i: c.launch(tier_amd, i, stream), reps, warm)
@@ -369,6 +374,8 @@ def main() -> int:
         # quantized GEMM at M=512 (config 3), x3-ref semantics
         for name, N, K in (("q4_K_5120x5120_m512", 5120, 5120), ("q4_K_14336x5120_m512", 14336, 5120),
                            ("q4_K_5120x14336_m512", 5120, 14336)):
+            if not want(name):
+                continue
             log(f"bench: {name}")
             M = 512
             rng = np.random.default_rng(N * 7 + K)
@@ -386,7 +393,8 @@ def main() -> int:
             secondary[name] = {"TFLOPS": round(tf, 2), "frac_x3_peak": round(tf / X3_PEAK_TFLOPS, 4),
                                "us_per_call": round(km * 1e3, 1)}
             del Wd, X, Y, WS
-        # x3-2x2 GEMM, config 2
+    # x3-2x2 GEMM, config 2
+    if want("x3s_4096x5120x5120"):
         log("bench: x3s_4096x5120x5120")
         M, N, K = 4096, 5120, 5120
         rng = np.random.default_rng(8)
@@ -402,8 +410,11 @@ def main() -> int:
         secondary["x3s_4096x5120x5120"] = {"TFLOPS": round(tf, 2), "frac_x3_peak": round(tf / X3_PEAK_TFLOPS, 4),
                                            "us_per_call": round(km * 1e3, 1), "includes": "X split + GEMM"}
         del bufs, Wf, Xf
+    if want("decoder_layer_t4096"):
         secondary["decoder_layer_t4096"] = bench_decoder_layer(tier_amd, hip, stream)
+    if want("moe_t4096"):
         secondary["moe_t4096"] = bench_moe(tier_amd, hip, stream)
+    if want("chat_streamed_4_layers"):
         secondary["chat_streamed_4_layers"] = bench_chat_stream(tier_amd, hip, stream)
 
     traffic, traffic_src = measured_traffic()
