@@ -21,8 +21,8 @@ experts (config 5), and the chat linears of four config-4 layers streamed from
 pinned host memory against the host-to-device copy rate.
 
 ``cpu_baseline``: the reference's own q_val GEMV (oracle/_ref, compiled from
-quant.h) on the host's threads, on the same weight (timed over a bounded number
-of repetitions).
+quant.h) on the host's threads, and on one thread, on the same weight (each timed
+over a bounded number of repetitions), with the host CPU model.
 """
 from __future__ import annotations
 
@@ -294,28 +294,50 @@ def measured_traffic():
     return int(d["bytes_per_launch"]), f"profiles/q4k_gemv_13824x5120.md ({d['kernel']})"
 
 
+def _host_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(case: GemvCase, budget_s: float):
-    """The reference q_val GEMV (oracle/_ref, built from quant.h) on every host thread; bounded repetitions."""
+    """The reference q_val GEMV (oracle/_ref, built from quant.h) on every host thread, and on
+    one thread; bounded repetitions of each."""
     import oracle
     threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
     W = np.ascontiguousarray(case.blocks)
     if oracle.ref_available():
         kind = "reference"
-        run = lambda: oracle.ref_gemv_threads(W, case.qtype, case.x, case.N, case.K, threads)  # noqa: E731
+        runner = lambda n: (lambda: oracle.ref_gemv_threads(W, case.qtype, case.x, case.N, case.K, n))  # noqa: E731
     else:  # the C restatement, single thread (lane order of gemv_q)
         kind, threads = "port", 1
-        run = lambda: oracle.gemv_lanes(W, case.qtype, case.x, case.N, case.K, 64)  # noqa: E731
-    run()
-    reps, t0 = 0, time.perf_counter()
-    while True:
+        runner = lambda n: (lambda: oracle.gemv_lanes(W, case.qtype, case.x, case.N, case.K, 64))  # noqa: E731
+
+    def timed(run, budget):
         run()
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or reps >= 200:
-            break
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            run()
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= budget or reps >= 200:
+                return reps, el
+
+    reps, el = timed(runner(threads), budget_s)
     gbs = case.bytes * reps / el / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": kind,
-            "sample": f"{reps} full {case.N}x{case.K} q4_K GEMVs ({el:.1f} s wall, {el * threads:.0f} thread-s)"}
+    out = {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+           "sample": f"{reps} full {case.N}x{case.K} q4_K GEMVs ({el:.1f} s wall, {el * threads:.0f} thread-s)",
+           "host": _host_model(), "nproc": os.cpu_count()}
+    if threads > 1:
+        reps1, el1 = timed(runner(1), budget_s / 2)
+        out["single_core"] = {"value": round(case.bytes * reps1 / el1 / 1e9, 3), "unit": "GB/s",
+                              "sample": f"{reps1} full GEMVs on 1 thread ({el1:.1f} s)"}
+    return out
 
 
 def main() -> int:

@@ -204,21 +204,23 @@ __global__ __launch_bounds__(512) void qgemm_q4k_x3ref(const QArgs p) {
     if (dwave) decode(min(kt + 1, nk - 1), o);  // stage kt+1 (its raw bytes came with group kt)
     const uint8_t* xs = lds + (kt % XRING) * XSTAGE;
     const uint8_t* bs = lds + BOFF + (kt & 1) * BPART;
-    half8 bf[NBW];
+    // every fragment of the stage first (one LDS latency per stage), then the MFMAs
+    half8 bf[NBW], af[3][2];
 #pragma unroll
     for (int jj = 0; jj < NBW; ++jj) bf[jj] = *(const half8*)(bs + min(2 * jj + wn, NB - 1) * 1024 + fo);
+#pragma unroll
+    for (int part = 0; part < 3; ++part)
+#pragma unroll
+      for (int i = 0; i < 2; ++i) af[part][i] = *(const half8*)(xs + part * XPART + (wm * 32 + i * 16) * 64 + fo);
     // parts lo, mid, hi (tier.cpp:940) into one fp32 accumulator
 #pragma unroll
     for (int part = 2; part >= 0; --part) {
-      half8 af[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) af[i] = *(const half8*)(xs + part * XPART + (wm * 32 + i * 16) * 64 + fo);
 #pragma unroll
       for (int jj = 0; jj < NBW; ++jj)
         if ((NB & 1) == 0 || jj < NBW - 1 || wn == 0)  // odd NB: the last block is wave-column 0's
 #pragma unroll
           for (int i = 0; i < 2; ++i)
-            acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[jj], acc[i][jj], 0, 0, 0);
+            acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[part][i], bf[jj], acc[i][jj], 0, 0, 0);
     }
     if (dwave) store_b((kt + 1) & 1, o);
   }
