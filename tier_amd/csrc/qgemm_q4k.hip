@@ -3,25 +3,32 @@
 // Y[M][ldy] (beta)= sum over the parts p of x (lo, mid, hi) of X_p[M][K] * W16[N][K]^T,
 // W16 = fp16(q_val(W_n, k)) -- the training path's dq_k<tier_fp16> (tier.cpp:515,
 // 293-298) followed by fp3gemm (tier.cpp:922-943) -- without writing W16 to
-// memory: the q4_K rows are decoded into the LDS B tile as the K loop needs
-// them.
+// memory: the q4_K rows are decoded into an LDS B tile as the K loop needs them.
 //
 // Tiling: a workgroup owns BM=128 rows of X x BN rows of W (BN in 64..128, a
-// multiple of 16 picked per shape so the tile count fills the CUs); 8 waves, two
-// per SIMD: wave w the X rows [32(w%4), 32(w%4)+32) against the 16-column blocks
-// j = 2jj + w/4 (every other block), on v_mfma_f32_16x16x32_f16.  K advances 32
-// per stage (one q4_K sub-block):
-//   * the three x parts (pre-split, HML planes) and the raw weight bytes reach
-//     LDS by global_load_lds_dwordx4;
-//   * thread (r, h) of waves 4..7 decodes elements [16h, 16h+16) of the
-//     sub-block of W row r from the raw bytes, exactly as q_val (d*sc*q -
-//     dmin*m, one rounding), rounds to fp16 (v_cvt, RNE) and stores them in the
-//     other B buffer while the current stage's MFMAs run.  Waves 0..3 only
-//     multiply, so each SIMD has one wave with MFMAs to issue while the other
-//     decodes or waits on LDS.
+// multiple of 16 picked per shape so the tile count fills the CUs), one K step
+// of 32 (one q4_K sub-block) per stage, v_mfma_f32_16x16x32_f16.  Its 8 waves
+// split into 4 consumers and 4 producers, one of each per SIMD, which hand
+// stages over through flags in LDS instead of a workgroup barrier:
+//   * consumer c multiplies x rows [32c, 32c+32) against all BN columns.  It
+//     loads its own A fragments (3 parts x 2 row blocks, 16 bytes per lane) from
+//     the pre-split x planes straight into a ring of registers, three stages
+//     ahead -- each consumer reads only its rows, so staging x in LDS would buy
+//     no reuse;
+//   * producer p streams the raw bytes (super-block header and the qs chunk of
+//     the sub-block) of W rows [p*BN/4, (p+1)*BN/4) through a ring of LDS slots
+//     with global_load_lds_dwordx4, six stages ahead, and decodes each row's 32
+//     elements exactly as q_val (d*sc*q - dmin*m, one rounding), rounded to fp16
+//     (v_cvt, RNE), into the B ring.
 // LDS rows hold 32 halfs as four 16-byte chunks, chunk c at slot
 // c ^ ((row >> 2) & 3), so the fragment reads (16 rows x 4 chunks) hit
 // distinct bank groups.
+//
+// Measured (512x5120x5120 .. 512x5120x14336, bit-identical to the barrier form
+// this replaced): 8-18 % faster.  Timing copies with parts switched off show
+// the consumers' x loads as the largest single cost (consumers alone: 125 us
+// with them, 57 us without, 122 us with every load hitting one cached address),
+// i.e. the vector-memory instructions themselves, not their latency.
 #include "tm_device.h"
 
 namespace tiermm {
@@ -32,8 +39,6 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 
 constexpr int QBM = 128, QBK = 32;
-constexpr int XPART = QBM * 64;  // bytes of one x part per stage
-constexpr int XRING = 4;         // x stages in LDS: three in flight while one is multiplied
 
 // A launch covers up to QG groups (one plain GEMM, or the experts of a routed
 // batch): group g multiplies rows [row0[g], row0[g] + rows[g]) of X and Y with
@@ -55,200 +60,209 @@ struct QArgs {
 
 __device__ __forceinline__ uint32_t swz(int row, int chunk) { return (uint32_t)(row * 64 + ((chunk ^ ((row >> 2) & 3)) * 16)); }
 
+__device__ __forceinline__ void lds_rel(int* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Waits until the four flags at f (16-byte aligned, LDS) are all >= v: one
+// 16-byte read per try.  The flags only grow, and the data they publish is read
+// after this returns (the empty asm keeps those reads below the loop).
+__device__ __forceinline__ void poll4(const int* f, int v) {
+  typedef int i4 __attribute__((ext_vector_type(4)));
+  const volatile __attribute__((address_space(3))) i4* fl =
+      (const volatile __attribute__((address_space(3))) i4*)(size_t)lds_addr(f);
+  for (;;) {
+    const i4 t = *fl;
+    if (min(min(t[0], t[1]), min(t[2], t[3])) >= v) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  asm volatile("" ::: "memory");
+}
+
+// Flags (stage numbers, slot-major so that one poll reads all four):
+//   ready[q % FL][p] = q -- producer p's B rows of stage q are stored;
+//   done[q % FL][c] = q  -- consumer c has read stage q's B tile.
+// Stage q's B tile is slot q % NBR; producer p's raw bytes of stage q are its
+// slot q % RR.  Producer p loads stage q + DR in its iteration q (that slot held
+// stage q + DR - RR, which it has decoded) and decodes stage q once every
+// consumer has read stage q - NBR (the slot's previous user).  That is a stage
+// below q, whose ready every producer has published, so each wait ends; a
+// consumer waits only for its own loads and for ready.
 template <int BN>
 __global__ __launch_bounds__(512) void qgemm_q4k_x3ref(const QArgs p) {
-  constexpr int NB = BN / 16, NBW = (NB + 1) / 2;  // blocks in the tile, per wave
+  constexpr int NB = BN / 16;
+  constexpr int NBR = 3, FL = 4, XR = 4, RR = 8, DR = 6;
+  constexpr int PR = BN / 4;
+  constexpr int RAWP = PR * 48;
+  constexpr int RAWI = (RAWP + 1023) / 1024, RSLOT = RAWI * 1024;
   constexpr int BPART = BN * 64;
-  constexpr int XSTAGE = 3 * XPART;
-  constexpr int BOFF = XRING * XSTAGE;                 // the two B buffers follow the x ring
-  constexpr int RAWB = BN * 48, NRI = (RAWB + 1023) / 1024, RAWS = NRI * 1024;
-  constexpr int RAWOFF = BOFF + 2 * BPART;             // then the raw weight ring
-  constexpr int JUNK = RAWOFF + XRING * RAWS;          // then a KiB for loads past the raw image
+  constexpr int RAWOFF = NBR * BPART;
+  constexpr int FLAGOFF = RAWOFF + 4 * RR * RSLOT;
+  static_assert(BN % 16 == 0 && BN <= 128, "tile width");
+  static_assert(NBR <= FL && DR < RR && RAWI * DR <= 63, "ring depths");
   extern __shared__ __attribute__((aligned(16))) uint16_t lds_h[];
   uint8_t* lds = (uint8_t*)lds_h;
   const uint32_t lds0 = lds_addr(lds);
+  int* ready = (int*)(lds + FLAGOFF);  // [FL][4]: slot-major, one 16-byte read per poll
+  int* done = ready + 4 * FL;          // [FL][4]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (tid < 8 * FL) ready[tid] = -1;
 
-  int grp = 0;  // the group of this workgroup (uniform scan over the tile prefix)
-  // One GEMM: workgroups go round-robin over the 8 XCDs, so XCD x is given the
-  // x-th eighth of the tile sequence (M-block major), a few M-blocks whose x rows
-  // stay in that XCD's L2 while its N tiles stream past.
+  int grp = 0;
   int b = (int)blockIdx.x;
   const int nt_all = p.tile0[p.ngroups];
   if (p.ngroups == 1 && (nt_all & 7) == 0) b = (b & 7) * (nt_all >> 3) + (b >> 3);
   while (grp + 1 < p.ngroups && b >= p.tile0[grp + 1]) ++grp;
   const int tile = b - p.tile0[grp];
   const int ntn = (p.N + BN - 1) / BN;
-  const int tm = tile / ntn, tn = tile % ntn;
-  const int m0 = tm * QBM, n0 = tn * BN;
+  const int m0 = (tile / ntn) * QBM, n0 = (tile % ntn) * BN;
   const int M = p.rows[grp];
   const uint16_t* Xg = p.X + (size_t)p.row0[grp] * p.K;
   float* Yg = p.Y + (size_t)p.row0[grp] * p.ldy;
   const uint8_t* Wg = p.W[grp];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave & 3, wn = wave >> 2;
-
-  // x DMA: 3 parts x 8 loads of 16 rows per stage, 3 per wave
-  const uint16_t* xsrc[3];
-  uint32_t xoff[3];
-#pragma unroll
-  for (int u = 0; u < 3; ++u) {
-    const int t = wave + 8 * u, part = t >> 3, ch = t & 7;
-    const int row = ch * 16 + (lane >> 2), slot = lane & 3;
-    xsrc[u] = Xg + part * p.xs + (size_t)min(m0 + row, M - 1) * p.K + 8 * (slot ^ ((row >> 2) & 3));
-    xoff[u] = (uint32_t)(part * XPART + ch * 1024);
-  }
-  auto issue_x = [&](int kt) __attribute__((always_inline)) {
-#pragma unroll
-    for (int u = 0; u < 3; ++u) dma16(xsrc[u] + kt * QBK, lds0 + (kt % XRING) * XSTAGE + xoff[u]);
-  };
-
-  // Raw weight bytes of a stage, per W row r: the super-block header and the two
-  // 16-byte qs chunks holding the sub-block ([r][3][16 bytes], RAWB bytes in a
-  // slot of RAWS).  They arrive by DMA like x, one stage ahead of x, so that
-  // stage kt's loads bring x(kt) and raw(kt+1).  A load writes 1 KiB at a
-  // wave-uniform LDS address: its lanes past RAWB land in the slot's padding,
-  // and whole loads past the image write a junk KiB, so that every wave issues
-  // the same number of loads.
-  constexpr int RAWI = (NRI + 7) / 8;  // raw loads per wave per stage
-  constexpr int GRPL = 3 + RAWI;       // loads per wave per stage
   const int nk = p.K / QBK;
-  const uint8_t* rsrc[RAWI];
-  int rkind[RAWI];
-#pragma unroll
-  for (int u = 0; u < RAWI; ++u) {
-    const int f = (wave + 8 * u) * 1024 + lane * 16;
-    const int r = min(f / 48, BN - 1), c = (f % 48) >> 4;
-    rsrc[u] = Wg + (size_t)min(n0 + r, p.N - 1) * p.rb;
-    rkind[u] = c;
-  }
-  auto issue_raw = [&](int kt) __attribute__((always_inline)) {
-    kt = min(kt, nk - 1);
-    const int sb = kt >> 3, s = kt & 7;
-#pragma unroll
-    for (int u = 0; u < RAWI; ++u) {
-      const int ii = wave + 8 * u, c = rkind[u];
-      const uint8_t* g = rsrc[u] + (size_t)sb * 144 + (c == 0 ? 0 : 16 + 32 * (s >> 1) + 16 * (c - 1));
-      const uint32_t dst = ii < NRI ? (uint32_t)(RAWOFF + (kt % XRING) * RAWS + ii * 1024) : (uint32_t)JUNK;
-      dma16(g, lds0 + dst);
-    }
-  };
+  __syncthreads();  // flags initialised
 
-  // decode: thread (r, h) of waves 4..7 turns elements [16h, 16h+16) of W row r
-  // into fp16 (threads past 2*BN repeat row BN-1 and store to the junk KiB, so a
-  // decoding wave has no divergent branch)
-  const int dt = tid - 256;
-  const int dr = min(max(dt, 0) >> 1, BN - 1), dh = tid & 1;
-  const bool dwave = wave >= 4;  // wave-uniform
-  const bool dec = dt >= 0 && dt < 2 * BN;
-  auto decode = [&](int kt, uint32_t (&o)[8]) __attribute__((always_inline)) {
-    const int s = kt & 7;
-    const uint8_t* raw = lds + RAWOFF + (kt % XRING) * RAWS + dr * 48;
-    const u32x4 H = *(const u32x4*)raw;
-    const u32x4 Q = *(const u32x4*)(raw + 16 + 16 * dh);
-    int sc, mn;
-    kq_scale_min(s, H[1], H[2], H[3], sc, mn);
-    const float dsc = h2f(H[0] & 0xffffu) * (float)sc, dm = h2f(H[0] >> 16) * (float)mn;
-    const int sh = 4 * (s & 1);
+  if (wave >= 4) {
+    // ------------------------------------------------------------ producer
+    const int pw = wave - 4;
+    const uint8_t* rsrc[RAWI];
+    int rkind[RAWI];
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const uint32_t v = Q[w] >> sh;
+    for (int j = 0; j < RAWI; ++j) {
+      const int f = min(j * 1024 + lane * 16, RAWP - 16);
+      rsrc[j] = Wg + (size_t)min(n0 + pw * PR + f / 48, p.N - 1) * p.rb;
+      rkind[j] = (f % 48) >> 4;
+    }
+    const uint32_t raw0 = lds0 + RAWOFF + pw * RR * RSLOT;
+    // raw bytes of stage q (q >= nk: stage nk - 1 again, into its own slot)
+    auto issue = [&](int q) __attribute__((always_inline)) {
+      const int qq = min(q, nk - 1), sb = qq >> 3, s = qq & 7;
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        // q_val (quant.h:83-84): both products exact, one rounding; then fp16 RNE
-        const float lo = fmaf(dsc, (float)((v >> (16 * b)) & 15u), -dm);
-        const float hi = fmaf(dsc, (float)((v >> (16 * b + 8)) & 15u), -dm);
-        o[2 * w + b] = (uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16);
+      for (int j = 0; j < RAWI; ++j) {
+        const int c = rkind[j];
+        dma16(rsrc[j] + (size_t)sb * 144 + (c == 0 ? 0 : 16 + 32 * (s >> 1) + 16 * (c - 1)),
+              raw0 + (qq % RR) * RSLOT + j * 1024);
       }
+    };
+    const int dr = lane >> 1, dh = lane & 1;
+    for (int q = 0; q < DR; ++q) issue(q);
+    for (int q = 0; q < nk; ++q) {
+      issue(q + DR);          // its slot held stage q + DR - RR < q, decoded already
+      vm_wait<RAWI * DR>();   // stage q's raw bytes have landed
+      if (q >= NBR) poll4(done + 4 * ((q - NBR) % FL), q - NBR);  // B slot: stage q - NBR read by all
+      if (lane < 2 * PR) {
+        const int s = q & 7;
+        const uint8_t* raw = lds + RAWOFF + (pw * RR + q % RR) * RSLOT + dr * 48;
+        const u32x4 H = *(const u32x4*)raw;
+        const u32x4 Q = *(const u32x4*)(raw + 16 + 16 * dh);
+        int sc, mn;
+        kq_scale_min(s, H[1], H[2], H[3], sc, mn);
+        const float dsc = h2f(H[0] & 0xffffu) * (float)sc, dm = h2f(H[0] >> 16) * (float)mn;
+        const int sh = 4 * (s & 1);
+        uint32_t o[8];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const uint32_t v = Q[w] >> sh;
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            // q_val (quant.h:83-84): both products exact, one rounding; then fp16 RNE
+            const float lo = fmaf(dsc, (float)((v >> (16 * e)) & 15u), -dm);
+            const float hi = fmaf(dsc, (float)((v >> (16 * e + 8)) & 15u), -dm);
+            o[2 * w + e] = (uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16);
+          }
+        }
+        uint8_t* bt = lds + (q % NBR) * BPART;
+        const int r = pw * PR + dr;
+        *(u32x4*)(bt + swz(r, 2 * dh)) = u32x4{o[0], o[1], o[2], o[3]};
+        *(u32x4*)(bt + swz(r, 2 * dh + 1)) = u32x4{o[4], o[5], o[6], o[7]};
+      }
+      if (lane == 0) lds_rel(&ready[4 * (q % FL) + pw], q);
     }
-  };
-  auto store_b = [&](int buf, const uint32_t (&o)[8]) __attribute__((always_inline)) {
-    uint8_t* bt = dec ? lds + BOFF + buf * BPART : lds + JUNK;
-    const int r = dec ? dr : 0;
-    *(u32x4*)(bt + swz(r, 2 * dh)) = u32x4{o[0], o[1], o[2], o[3]};
-    *(u32x4*)(bt + swz(r, 2 * dh + 1)) = u32x4{o[4], o[5], o[6], o[7]};
-  };
+    vm_wait<0>();  // drain the re-loads past the end
+    return;
+  }
 
-  float4v acc[2][NBW];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int jj = 0; jj < NBW; ++jj) acc[i][jj] = float4v{0.f, 0.f, 0.f, 0.f};
-
-  // fragment offsets: lane l reads row (l%16) of a 16-row block, chunk l/16
+  // -------------------------------------------------------------- consumer
+  const int c = wave;
   const int fr = lane & 15, fc = lane >> 4;
   const uint32_t fo = swz(fr, fc);
-
-  // Loads (every wave, in issue order): raw(0), then per stage q = 0, 1, 2, ...
-  // the group {raw(q+1), x(q)}; group q+3 is issued in stage q (past the end,
-  // the last stage is re-loaded into the free slots).  At the top of stage kt
-  // groups kt+1 and kt+2 are younger than group kt: 2*GRPL loads.
-  issue_raw(0);
-  for (int q = 0; q < XRING - 1; ++q) {
-    issue_raw(q + 1);
-    issue_x(min(q, nk - 1));
-  }
-  vm_wait<(XRING - 1) * GRPL>();  // raw(0)
-  __syncthreads();
-  if (dwave) {
-    uint32_t o[8];
-    decode(0, o);
-    store_b(0, o);
-  }
-  for (int kt = 0; kt < nk; ++kt) {
-    vm_wait<2 * GRPL>();  // group kt: x(kt), raw(kt+1)
-    __syncthreads();      // ... for every wave, and B(kt) is written; slot (kt-1) % XRING and B(kt-1) are free
-    issue_raw(kt + XRING);
-    issue_x(min(kt + XRING - 1, nk - 1));
-    uint32_t o[8];
-    if (dwave) decode(min(kt + 1, nk - 1), o);  // stage kt+1 (its raw bytes came with group kt)
-    const uint8_t* xs = lds + (kt % XRING) * XSTAGE;
-    const uint8_t* bs = lds + BOFF + (kt & 1) * BPART;
-    // every fragment of the stage first (one LDS latency per stage), then the MFMAs
-    half8 bf[NBW], af[3][2];
+  // A fragment (part, i): row c*32 + 16i + fr of the tile, halfs 8fc.. of stage q
+  const uint16_t* xa[3][2];
 #pragma unroll
-    for (int jj = 0; jj < NBW; ++jj) bf[jj] = *(const half8*)(bs + min(2 * jj + wn, NB - 1) * 1024 + fo);
+  for (int part = 0; part < 3; ++part)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      xa[part][i] = Xg + part * p.xs + (size_t)min(m0 + c * 32 + i * 16 + fr, M - 1) * p.K + 8 * fc;
+  u32x4 A[XR][3][2];
+  auto loadA = [&](int q, u32x4 (&dst)[3][2]) __attribute__((always_inline)) {
+    const int qq = min(q, nk - 1);  // past the end: a re-read, so every stage issues 6 loads
 #pragma unroll
     for (int part = 0; part < 3; ++part)
 #pragma unroll
-      for (int i = 0; i < 2; ++i) af[part][i] = *(const half8*)(xs + part * XPART + (wm * 32 + i * 16) * 64 + fo);
-    // parts lo, mid, hi (tier.cpp:940) into one fp32 accumulator
+      for (int i = 0; i < 2; ++i) dst[part][i] = gload16(xa[part][i] + qq * QBK);
+  };
+  float4v acc[2][NB];
 #pragma unroll
-    for (int part = 2; part >= 0; --part) {
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int jj = 0; jj < NBW; ++jj)
-        if ((NB & 1) == 0 || jj < NBW - 1 || wn == 0)  // odd NB: the last block is wave-column 0's
+    for (int j = 0; j < NB; ++j) acc[i][j] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int d = 0; d < XR - 1; ++d) loadA(d, A[d]);
+  for (int q0 = 0; q0 < nk; q0 += XR) {  // nk is a multiple of 8
+#pragma unroll
+    for (int u = 0; u < XR; ++u) {
+      const int q = q0 + u;
+      loadA(q + XR - 1, A[(u + XR - 1) % XR]);
+      vm_wait<6 * (XR - 1)>();  // stage q's fragments are in registers
+#pragma unroll
+      for (int part = 0; part < 3; ++part)
+#pragma unroll
+        for (int i = 0; i < 2; ++i) asm volatile("" : "+v"(A[u][part][i]));
+      const int sl = q % FL;
+      poll4(ready + 4 * sl, q);
+      const uint8_t* bs = lds + (q % NBR) * BPART;
+      half8 bf[NB];
+#pragma unroll
+      for (int j = 0; j < NB; ++j) bf[j] = *(const half8*)(bs + j * 1024 + fo);
+      // parts lo, mid, hi (tier.cpp:940) into one fp32 accumulator
+#pragma unroll
+      for (int part = 2; part >= 0; --part)
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
 #pragma unroll
           for (int i = 0; i < 2; ++i)
-            acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[part][i], bf[jj], acc[i][jj], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, A[u][part][i]), bf[j],
+                                                               acc[i][j], 0, 0, 0);
+      if (lane == 0) lds_rel(&done[4 * sl + c], q);
     }
-    if (dwave) store_b((kt + 1) & 1, o);
   }
-  vm_wait<0>();  // drain the re-loads past the end
+  vm_wait<0>();  // drain the re-reads past the end
 
   // epilogue: register i of lane l holds row 4*(l/16) + i, column l%16 of a 16x16 block
 #pragma unroll
-  for (int jj = 0; jj < NBW; ++jj) {
-    const int j = 2 * jj + wn;
+  for (int j = 0; j < NB; ++j) {
     const int col = n0 + j * 16 + (lane & 15);
-    if (j >= NB || col >= p.N) continue;
+    if (col >= p.N) continue;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int row = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + r;
+        const int row = m0 + c * 32 + i * 16 + 4 * (lane >> 4) + r;
         if (row >= M) continue;
-        float* c = Yg + (size_t)row * p.ldy + col;
-        float v = acc[i][jj][r];
-        if (p.beta != 0.f) v = fmaf(p.beta, *c, v);
-        *c = v;
+        float* cp = Yg + (size_t)row * p.ldy + col;
+        float v = acc[i][j][r];
+        if (p.beta != 0.f) v = fmaf(p.beta, *cp, v);
+        *cp = v;
       }
   }
 }
 
 template <int BN>
 int launch_q(const QArgs& a, hipStream_t s, const char* who) {
-  constexpr size_t lds = (size_t)XRING * 3 * XPART + 2 * (size_t)BN * 64 + (size_t)XRING * ((BN * 48 + 1023) / 1024) * 1024 + 1024;
+  constexpr int PR = BN / 4, RSLOT = (PR * 48 + 1023) / 1024 * 1024;
+  constexpr size_t lds = 3 * (size_t)BN * 64 + 4 * 8 * (size_t)RSLOT + 2 * 4 * 4 * 4;
   static_assert(lds <= 160 * 1024, "LDS budget");
   static bool attr_set = false;
   if (!attr_set) {
@@ -261,6 +275,7 @@ int launch_q(const QArgs& a, hipStream_t s, const char* who) {
   TM_LAUNCH_CHECK(who);
   return TIERMM_OK;
 }
+
 
 // Tiles of one BN over the groups' row counts.
 long q_tiles(const int* rows, int n, int N, int bn) {
