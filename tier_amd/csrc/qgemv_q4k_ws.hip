@@ -1,219 +1,301 @@
-// qgemv_q4k_ws.hip -- Q4_K decode GEMV with a producer wave per workgroup.
+// qgemv_q4k_ws.hip -- Q4_K decode GEMV for tall matrices: a workgroup streams
+// one 16-row tile at a time through producer waves.
 //
-// Same arithmetic and LDS layouts as qgemv_q4k.hip (gemv_q, tier.cpp:299-306;
-// q_val Q4_K, quant.h:83-84).  The difference is who moves the weights: one
-// wave of the workgroup does nothing but issue the global->LDS loads into a
-// ring of NS stages shared by the workgroup, keeping D stages in flight, while
-// the NC consumer waves prepare x and run the MFMA + scale work.  A consumer
-// that computes therefore never holds back the weight stream, and the x
-// preparation at the start overlaps D stages of loads.
+// Same arithmetic and x digit layout as qgemv_q4k.hip (gemv_q, tier.cpp:299-306;
+// q_val Q4_K, quant.h:83-84); q4k_mfma.h holds the shared pieces.
 //
-// Stage order: q = gi * NC + c (consumer c fastest, gi = c's group index), so
-// the consumers advance together; stage q lives in ring slot q % NS.
-// Hand-off through two LDS flag arrays (values are stage numbers):
-//   full[slot] = q  -- set by the producer once stage q has landed (its own
-//                      vmcnt wait: loads retire in order);
-//   done[slot] = q  -- set by the consumer when it has read stage q.
-// The producer reuses a slot for stage q only after done[slot] == q - NS.
-// Every wait is for a stage that is already issued (full) or already marked
-// full (done), so all waves finish: the producer marks stage q - D right after
-// issuing q, and waits only on stages numbered <= q - NS < q - D.
+// Work split.  Workgroup w takes the row tiles w, w + G, w + 2G, ... (G = the
+// grid, R tiles each), so at any moment the chip reads a compact window of
+// consecutive tiles, and it streams them one after another.  A tile is cut
+// into stages of GS super-blocks: each of the 4 producer waves (one per SIMD)
+// brings 4 of the 16 rows (4 row segments of GS*144 bytes) into a ring of NS
+// slots of its own with global_load_lds_dwordx4, D stages ahead.  Long row
+// segments and few concurrent tiles measured faster than 16 short segments
+// per wave from 864 tiles at once (13824x5120: 8.9 against 9.2 us; 10240x8192:
+// 10.4 against 11.8 us).
+//
+// Consumers.  GS == NC: consumer c owns super-block column c of every stage,
+// i.e. columns c, c + NC, ... of every row, so the x digits and the x metadata
+// it needs sit in its registers from the start (MS columns) and its LDS reads
+// are the weight bytes alone.  Its partial sum of each tile goes to LDS; after
+// the last tile the workgroup adds the NC partials of each row in a fixed order.
+//
+// Hand-off through LDS flags holding stage numbers, which only grow:
+//   full[slot][p] = q  -- producer p's rows of stage q have landed (its own
+//                         vmcnt wait: loads retire in order);
+//   done[slot][c] = q  -- consumer c is past stage q (set without waiting
+//                         when the stage holds no column of c).
+// A producer refills a slot with stage q once every done[slot][.] >= q - NS;
+// a consumer reads stage q once every full[slot][.] >= q.  Every wait ends: a
+// producer has marked stage q - D full before it issues q, and it waits only
+// for stages <= q - NS < q - D, which all consumers can finish; consumers wait
+// only for stages that are issued and are marked full in order.
+#include <climits>
+
 #include "q4k_mfma.h"
 
 namespace tiermm {
 namespace {
 
-__device__ __forceinline__ int lds_acquire(const int* p) {
-  return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-__device__ __forceinline__ void lds_release(int* p, int v) {
+constexpr int NP = 4;      // producer waves
+constexpr int PROWS = 4;   // rows of a tile per producer
+constexpr int GTILE = 224; // target grid: tiles per workgroup R = ceil(tiles / GTILE)
+
+constexpr int pad4(int n) { return (n + 3) / 4 * 4; }
+
+__device__ __forceinline__ void lds_rel(int* p, int v) {
   __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// Marks the stages still in flight as they land: with `total - marked`
-// outstanding, the oldest has landed once at most R younger ones are.
-template <int R, int NLD, int NS>
-__device__ __forceinline__ void drain(int total, int& marked, int* full) {
-  if constexpr (R >= 0) {
-    if (total - marked > R) {
-      vm_wait<NLD * R>();
-      lds_release(&full[marked % NS], marked);
-      ++marked;
+// Waits until the NF (a multiple of 4) flags at f (16-byte aligned, LDS) are
+// all >= v, reading them 16 bytes at a time.  The data they publish is read
+// after this returns (the empty asm keeps those reads below the loop).
+template <int NF>
+__device__ __forceinline__ void poll_ge(const int* f, int v) {
+  typedef int i4 __attribute__((ext_vector_type(4)));
+  const volatile __attribute__((address_space(3))) i4* fl =
+      (const volatile __attribute__((address_space(3))) i4*)(size_t)lds_addr(f);
+  for (;;) {
+    int m = INT_MAX;
+#pragma unroll
+    for (int j = 0; j < NF / 4; ++j) {
+      const i4 t = fl[j];
+      m = min(m, min(min(t[0], t[1]), min(t[2], t[3])));
     }
-    drain<R - 1, NLD, NS>(total, marked, full);
+    if (m >= v) break;
+    __builtin_amdgcn_s_sleep(1);
   }
+  asm volatile("" ::: "memory");
 }
 
-// CT row tiles x CK K-splits = NC consumer waves, plus NP producer waves
-// (waves NC..NC+NP-1); producer p serves consumers c with c % NP == p through
-// a ring of its own.
-template <int CT, int CK, int NP, int GS, int NS, int D, int XP, int XK>
-__global__ __launch_bounds__(64 * (CT * CK + NP)) void qgemv_q4k_ws(const uint8_t* __restrict__ W, size_t rb,
-                                                                 const float* __restrict__ x,
-                                                                 float* __restrict__ y, int N, int K) {
-  static_assert(D >= 1 && NS > D, "ring deeper than the loads in flight");
-  static_assert(Stage<GS>::NLD * D <= 63, "vmcnt counts at most 63 loads");
-  constexpr int NC = CT * CK, NL = NC / NP;  // NL consumers per producer
-  static_assert(NC % NP == 0, "every producer serves the same number of consumers");
-  static_assert(NC + NP <= 16, "at most 1024 threads per workgroup");
-  constexpr int GRP = Stage<GS>::GRP, SBYTES = Stage<GS>::BYTES, NLD = Stage<GS>::NLD;
-  extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // NP*NS*SBYTES + NC*64 + 2*NP*NS*4
-  __shared__ __attribute__((aligned(16))) uint8_t xlds[xq_bytes(XK)];
-  const int nsb_all = K >> 8;
-  uint8_t* xq = xlds;
-  float* meta = (float*)(xq + nsb_all * XQ_SB);
-  uint8_t* zero = xq + nsb_all * (XQ_SB + META_SB);
-  float* red = (float*)(ring + NP * NS * SBYTES);
+template <int NC, int NS, int R>
+struct WsLayout {
+  static constexpr int GS = NC;                                 // super-blocks per stage
+  static constexpr int GRP = GS * SB_BYTES;                     // one row's segment
+  static constexpr int SLOT = PROWS * GRP;                      // one producer's part of a stage
+  static constexpr int NLD = (SLOT + 1023) / 1024;              // 1 KiB loads per part
+  static constexpr int LAST = (SLOT - (NLD - 1) * 1024) / 16;   // lanes of the last load
+  static constexpr int NCP = pad4(NC);
+  static constexpr size_t RING = (size_t)NP * NS * SLOT;
+  static constexpr size_t LDS = RING + NS * NP * 4 + NS * NCP * 4 + (size_t)R * NC * 16 * 4;
+};
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  // K split: consumer k of a tile takes super-blocks [sbk(k), sbk(k+1)); all
-  // splits are given the same number of groups (short ones re-read and skip).
-  const int ngrp = ((nsb_all + CK - 1) / CK + GS - 1) / GS;
-  const int total = ngrp * NL;  // stages of one producer
+// The q4k_superblock arithmetic with this lane's A operands (x digits of the
+// super-block column) and x metadata already in registers.
+__device__ __forceinline__ float q4k_superblock_reg(const uint8_t* hp, int g, const i32x4 (&A)[4], const float4 mt,
+                                                    float acc) {
+  const u32x4 H = *(const u32x4*)hp;
+  const u32x4 cA = *(const u32x4*)(hp + 16 + 16 * g);
+  const u32x4 cB = *(const u32x4*)(hp + 80 + 16 * g);
+  i32x4 B0, B1, B2, B3;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    B0[w] = (int)(cA[w] & 0x0f0f0f0fu);
+    B1[w] = (int)((cA[w] >> 4) & 0x0f0f0f0fu);
+    B2[w] = (int)(cB[w] & 0x0f0f0f0fu);
+    B3[w] = (int)((cB[w] >> 4) & 0x0f0f0f0fu);
+  }
+  const i32x4 z = {0, 0, 0, 0};
+  i32x4 Ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], B0, z, 0, 0, 0);
+  Ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[1], B1, Ca, 0, 0, 0);
+  i32x4 Cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[2], B2, z, 0, 0, 0);
+  Cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[3], B3, Cb, 0, 0, 0);
+  // |C| <= 32*15*128: both halves below 2^24, so the two conversions are exact
+  const float Da = fmaf((float)(Ca[3] * 256 + Ca[2]), 65536.f, (float)(Ca[1] * 256 + Ca[0]));
+  const float Db = fmaf((float)(Cb[3] * 256 + Cb[2]), 65536.f, (float)(Cb[1] * 256 + Cb[0]));
+  const int sh = 8 * g;  // scale byte of sub-blocks g and 4+g (quant.h:47-48)
+  const uint32_t hy = H[1], hz = H[2], hw = H[3];
+  const int sca = (hy >> sh) & 63, mna = (hz >> sh) & 63;
+  const int scb = ((hw >> sh) & 15) | (((hy >> (sh + 6)) & 3) << 4);
+  const int mnb = ((hw >> (sh + 4)) & 15) | (((hz >> (sh + 6)) & 3) << 4);
+  const float d = h2f(H[0] & 0xffffu), dmin = h2f(H[0] >> 16);
+  const float u = fmaf((float)scb * mt.y, Db, (float)sca * mt.x * Da);
+  const float m = fmaf((float)mnb, mt.w, (float)mna * mt.z);
+  acc = fmaf(d, u, acc);
+  return fmaf(-dmin, m, acc);
+}
+
+template <int R, int NC, int NS, int D, int XP, int XK>
+__global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __restrict__ W, size_t rb,
+                                                            const float* __restrict__ x, float* __restrict__ y,
+                                                            int N, int K) {
+  using L = WsLayout<NC, NS, R>;
+  constexpr int GS = L::GS, GRP = L::GRP, SLOT = L::SLOT, NLD = L::NLD, NCP = L::NCP;
+  constexpr int MS = (XK / 256 + GS - 1) / GS;  // super-block columns per consumer
+  static_assert(NLD * D <= 63, "vmcnt counts at most 63 loads");
+  static_assert(D >= 1 && NS > D, "ring deeper than the stages in flight");
+  static_assert(NC + NP <= 16, "at most 1024 threads per workgroup");
+  static_assert(SLOT % 16 == 0, "16-byte aligned slots");
+  extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // L::LDS bytes
+  __shared__ __attribute__((aligned(16))) uint8_t xlds[xq_bytes(XK)];
+  int* full = (int*)(ring + L::RING);  // [NS][NP]
+  int* done = full + NS * NP;          // [NS][NCP]
+  float* red = (float*)(done + NS * NCP);  // [R][NC][16]
+  const int nsb = K >> 8, ngrp = (nsb + GS - 1) / GS, total = R * ngrp;
+  const int tiles = (N + 15) >> 4;
+  uint8_t* xq = xlds;
+  float* meta = (float*)(xq + nsb * XQ_SB);
+  uint8_t* zero = xq + nsb * (XQ_SB + META_SB);
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
   if (wave >= NC) {
     // ------------------------------------------------------------ producer
     const int p = wave - NC;
-    int* full = (int*)(red + NC * 16) + 2 * NS * p;
-    int* done = full + NS;
-    if (lane < NS) {
-      full[lane] = -1;
-      done[lane] = -1;
-    }
-    // per-lane byte of the stage image: row and column within the group
+    if (lane < NS) full[NP * lane + p] = -1;
+    if (p == 0)  // consumer flags; padding entries never hold a wait back
+      for (int i = lane; i < NS * NCP; i += 64) done[i] = (i % NCP) < NC ? -1 : INT_MAX;
+    // byte f of a slot: row f / GRP of the producer's 4, byte f % GRP of its segment
     int roff[NLD], coff[NLD];
 #pragma unroll
     for (int j = 0; j < NLD; ++j) {
-      const int f = min(j * 1024 + lane * 16, SBYTES - 16);
+      const int f = min(j * 1024 + lane * 16, SLOT - 16);
       roff[j] = f / GRP;
       coff[j] = f % GRP;
     }
-    const uint32_t ring_lds = lds_addr(ring + p * NS * SBYTES);
+    const uint32_t ring_lds = lds_addr(ring + p * NS * SLOT);
     auto issue = [&](int q) __attribute__((always_inline)) {
-      const int c = (q % NL) * NP + p, gi = q / NL;
-      const int t = c / CK, k = c % CK;
-      const int row0 = (blockIdx.x * CT + t) * 16;
-      const int rbase = min(row0, N - 1), rmax = min(15, N - 1 - rbase);
-      const int sbk = k * nsb_all / CK, nsb = (k + 1) * nsb_all / CK - sbk;
-      const uint8_t* base0 = W + (size_t)rbase * rb + (size_t)sbk * SB_BYTES;
-      int ro[NLD];
+      const int r = q / ngrp, gi = q - r * ngrp;
+      // a tile past the last one (its workgroup has fewer) re-reads the last tile
+      const int tile = min((int)blockIdx.x + r * (int)gridDim.x, tiles - 1);
+      const int rbase = min(tile * 16 + PROWS * p, N - 1), rmax = min(PROWS - 1, N - 1 - rbase);
+      // bytes past the row's last super-block re-read the last valid 16 bytes
+      const int lastb = min(GS, nsb - GS * gi) * SB_BYTES - 16;
+      const uint8_t* b = W + (size_t)rbase * rb + (size_t)gi * GRP;
+      const uint32_t dst = ring_lds + (q % NS) * SLOT;
 #pragma unroll
-      for (int j = 0; j < NLD; ++j) ro[j] = min(roff[j], rmax);
-      load_group<GS>(base0, rb, ro, coff, lane, gi, nsb, ring_lds + (q % NS) * SBYTES);
+      for (int j = 0; j < NLD; ++j)
+        if (j < NLD - 1 || L::LAST == 64 || lane < L::LAST)
+          dma16(b + (size_t)min(roff[j], rmax) * rb + min(coff[j], lastb), dst + j * 1024);
     };
     const int pro = min(D, total);
     for (int q = 0; q < pro; ++q) issue(q);
     __syncthreads();  // flags initialised; consumers have prepared x
     int marked = 0;   // stages marked full so far
     for (int q = D; q < total; ++q) {
-      if (q >= NS)
-        while (lds_acquire(&done[q % NS]) != q - NS) __builtin_amdgcn_s_sleep(1);
+      if (q >= NS) poll_ge<NCP>(done + (q % NS) * NCP, q - NS);
       issue(q);
       vm_wait<NLD * D>();  // stage q - D has landed
-      lds_release(&full[marked % NS], marked);
+      if (lane == 0) lds_rel(&full[NP * (marked % NS) + p], marked);
       ++marked;
     }
-    // drain: the last min(D, total) stages, oldest first
-    drain<D - 1, NLD, NS>(total, marked, full);
-    __syncthreads();  // the consumers' partial sums are in red[]
-    return;
-  }
-
-  // -------------------------------------------------------------- consumers
-  const int c = wave, t = c / CK, k = c % CK;
-  const int n = lane & 15, g = lane >> 4;
-  const int* full = (const int*)(red + NC * 16) + 2 * NS * (c % NP);
-  int* done = (int*)full + NS;
-  const uint8_t* myring = ring + (c % NP) * NS * SBYTES;
-  const int row0 = (blockIdx.x * CT + t) * 16;
-  const int sbk = k * nsb_all / CK, nsb = (k + 1) * nsb_all / CK - sbk;
-  constexpr int NT = 64 * NC;
-
-  // x: one thread per 16 elements (threads past K/16 load a clamped copy and skip)
-  u32x4 xr[XP][4];
+    vm_wait<0>();
+    for (; marked < total; ++marked)
+      if (lane == 0) lds_rel(&full[NP * (marked % NS) + p], marked);
+    __syncthreads();  // partial sums are in red[]
+  } else {
+    // -------------------------------------------------------------- consumers
+    const int c = wave, n = lane & 15, g = lane >> 4;
+    constexpr int NT = 64 * NC;
+    // x: one thread per 16 elements (threads past K/16 load a clamped copy and skip)
+    u32x4 xr[XP][4];
 #pragma unroll
-  for (int j = 0; j < XP; ++j) {
-    const int hh = min(tid + j * NT, (K >> 4) - 1);
+    for (int j = 0; j < XP; ++j) {
+      const int hh = min(tid + j * NT, (K >> 4) - 1);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) xr[j][i] = *(const u32x4*)(x + hh * 16 + 4 * i);
-  }
-  for (int i = tid; i < ZERO_BYTES / 4; i += NT) ((uint32_t*)zero)[i] = 0u;
-#pragma unroll
-  for (int j = 0; j < XP; ++j) {
-    const int hh = tid + j * NT;
-    if (hh < (K >> 4)) {
-      float v[16];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int w = 0; w < 4; ++w) v[4 * i + w] = __uint_as_float(xr[j][i][w]);
-      prep_half(hh >> 1, hh & 1, v, xq, meta);
+      for (int i = 0; i < 4; ++i) xr[j][i] = *(const u32x4*)(x + hh * 16 + 4 * i);
     }
-  }
-  __syncthreads();
-
-  uint32_t aoff[2], astep[2];
+    for (int i = tid; i < ZERO_BYTES / 4; i += NT) ((uint32_t*)zero)[i] = 0u;
 #pragma unroll
-  for (int p = 0; p < 2; ++p) {
-    const bool live = (n >> 2) == 2 * (g >> 1) + p;
-    aoff[p] = live ? (uint32_t)(sbk * XQ_SB + g * 64 + (n & 3) * 16) : (uint32_t)(zero - xlds);
-    astep[p] = live ? (uint32_t)XQ_SB : 0u;
-  }
-  float acc = 0.f;
-  for (int gi = 0; gi < ngrp; ++gi) {
-    const int q = gi * NL + c / NP, slot = q % NS;
-    while (lds_acquire(&full[slot]) != q) __builtin_amdgcn_s_sleep(1);
-    const uint8_t* st = myring + slot * SBYTES;
+    for (int j = 0; j < XP; ++j) {
+      const int hh = tid + j * NT;
+      if (hh < (K >> 4)) {
+        float v[16];
 #pragma unroll
-    for (int i = 0; i < GS; ++i) {
-      const int sb = GS * gi + i;
-      if (sb < nsb)
-        acc = q4k_superblock(st + n * GRP + i * SB_BYTES, g, xlds + aoff[0] + (uint32_t)sb * astep[0],
-                             xlds + aoff[1] + (uint32_t)sb * astep[1], meta + (sbk + sb) * 16 + g * 4, acc);
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int w = 0; w < 4; ++w) v[4 * i + w] = __uint_as_float(xr[j][i][w]);
+        prep_half(hh >> 1, hh & 1, v, xq, meta);
+      }
     }
-    lds_release(&done[slot], q);
-  }
-
-  acc += __shfl_xor(acc, 16, 64);
-  acc += __shfl_xor(acc, 32, 64);
-  if (g == 0) red[c * 16 + n] = acc;
-  __syncthreads();
-  if (k == 0 && g == 0) {
-    float s = 0.f;
+    __syncthreads();
+    // this lane's A operands of its columns c + GS*m (zeros where it carries no digit)
+    i32x4 A[MS][4];
+    float4 mt[MS];
 #pragma unroll
-    for (int kk = 0; kk < CK; ++kk) s += red[(t * CK + kk) * 16 + n];
-    if (row0 + n < N) y[row0 + n] = s;
+    for (int m = 0; m < MS; ++m) {
+      const int sb = min(GS * m + c, nsb - 1);
+      uint32_t off[2];
+#pragma unroll
+      for (int pp = 0; pp < 2; ++pp)
+        off[pp] = (n >> 2) == 2 * (g >> 1) + pp ? (uint32_t)(sb * XQ_SB + g * 64 + (n & 3) * 16)
+                                                : (uint32_t)(zero - xlds);
+      A[m][0] = *(const i32x4*)(xlds + off[0]);
+      A[m][1] = *(const i32x4*)(xlds + off[1] + XQ_T);
+      A[m][2] = *(const i32x4*)(xlds + off[0] + 2 * XQ_T);
+      A[m][3] = *(const i32x4*)(xlds + off[1] + 3 * XQ_T);
+      mt[m] = *(const float4*)(meta + sb * 16 + g * 4);
+    }
+    // row n of a stage: producer n / 4's slot, row n % 4 of it; column c
+    const uint8_t* rowbase = ring + (n / PROWS) * NS * SLOT + (n % PROWS) * GRP + c * SB_BYTES;
+    for (int r = 0; r < R; ++r) {
+      float acc = 0.f;
+#pragma unroll
+      for (int gi = 0; gi < MS; ++gi) {
+        if (gi < ngrp) {
+          const int q = r * ngrp + gi, slot = q % NS;
+          if (GS * gi + c < nsb) {
+            poll_ge<NP>(full + NP * slot, q);
+            acc = q4k_superblock_reg(rowbase + slot * SLOT, g, A[gi], mt[gi], acc);
+          }
+          if (lane == 0) lds_rel(&done[slot * NCP + c], q);
+        }
+      }
+      acc += __shfl_xor(acc, 16, 64);
+      acc += __shfl_xor(acc, 32, 64);
+      if (g == 0) red[(r * NC + c) * 16 + n] = acc;
+    }
+    __syncthreads();
+  }
+  for (int i = tid; i < R * 16; i += 64 * (NC + NP)) {
+    const int r = i >> 4, n = i & 15;
+    const int tile = (int)blockIdx.x + r * (int)gridDim.x;
+    if (tile < tiles && tile * 16 + n < N) {
+      float s = 0.f;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) s += red[(r * NC + c) * 16 + n];
+      y[tile * 16 + n] = s;
+    }
   }
 }
 
-template <int CT, int CK, int NP, int GS, int NS, int D, int XP, int XK>
+template <int R, int NC, int NS, int D, int XP, int XK>
 int launch_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
-  constexpr int NC = CT * CK;
-  constexpr size_t lds = (size_t)NP * NS * Stage<GS>::BYTES + NC * 64 + 2 * NP * NS * 4;  // plus the static x digits
-  static_assert(xq_bytes(XK) + lds <= 160 * 1024, "LDS budget");
+  using L = WsLayout<NC, NS, R>;
+  static_assert(xq_bytes(XK) + L::LDS <= 160 * 1024, "LDS budget");
   static_assert(XK / 16 <= 64 * NC * XP, "x preparation: one thread per 16 elements");
   const int tiles = (N + 15) / 16;
-  const unsigned grid = (unsigned)((tiles + CT - 1) / CT);
+  const unsigned grid = (unsigned)((tiles + R - 1) / R);
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)qgemv_q4k_ws<CT, CK, NP, GS, NS, D, XP, XK>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipError_t e = hipFuncSetAttribute((const void*)qgemv_q4k_ws<R, NC, NS, D, XP, XK>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)L::LDS);
     if (e != hipSuccess) return hip_fail(e, "tiermm_qgemv: q4_K LDS attribute");
     attr_set = true;
   }
-  qgemv_q4k_ws<CT, CK, NP, GS, NS, D, XP, XK><<<grid, 64 * (NC + NP), lds, s>>>((const uint8_t*)W, rb, x, y, N, K);
+  qgemv_q4k_ws<R, NC, NS, D, XP, XK><<<grid, 64 * (NC + NP), L::LDS, s>>>((const uint8_t*)W, rb, x, y, N, K);
   TM_LAUNCH_CHECK("tiermm_qgemv: q4_K launch");
   return TIERMM_OK;
 }
 
+template <int NC, int NS, int D, int XP, int XK>
+int launch_ws_r(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
+  const int tiles = (N + 15) / 16, r = (tiles + GTILE - 1) / GTILE;
+  if (r <= 3) return launch_ws<3, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
+  if (r == 4) return launch_ws<4, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
+  if (r == 5) return launch_ws<5, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
+  if (r == 6) return launch_ws<6, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
+  return launch_ws<8, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
+}
+
 }  // namespace
 
-// Tall matrices (enough row tiles for every CU at four tiles per workgroup):
-// 4 tiles x 2 K-halves of consumers and one producer per SIMD, each with a
-// ring of four 2-super-block stages, two in flight.
+// Tall matrices (at least 640 row tiles).  Tiles per workgroup: the grid lands
+// near 224 workgroups (a uniform count per workgroup measured faster than a
+// ragged one).  Stages of 12 super-blocks up to K = 5120 (x digits of two
+// columns per consumer), of 8 up to 8192 (four columns).
 int qgemv_q4k_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
-  if (K <= 5120) return launch_ws<4, 2, 4, 2, 4, 2, 1, 5120>(W, rb, x, y, N, K, s);
-  if (K <= 8192) return launch_ws<4, 2, 4, 2, 4, 2, 1, 8192>(W, rb, x, y, N, K, s);
+  if (K <= 5120) return launch_ws_r<12, 4, 2, 1, 5120>(W, rb, x, y, N, K, s);
+  if (K <= 8192) return launch_ws_r<8, 4, 2, 1, 8192>(W, rb, x, y, N, K, s);
   return set_error(TIERMM_UNSUPPORTED, "tiermm_qgemv: q4_K K=%d above %d", K, 8192);
 }
 
