@@ -142,6 +142,23 @@ def test_gemv_q4k_tall_ragged(gpu, N, K):
     assert oracle.rel_fro(y, oracle.gemv_f64(blocks, t, x, N, K)) <= TOL
 
 
+@pytest.mark.parametrize("N,K", [(10256, 2048), (13824, 5120), (16390, 2048), (20000, 768), (28700, 1024),
+                                 (40000, 512), (14000, 8192)])
+def test_gemv_q4k_tall_tiles_per_workgroup(gpu, N, K):
+    """The tall q4_K kernel at each count of row tiles per workgroup it is built for
+    (3, 4, 5, 6 and 8; 40000 rows need more workgroups than CUs), with workgroups that
+    hold fewer tiles than the others and partial last row tiles (16390, 28700)."""
+    t = tier_amd.Q4_K
+    rng = np.random.default_rng(7 * N + K)
+    blocks = oracle.random_blocks(rng, t, N * (K // 256)).reshape(N, -1)
+    x = rng.standard_normal(K).astype(np.float32)
+    y = _gemv(blocks, t, x, N, K)
+    want = oracle.gemv_f64(blocks, t, x, N, K)
+    assert oracle.rel_fro(y, want) <= TOL
+    # every row written, none left at the 0xff fill
+    assert np.all(np.isfinite(y))
+
+
 def test_gemv_zero_and_extreme_inputs(gpu):
     t, N, K = tier_amd.Q4_K, 64, 1024
     blocks = quantized_weight(t, N, K, seed=5)
