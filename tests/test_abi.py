@@ -130,7 +130,9 @@ def test_workspace_sizes():
     assert tier_amd.x3_gemm_ws_bytes(5120, 4096, 5120) == 3 * 4096 * 5120 * 2 + 5120 * 5120 * 2
     assert tier_amd.x3_rows_ws_bytes(256, 5120, 14336) == 3 * 256 * 5120 * 2
     # q4_K decodes W inside the GEMM: only the three fp16 planes of x
-    assert tier_amd.qgemm_ws_bytes(tier_amd.Q4_K, 512, 5120, 5120) == 3 * 512 * 5120 * 2
+    # fused q4_K path: the x planes, then split-K partial sums (2 splits at this shape on 256 CUs)
+    assert tier_amd.qgemm_ws_bytes(tier_amd.Q4_K, 512, 5120, 5120) == 3 * 512 * 5120 * 2 + 2 * 512 * 5120 * 4
+    assert tier_amd.qgemm_ws_bytes(tier_amd.Q4_K, 512, 14336, 5120) == 3 * 512 * 5120 * 2
     # other types stage fp16 W in the workspace as well
     assert tier_amd.qgemm_ws_bytes(tier_amd.Q6_K, 512, 5120, 5120) == 5120 * 5120 * 2 + 3 * 512 * 5120 * 2
     # routed experts: 256-row tiles that fill the chip stage the fp16 weights of

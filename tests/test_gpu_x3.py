@@ -173,6 +173,48 @@ def test_qgemm_q4k_fused_shapes(gpu, M, N, K, beta):
     assert oracle.rel_fro(got, ref) <= BAR
 
 
+@pytest.mark.parametrize("bn,ks", [(160, 1), (160, 2), (160, 4), (128, 2), (112, 4), (96, 2), (80, 4), (64, 2),
+                                   (64, 1)])
+@pytest.mark.parametrize("M,N,K,beta", [(300, 1000, 1024, 1.0), (512, 352, 2048, 0.0)])
+def test_qgemm_q4k_tile_plans(gpu, monkeypatch, bn, ks, M, N, K, beta):
+    """Every tile width and split-K factor of the fused q4_K kernel, forced through
+    TIERMM_QGEMM_TILE: partial M and N tiles, the split-K reduce with beta = 1, and the
+    workspace query sized for the partial sums."""
+    monkeypatch.setenv("TIERMM_QGEMM_TILE", f"{bn},{ks}")
+    t = tier_amd.Q4_K
+    assert tier_amd.qgemm_ws_bytes(t, M, N, K) == 3 * M * K * 2 + (ks * M * N * 4 if ks > 1 else 0)
+    rng = np.random.default_rng(M + N + K + bn + ks)
+    blocks = oracle.random_blocks(rng, t, N * (K // 256)).reshape(N, -1)
+    x = activations(M, K, seed=23)
+    y0 = rng.standard_normal((M, N)).astype(np.float32)
+    W, X, Y = hip.to_device(blocks), hip.to_device(x), hip.to_device(y0)
+    tier_amd.qgemm(W.ptr, t, tier_amd.q_row_bytes(t, K), X.ptr, Y.ptr, M, N, K, beta=beta)
+    hip.synchronize()
+    got = Y.download(np.float32, M * N).reshape(M, N)
+    w16 = oracle.h2f(oracle.dequant(blocks, t, K, oracle.OUT_F16)).reshape(N, K)
+    ref = x.astype(np.float64) @ w16.astype(np.float64).T + beta * y0.astype(np.float64)
+    assert np.all(np.isfinite(got))
+    assert oracle.rel_fro(got, ref) <= BAR
+
+
+@pytest.mark.parametrize("N,K", [(5120, 5120), (5120, 14336)])
+def test_qgemm_m512_split_k_sampled(gpu, N, K):
+    """Config 3 shapes whose default plan splits K (wide tiles, two splits and the reduce);
+    fp64 check on sampled output rows."""
+    t, M = tier_amd.Q4_K, 512
+    blocks = quantized_weight(t, N, K, seed=35)
+    x = activations(M, K, seed=36)
+    W, X, Y = hip.to_device(blocks), hip.to_device(x), hip.DeviceBuffer(M * N * 4)
+    tier_amd.qgemm(W.ptr, t, tier_amd.q_row_bytes(t, K), X.ptr, Y.ptr, M, N, K)
+    hip.synchronize()
+    got = Y.download(np.float32, M * N).reshape(M, N)
+    rows = np.random.default_rng(3).choice(M, 48, replace=False)
+    w16 = oracle.h2f(oracle.dequant(blocks, t, K, oracle.OUT_F16)).reshape(N, K)
+    ref = x[rows].astype(np.float64) @ w16.astype(np.float64).T
+    assert np.all(np.isfinite(got))
+    assert oracle.rel_fro(got[rows], ref) <= BAR
+
+
 def test_qgemm_config3_m512_sampled(gpu):
     """Config 3 prefill: q4_K 14336x5120 at M=512; fp64 check on sampled output rows."""
     t, M, N, K = tier_amd.Q4_K, 512, 14336, 5120

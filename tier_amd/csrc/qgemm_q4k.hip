@@ -5,9 +5,14 @@
 // 293-298) followed by fp3gemm (tier.cpp:922-943) -- without writing W16 to
 // memory: the q4_K rows are decoded into an LDS B tile as the K loop needs them.
 //
-// Tiling: a workgroup owns BM=128 rows of X x BN rows of W (BN in 64..128, a
-// multiple of 16 picked per shape so the tile count fills the CUs), one K step
-// of 32 (one q4_K sub-block) per stage, v_mfma_f32_16x16x32_f16.  Its 8 waves
+// Tiling: a workgroup owns BM=128 rows of X x BN rows of W (BN in 64..160, a
+// multiple of 16), one K step of 32 (one q4_K sub-block) per stage,
+// v_mfma_f32_16x16x32_f16.  Optionally K is split KS ways (split-K): workgroup
+// kz of a tile covers K steps [kz*nk/KS, (kz+1)*nk/KS) and stores its partial
+// sums; a second kernel adds the KS partials in a fixed order.  (BN, KS) comes
+// from a cost model per shape (q_plan): rounds of workgroups over the CUs times
+// a per-workgroup time.  A wide BN reads fewer x bytes per MFMA, which is the
+// consumers' limit (below); split-K keeps the wide tiles numerous enough.  Its 8 waves
 // split into 4 consumers and 4 producers, one of each per SIMD, which hand
 // stages over through flags in LDS instead of a workgroup barrier:
 //   * consumer c multiplies x rows [32c, 32c+32) against all BN columns.  It
@@ -29,9 +34,14 @@
 // the consumers' x loads as the largest single cost (consumers alone: 125 us
 // with them, 57 us without, 122 us with every load hitting one cached address),
 // i.e. the vector-memory instructions themselves, not their latency.
+#include <cstdio>
+#include <cstdlib>
+
 #include "tm_device.h"
 
 namespace tiermm {
+
+int device_cus(int* cus);
 
 namespace {
 
@@ -51,6 +61,8 @@ struct QArgs {
   size_t rb;
   int ldy, N, K;
   float beta;
+  float* P;   // split K: partial sums of split kz at P + kz * ps, rows of N floats
+  size_t ps;
   int ngroups;
   int tile0[QG + 1];
   int row0[QG];
@@ -88,7 +100,7 @@ __device__ __forceinline__ void poll4(const int* f, int v) {
 // consumer has read stage q - NBR (the slot's previous user).  That is a stage
 // below q, whose ready every producer has published, so each wait ends; a
 // consumer waits only for its own loads and for ready.
-template <int BN>
+template <int BN, int KS>
 __global__ __launch_bounds__(512) void qgemm_q4k_x3ref(const QArgs p) {
   constexpr int NB = BN / 16;
   constexpr int NBR = 3, FL = 4, XR = 4, RR = 8, DR = 6;
@@ -98,7 +110,7 @@ __global__ __launch_bounds__(512) void qgemm_q4k_x3ref(const QArgs p) {
   constexpr int BPART = BN * 64;
   constexpr int RAWOFF = NBR * BPART;
   constexpr int FLAGOFF = RAWOFF + 4 * RR * RSLOT;
-  static_assert(BN % 16 == 0 && BN <= 128, "tile width");
+  static_assert(BN % 16 == 0 && BN <= 160, "tile width");
   static_assert(NBR <= FL && DR < RR && RAWI * DR <= 63, "ring depths");
   extern __shared__ __attribute__((aligned(16))) uint16_t lds_h[];
   uint8_t* lds = (uint8_t*)lds_h;
@@ -110,8 +122,11 @@ __global__ __launch_bounds__(512) void qgemm_q4k_x3ref(const QArgs p) {
   if (tid < 8 * FL) ready[tid] = -1;
 
   int grp = 0;
-  int b = (int)blockIdx.x;
   const int nt_all = p.tile0[p.ngroups];
+  // split kz of every tile is the kz-th copy of the tile sequence, so both
+  // splits of a tile go to the same XCD
+  int b = (int)blockIdx.x % nt_all;
+  const int kz = (int)blockIdx.x / nt_all;
   if (p.ngroups == 1 && (nt_all & 7) == 0) b = (b & 7) * (nt_all >> 3) + (b >> 3);
   while (grp + 1 < p.ngroups && b >= p.tile0[grp + 1]) ++grp;
   const int tile = b - p.tile0[grp];
@@ -121,7 +136,7 @@ __global__ __launch_bounds__(512) void qgemm_q4k_x3ref(const QArgs p) {
   const uint16_t* Xg = p.X + (size_t)p.row0[grp] * p.K;
   float* Yg = p.Y + (size_t)p.row0[grp] * p.ldy;
   const uint8_t* Wg = p.W[grp];
-  const int nk = p.K / QBK;
+  const int nk = p.K / QBK / KS, kq0 = kz * nk;  // this split's K steps (a multiple of 8)
   __syncthreads();  // flags initialised
 
   if (wave >= 4) {
@@ -138,21 +153,21 @@ __global__ __launch_bounds__(512) void qgemm_q4k_x3ref(const QArgs p) {
     const uint32_t raw0 = lds0 + RAWOFF + pw * RR * RSLOT;
     // raw bytes of stage q (q >= nk: stage nk - 1 again, into its own slot)
     auto issue = [&](int q) __attribute__((always_inline)) {
-      const int qq = min(q, nk - 1), sb = qq >> 3, s = qq & 7;
+      const int qq = kq0 + min(q, nk - 1), sb = qq >> 3, s = qq & 7;
 #pragma unroll
       for (int j = 0; j < RAWI; ++j) {
         const int c = rkind[j];
         dma16(rsrc[j] + (size_t)sb * 144 + (c == 0 ? 0 : 16 + 32 * (s >> 1) + 16 * (c - 1)),
-              raw0 + (qq % RR) * RSLOT + j * 1024);
+              raw0 + (min(q, nk - 1) % RR) * RSLOT + j * 1024);
       }
     };
-    const int dr = lane >> 1, dh = lane & 1;
     for (int q = 0; q < DR; ++q) issue(q);
     for (int q = 0; q < nk; ++q) {
       issue(q + DR);          // its slot held stage q + DR - RR < q, decoded already
       vm_wait<RAWI * DR>();   // stage q's raw bytes have landed
       if (q >= NBR) poll4(done + 4 * ((q - NBR) % FL), q - NBR);  // B slot: stage q - NBR read by all
-      if (lane < 2 * PR) {
+      for (int li = lane; li < 2 * PR; li += 64) {  // row li / 2, half li % 2 (two passes for BN = 160)
+        const int dr = li >> 1, dh = li & 1;
         const int s = q & 7;
         const uint8_t* raw = lds + RAWOFF + (pw * RR + q % RR) * RSLOT + dr * 48;
         const u32x4 H = *(const u32x4*)raw;
@@ -197,7 +212,7 @@ __global__ __launch_bounds__(512) void qgemm_q4k_x3ref(const QArgs p) {
       xa[part][i] = Xg + part * p.xs + (size_t)min(m0 + c * 32 + i * 16 + fr, M - 1) * p.K + 8 * fc;
   u32x4 A[XR][3][2];
   auto loadA = [&](int q, u32x4 (&dst)[3][2]) __attribute__((always_inline)) {
-    const int qq = min(q, nk - 1);  // past the end: a re-read, so every stage issues 6 loads
+    const int qq = kq0 + min(q, nk - 1);  // past the end: a re-read, so every stage issues 6 loads
 #pragma unroll
     for (int part = 0; part < 3; ++part)
 #pragma unroll
@@ -251,31 +266,58 @@ __global__ __launch_bounds__(512) void qgemm_q4k_x3ref(const QArgs p) {
       for (int r = 0; r < 4; ++r) {
         const int row = m0 + c * 32 + i * 16 + 4 * (lane >> 4) + r;
         if (row >= M) continue;
-        float* cp = Yg + (size_t)row * p.ldy + col;
-        float v = acc[i][j][r];
-        if (p.beta != 0.f) v = fmaf(p.beta, *cp, v);
-        *cp = v;
+        if constexpr (KS == 1) {
+          float* cp = Yg + (size_t)row * p.ldy + col;
+          float v = acc[i][j][r];
+          if (p.beta != 0.f) v = fmaf(p.beta, *cp, v);
+          *cp = v;
+        } else {
+          p.P[(size_t)kz * p.ps + (size_t)row * p.N + col] = acc[i][j][r];  // split K: one group
+        }
       }
   }
 }
 
-template <int BN>
+// Y (beta)= sum of the KS partial sums, in split order, for rows [0, rows).
+__global__ __launch_bounds__(256) void qgemm_splitk_reduce(const float* __restrict__ P, size_t ps, int ks,
+                                                          float* __restrict__ Y, int ldy, int rows, int N, float beta) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (size_t)rows * N) return;
+  float v = P[i];
+  for (int z = 1; z < ks; ++z) v += P[z * ps + i];
+  float* y = Y + (i / N) * (size_t)ldy + i % N;
+  if (beta != 0.f) v = fmaf(beta, *y, v);
+  *y = v;
+}
+
+template <int BN, int KS>
 int launch_q(const QArgs& a, hipStream_t s, const char* who) {
   constexpr int PR = BN / 4, RSLOT = (PR * 48 + 1023) / 1024 * 1024;
   constexpr size_t lds = 3 * (size_t)BN * 64 + 4 * 8 * (size_t)RSLOT + 2 * 4 * 4 * 4;
   static_assert(lds <= 160 * 1024, "LDS budget");
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)qgemm_q4k_x3ref<BN>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)lds);
+    hipError_t e = hipFuncSetAttribute((const void*)qgemm_q4k_x3ref<BN, KS>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return hip_fail(e, who);
     attr_set = true;
   }
-  qgemm_q4k_x3ref<BN><<<(unsigned)a.tile0[a.ngroups], 512, lds, s>>>(a);
+  qgemm_q4k_x3ref<BN, KS><<<(unsigned)a.tile0[a.ngroups] * KS, 512, lds, s>>>(a);
   TM_LAUNCH_CHECK(who);
   return TIERMM_OK;
 }
 
+template <int KS>
+int launch_q_bn(int bn, const QArgs& a, hipStream_t s, const char* who) {
+  switch (bn) {
+    case 160: return launch_q<160, KS>(a, s, who);
+    case 128: return launch_q<128, KS>(a, s, who);
+    case 112: return launch_q<112, KS>(a, s, who);
+    case 96: return launch_q<96, KS>(a, s, who);
+    case 80: return launch_q<80, KS>(a, s, who);
+    default: return launch_q<64, KS>(a, s, who);
+  }
+}
 
 // Tiles of one BN over the groups' row counts.
 long q_tiles(const int* rows, int n, int N, int bn) {
@@ -284,28 +326,78 @@ long q_tiles(const int* rows, int n, int N, int bn) {
   return t;
 }
 
+constexpr int kBns[6] = {160, 128, 112, 96, 80, 64};
+// Per-workgroup time model, us: kRound + kUnit[BN] * BN * (K steps of the split), fitted to
+// 512x{5120,14336,4096,1024,2048,1408}x{5120,14336,4096,2048} and {256,1024,2048}x5120x5120
+// on MI355X (every (BN, KS) of the sweep; the model picks the measured best in each).
+constexpr double kRound = 12.0;
+constexpr double kUnit[6] = {6.25e-3, 6.8e-3, 7.0e-3, 8.0e-3, 8.7e-3, 10.5e-3};
+constexpr size_t kMaxPartials = (size_t)256 << 20;  // bytes of split-K partial sums
+
+struct QPlan {
+  int bn, ks;
+};
+
+bool plan_ok(int bn, int ks, int K, size_t rows_total, int N, bool split) {
+  if (ks > 1 && (!split || (K / 256) % ks || (size_t)ks * rows_total * N * 4 > kMaxPartials)) return false;
+  for (int b : kBns)
+    if (b == bn) return ks == 1 || ks == 2 || ks == 4;
+  return false;
+}
+
+// (BN, KS) for the fused kernel.  TIERMM_QGEMM_TILE="BN,KS" overrides the model when
+// the pair is valid for the shape (tests and tuning).
+QPlan q_plan(const int* rows, int n, int N, int K, int cus, bool split) {
+  size_t rows_total = 0;
+  for (int g = 0; g < n; ++g) rows_total += (size_t)rows[g];
+  if (const char* e = getenv("TIERMM_QGEMM_TILE")) {
+    int bn = 0, ks = 0;
+    if (sscanf(e, "%d,%d", &bn, &ks) == 2 && plan_ok(bn, ks, K, rows_total, N, split)) return {bn, ks};
+  }
+  const int nk = K / QBK;
+  QPlan best{128, 1};
+  double best_t = -1;
+  for (int i = 0; i < 6; ++i)
+    for (int ks = 1; ks <= 4; ks *= 2) {
+      if (!plan_ok(kBns[i], ks, K, rows_total, N, split)) continue;
+      const long wg = q_tiles(rows, n, N, kBns[i]) * ks;
+      double t = (double)((wg + cus - 1) / cus) * (kRound + kUnit[i] * kBns[i] * nk / ks);
+      if (ks > 1) t += (double)rows_total * N * 4 * (ks + 1) / 4e6;  // the reduce, ~4 TB/s
+      if (best_t < 0 || t < best_t) {
+        best_t = t;
+        best = {kBns[i], ks};
+      }
+    }
+  return best;
+}
+
+// CUs of the current device, or 256 (MI355X) where no device is visible (a size
+// query on a host without a GPU); no error is recorded for that case.
+int cus_or_default() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  return device_cus(&cus) == TIERMM_OK && cus > 0 ? cus : 256;
+}
+
 }  // namespace
 
+// Bytes of split-K partial sums the fused GEMM of one M x N x K problem needs.
+size_t qgemm_q4k_partials_bytes(int M, int N, int K) {
+  const QPlan pl = q_plan(&M, 1, N, K, cus_or_default(), true);
+  return pl.ks > 1 ? (size_t)pl.ks * M * N * sizeof(float) : 0;
+}
+
 // Fused q4_K x3-ref GEMM over n groups (rows[g] rows of x from row0[g], weight W[g]);
-// the x planes hold every group's rows (plane stride xs).  BN is the one with the
-// shortest critical path: rounds of workgroups over the CUs times the work of a
-// tile (proportional to BN), larger BN on ties.
+// the x planes hold every group's rows (plane stride xs).  A single group may split K,
+// with `partials` (qgemm_q4k_partials_bytes) holding the partial sums.
 int qgemm_q4k_fused_groups(const void* const* W, const int* row0, const int* rows, int n, size_t rb,
                            const uint16_t* xparts, size_t xs, float* Y, int ldy, int N, int K, float beta, int cus,
-                           hipStream_t s, const char* who) {
-  const int cand[5] = {128, 112, 96, 80, 64};
-  int best = 128;
-  long best_t = -1;
-  for (int c : cand) {
-    const long t = (q_tiles(rows, n, N, c) + cus - 1) / cus * c;
-    if (best_t < 0 || t < best_t) {
-      best_t = t;
-      best = c;
-    }
-  }
+                           hipStream_t s, const char* who, float* partials) {
+  const QPlan pl = q_plan(rows, n, N, K, cus, n == 1 && partials != nullptr);
   for (int g0 = 0; g0 < n; g0 += QG) {
     QArgs a{};
     a.X = xparts; a.xs = xs; a.Y = Y; a.rb = rb; a.ldy = ldy; a.N = N; a.K = K; a.beta = beta;
+    a.P = partials; a.ps = n == 1 ? (size_t)rows[0] * N : 0;
     a.ngroups = 0;
     a.tile0[0] = 0;
     for (int g = g0; g < n && g < g0 + QG; ++g) {
@@ -314,26 +406,31 @@ int qgemm_q4k_fused_groups(const void* const* W, const int* row0, const int* row
       a.row0[j] = row0[g];
       a.rows[j] = rows[g];
       a.W[j] = (const uint8_t*)W[g];
-      a.tile0[j + 1] = a.tile0[j] + (int)q_tiles(&rows[g], 1, N, best);
+      a.tile0[j + 1] = a.tile0[j] + (int)q_tiles(&rows[g], 1, N, pl.bn);
     }
     if (a.ngroups == 0) continue;
     int st;
-    switch (best) {
-      case 128: st = launch_q<128>(a, s, who); break;
-      case 112: st = launch_q<112>(a, s, who); break;
-      case 96: st = launch_q<96>(a, s, who); break;
-      case 80: st = launch_q<80>(a, s, who); break;
-      default: st = launch_q<64>(a, s, who); break;
+    switch (pl.ks) {
+      case 4: st = launch_q_bn<4>(pl.bn, a, s, who); break;
+      case 2: st = launch_q_bn<2>(pl.bn, a, s, who); break;
+      default: st = launch_q_bn<1>(pl.bn, a, s, who); break;
     }
     if (st) return st;
+    if (pl.ks > 1) {  // n == 1: rows row0[0].. of Y
+      const size_t cnt = (size_t)rows[0] * N;
+      qgemm_splitk_reduce<<<(unsigned)((cnt + 255) / 256), 256, 0, s>>>(partials, a.ps, pl.ks,
+                                                                       Y + (size_t)row0[0] * ldy, ldy, rows[0], N,
+                                                                       beta);
+      TM_LAUNCH_CHECK(who);
+    }
   }
   return TIERMM_OK;
 }
 
 int qgemm_q4k_fused(const void* W, size_t rb, const uint16_t* xparts, size_t xs, float* Y, int ldy, int M, int N, int K,
-                    float beta, int cus, hipStream_t s, const char* who) {
+                    float beta, int cus, hipStream_t s, const char* who, float* partials) {
   const int row0 = 0;
-  return qgemm_q4k_fused_groups(&W, &row0, &M, 1, rb, xparts, xs, Y, ldy, N, K, beta, cus, s, who);
+  return qgemm_q4k_fused_groups(&W, &row0, &M, 1, rb, xparts, xs, Y, ldy, N, K, beta, cus, s, who, partials);
 }
 
 }  // namespace tiermm

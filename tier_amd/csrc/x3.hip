@@ -29,10 +29,11 @@ int dequant_f16_rows(const void* W, int qtype, size_t rb, int cols, size_t nrows
 int dequant_f16_group(const void* const* W, uint16_t* const* out, int n, int qtype, size_t rb, int cols,
                       size_t nrows, hipStream_t s);
 int qgemm_q4k_fused(const void* W, size_t rb, const uint16_t* xparts, size_t xs, float* Y, int ldy, int M, int N, int K,
-                    float beta, int cus, hipStream_t s, const char* who);
+                    float beta, int cus, hipStream_t s, const char* who, float* partials);
 int qgemm_q4k_fused_groups(const void* const* W, const int* row0, const int* rows, int n, size_t rb,
                            const uint16_t* xparts, size_t xs, float* Y, int ldy, int N, int K, float beta, int cus,
-                           hipStream_t s, const char* who);
+                           hipStream_t s, const char* who, float* partials);
+size_t qgemm_q4k_partials_bytes(int M, int N, int K);
 int device_cus(int* cus);
 
 namespace {
@@ -914,7 +915,8 @@ size_t tiermm_qgemm_ws_bytes(int qtype, int M, int N, int K, int mode) {
     return al256((size_t)N * K * 4) + 2 * al256((size_t)N * K * 2) + al256((size_t)N * 4) +
            2 * al256((size_t)M * K * 2) + al256((size_t)M * 4);
   const size_t parts = (size_t)3 * M * K * sizeof(uint16_t);  // x split in three fp16 planes
-  if (qtype == TIERMM_Q4_K && big_tiles(M, N) < 192) return parts;  // W decoded inside the GEMM
+  if (qtype == TIERMM_Q4_K && big_tiles(M, N) < 192)  // W decoded inside the GEMM; split-K partial sums
+    return al256(parts) + qgemm_q4k_partials_bytes(M, N, K);
   return (size_t)N * K * sizeof(uint16_t) + parts;                   // W16 staged in the workspace
 }
 
@@ -960,12 +962,13 @@ int tiermm_qgemm(const void* W, int qtype, size_t rb, const float* X, float* Y, 
   }
   if (qtype == TIERMM_Q4_K && big_tiles(M, N) < 192) {  // small M: decode W inside the GEMM
     uint16_t* parts = (uint16_t*)w;
+    float* partials = (float*)((uint8_t*)w + al256(3 * mk * sizeof(uint16_t)));
     st = split3_launch(X, parts, mk, mk, TIERMM_HML, s);
     if (st) return st;
     int cus = 0;
     st = device_cus(&cus);
     if (st) return st;
-    return qgemm_q4k_fused(W, rb, parts, mk, Y, ldy, M, N, K, beta, cus, s, who);
+    return qgemm_q4k_fused(W, rb, parts, mk, Y, ldy, M, N, K, beta, cus, s, who, partials);
   }
   uint16_t* w16 = (uint16_t*)w;
   uint16_t* parts = w16 + (size_t)N * K;
@@ -1100,7 +1103,7 @@ int tiermm_qgemm_grouped(const void* const* W_e, const int* qtype_e, const size_
   }
   if (!gw.empty()) {
     st = qgemm_q4k_fused_groups(gw.data(), g0.data(), gr.data(), (int)gw.size(), grb, parts, pk, Y_sorted, N, N, K,
-                                0.f, cus, s, who);
+                                0.f, cus, s, who, nullptr);
     if (st) return st;
   }
   // other types: fp16 W staged per expert, then the x3-ref GEMM on the expert's rows
