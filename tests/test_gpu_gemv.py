@@ -142,14 +142,15 @@ def test_gemv_q4k_tall_ragged(gpu, N, K):
     assert oracle.rel_fro(y, oracle.gemv_f64(blocks, t, x, N, K)) <= TOL
 
 
+@pytest.mark.parametrize("t", [tier_amd.Q4_K, tier_amd.Q5_K])
 @pytest.mark.parametrize("N,K", [(10256, 2048), (13824, 5120), (16390, 2048), (20000, 768), (28700, 1024),
                                  (40000, 512), (14000, 8192)])
-def test_gemv_q4k_tall_tiles_per_workgroup(gpu, N, K):
-    """The tall q4_K kernel at each count of row tiles per workgroup it is built for
-    (3, 4, 5, 6 and 8; 40000 rows need more workgroups than CUs), with workgroups that
-    hold fewer tiles than the others and partial last row tiles (16390, 28700)."""
-    t = tier_amd.Q4_K
-    rng = np.random.default_rng(7 * N + K)
+def test_gemv_tall_tiles_per_workgroup(gpu, t, N, K):
+    """The tall whole-tile kernel (q4_K, q5_K) at each count of row tiles per workgroup it
+    is built for (3, 4, 5, 6 and 8; 40000 rows need more workgroups than CUs), with
+    workgroups that hold fewer tiles than the others and partial last row tiles (16390,
+    28700)."""
+    rng = np.random.default_rng(7 * N + K + t)
     blocks = oracle.random_blocks(rng, t, N * (K // 256)).reshape(N, -1)
     x = rng.standard_normal(K).astype(np.float32)
     y = _gemv(blocks, t, x, N, K)

@@ -95,18 +95,24 @@ __device__ __forceinline__ void load_group(const uint8_t* base0, size_t rb, cons
 
 constexpr int xq_bytes(int kmax) { return (kmax / 256) * (XQ_SB + META_SB) + ZERO_BYTES; }
 
+// This lane's A operands of one super-block column: rows a0p / a1p for MFMA
+// parities 0 / 1 (see q4k_superblock).
+__device__ __forceinline__ void load_a(const uint8_t* a0p, const uint8_t* a1p, i32x4 (&A)[4]) {
+  A[0] = *(const i32x4*)(a0p);
+  A[1] = *(const i32x4*)(a1p + XQ_T);
+  A[2] = *(const i32x4*)(a0p + 2 * XQ_T);
+  A[3] = *(const i32x4*)(a1p + 3 * XQ_T);
+}
+
 // One super-block of a 16-row tile (gemv_q's per-element sum, tier.cpp:299-306,
 // regrouped by sub-block): hp = the header of row n's super-block in the stage
-// (qs follows at +16), a0p / a1p = this lane's A-operand rows for MFMA parities
-// 0 / 1, mt = (2^-e_g, 2^-e_4+g, S_g, S_4+g) of the super-block's x.  Returns
+// (qs follows at +16), A = this lane's A operands of the super-block's x digits,
+// mt = (2^-e_g, 2^-e_4+g, S_g, S_4+g) of the super-block's x.  Returns
 // acc + d * sum_s sc_s * f_s * D_s - dmin * sum_s m_s * S_s over sub-blocks g, 4+g.
-__device__ __forceinline__ float q4k_superblock(const uint8_t* hp, int g, const uint8_t* a0p, const uint8_t* a1p,
-                                                const float* mtp, float acc) {
+__device__ __forceinline__ float q4k_sb(const uint8_t* hp, int g, const i32x4 (&A)[4], const float4 mt, float acc) {
   const u32x4 H = *(const u32x4*)hp;
   const u32x4 cA = *(const u32x4*)(hp + 16 + 16 * g);
   const u32x4 cB = *(const u32x4*)(hp + 80 + 16 * g);
-  const i32x4 A0 = *(const i32x4*)(a0p), A1 = *(const i32x4*)(a1p + XQ_T);
-  const i32x4 A2 = *(const i32x4*)(a0p + 2 * XQ_T), A3 = *(const i32x4*)(a1p + 3 * XQ_T);
   i32x4 B0, B1, B2, B3;
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
@@ -116,14 +122,13 @@ __device__ __forceinline__ float q4k_superblock(const uint8_t* hp, int g, const 
     B3[w] = (int)((cB[w] >> 4) & 0x0f0f0f0fu);
   }
   const i32x4 z = {0, 0, 0, 0};
-  i32x4 Ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, z, 0, 0, 0);
-  Ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, Ca, 0, 0, 0);
-  i32x4 Cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(A2, B2, z, 0, 0, 0);
-  Cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(A3, B3, Cb, 0, 0, 0);
+  i32x4 Ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], B0, z, 0, 0, 0);
+  Ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[1], B1, Ca, 0, 0, 0);
+  i32x4 Cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[2], B2, z, 0, 0, 0);
+  Cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[3], B3, Cb, 0, 0, 0);
   // |C| <= 32*15*128: both halves below 2^24, so the two conversions are exact
   const float Da = fmaf((float)(Ca[3] * 256 + Ca[2]), 65536.f, (float)(Ca[1] * 256 + Ca[0]));
   const float Db = fmaf((float)(Cb[3] * 256 + Cb[2]), 65536.f, (float)(Cb[1] * 256 + Cb[0]));
-  const float4 mt = *(const float4*)mtp;
   const int sh = 8 * g;  // scale byte of sub-blocks g and 4+g (quant.h:47-48)
   const uint32_t hy = H[1], hz = H[2], hw = H[3];
   const int sca = (hy >> sh) & 63, mna = (hz >> sh) & 63;
@@ -135,6 +140,14 @@ __device__ __forceinline__ float q4k_superblock(const uint8_t* hp, int g, const 
   acc = fmaf(d, u, acc);
   return fmaf(-dmin, m, acc);
 }
+// The same with the A operands and metadata read from LDS: a0p / a1p = this
+// lane's A-operand rows for MFMA parities 0 / 1, mtp = the metadata.
+__device__ __forceinline__ float q4k_superblock(const uint8_t* hp, int g, const uint8_t* a0p, const uint8_t* a1p,
+                                                const float* mtp, float acc) {
+  i32x4 A[4];
+  load_a(a0p, a1p, A);
+  return q4k_sb(hp, g, A, *(const float4*)mtp, acc);
+}
 
 // Q5_K super-block (176 bytes: d, dmin, scales as Q4_K, qh[32], qs[128]; quant.h:49,
 // 85-86): the Q4_K arithmetic with the fifth bit of each weight from qh.  Element
@@ -142,14 +155,11 @@ __device__ __forceinline__ float q4k_superblock(const uint8_t* hp, int g, const 
 // lane group g's chunks g and g+4 cover l = 16(g&1) + [0,16), so its 16 qh bytes
 // serve all four MFMAs, with bits s0, s0+1, s0+4, s0+5 for s0 = 2(g>>1).
 // Weights reach 31: the digit combination rounds once (relative 2^-24).
-__device__ __forceinline__ float q5k_superblock(const uint8_t* hp, int g, const uint8_t* a0p, const uint8_t* a1p,
-                                                const float* mtp, float acc) {
+__device__ __forceinline__ float q5k_sb(const uint8_t* hp, int g, const i32x4 (&A)[4], const float4 mt, float acc) {
   const u32x4 H = *(const u32x4*)hp;
   const u32x4 Qh = *(const u32x4*)(hp + 16 + 16 * (g & 1));
   const u32x4 cA = *(const u32x4*)(hp + 48 + 16 * g);
   const u32x4 cB = *(const u32x4*)(hp + 112 + 16 * g);
-  const i32x4 A0 = *(const i32x4*)(a0p), A1 = *(const i32x4*)(a1p + XQ_T);
-  const i32x4 A2 = *(const i32x4*)(a0p + 2 * XQ_T), A3 = *(const i32x4*)(a1p + 3 * XQ_T);
   const int s0 = 2 * (g >> 1);
   i32x4 B0, B1, B2, B3;
 #pragma unroll
@@ -161,14 +171,13 @@ __device__ __forceinline__ float q5k_superblock(const uint8_t* hp, int g, const 
     B3[w] = (int)(((cB[w] >> 4) & 0x0f0f0f0fu) | ((qs >> 1) & 0x10101010u));
   }
   const i32x4 z = {0, 0, 0, 0};
-  i32x4 Ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, z, 0, 0, 0);
-  Ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, Ca, 0, 0, 0);
-  i32x4 Cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(A2, B2, z, 0, 0, 0);
-  Cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(A3, B3, Cb, 0, 0, 0);
+  i32x4 Ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], B0, z, 0, 0, 0);
+  Ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[1], B1, Ca, 0, 0, 0);
+  i32x4 Cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[2], B2, z, 0, 0, 0);
+  Cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[3], B3, Cb, 0, 0, 0);
   // |C| <= 32*31*128: the halves stay exact in int32
   const float Da = fmaf((float)(Ca[3] * 256 + Ca[2]), 65536.f, (float)(Ca[1] * 256 + Ca[0]));
   const float Db = fmaf((float)(Cb[3] * 256 + Cb[2]), 65536.f, (float)(Cb[1] * 256 + Cb[0]));
-  const float4 mt = *(const float4*)mtp;
   const int sh = 8 * g;
   const uint32_t hy = H[1], hz = H[2], hw = H[3];
   const int sca = (hy >> sh) & 63, mna = (hz >> sh) & 63;
@@ -180,6 +189,12 @@ __device__ __forceinline__ float q5k_superblock(const uint8_t* hp, int g, const 
   acc = fmaf(d, u, acc);
   return fmaf(-dmin, m, acc);
 }
+__device__ __forceinline__ float q5k_superblock(const uint8_t* hp, int g, const uint8_t* a0p, const uint8_t* a1p,
+                                                const float* mtp, float acc) {
+  i32x4 A[4];
+  load_a(a0p, a1p, A);
+  return q5k_sb(hp, g, A, *(const float4*)mtp, acc);
+}
 
 // Q8_0 in groups of eight blocks (272 bytes = 256 weights, 16-byte multiple),
 // the "super-block" of the MFMA GEMV (quant.h:68).  Sub-block s is block s: its
@@ -187,8 +202,7 @@ __device__ __forceinline__ float q5k_superblock(const uint8_t* hp, int g, const 
 // supplies weights 16(g&1) + [0,16) of block 4(t>>1) + 2(g>>1) + (t&1), whose
 // bytes sit 2 (t even) or 0 (t odd) past a dword boundary; Ca ends with block
 // g's digit dots, Cb with block 4+g's.
-__device__ __forceinline__ float q8_group(const uint8_t* hp, int g, const uint8_t* a0p, const uint8_t* a1p,
-                                          const float* mtp, float acc) {
+__device__ __forceinline__ float q8_sb(const uint8_t* hp, int g, const i32x4 (&A)[4], const float4 mt, float acc) {
   i32x4 B[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
@@ -205,24 +219,27 @@ __device__ __forceinline__ float q8_group(const uint8_t* hp, int g, const uint8_
       for (int w = 0; w < 4; ++w) B[t][w] = (int)__builtin_amdgcn_alignbyte(v[w + 1], v[w], 2);
     }
   }
-  const i32x4 A0 = *(const i32x4*)(a0p), A1 = *(const i32x4*)(a1p + XQ_T);
-  const i32x4 A2 = *(const i32x4*)(a0p + 2 * XQ_T), A3 = *(const i32x4*)(a1p + 3 * XQ_T);
   const i32x4 z = {0, 0, 0, 0};
-  i32x4 Ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B[0], z, 0, 0, 0);
-  Ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B[1], Ca, 0, 0, 0);
-  i32x4 Cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(A2, B[2], z, 0, 0, 0);
-  Cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(A3, B[3], Cb, 0, 0, 0);
+  i32x4 Ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], B[0], z, 0, 0, 0);
+  Ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[1], B[1], Ca, 0, 0, 0);
+  i32x4 Cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[2], B[2], z, 0, 0, 0);
+  Cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[3], B[3], Cb, 0, 0, 0);
   // |C| <= 32*127*128 < 2^19: the int32 halves are exact, their conversion rounds once
   const float Da = fmaf((float)(Ca[3] * 256 + Ca[2]), 65536.f, (float)(Ca[1] * 256 + Ca[0]));
   const float Db = fmaf((float)(Cb[3] * 256 + Cb[2]), 65536.f, (float)(Cb[1] * 256 + Cb[0]));
-  const float4 mt = *(const float4*)mtp;
   const float da = h2f(*(const uint16_t*)(hp + 34 * g)), db = h2f(*(const uint16_t*)(hp + 34 * (4 + g)));
   acc = fmaf(da * mt.x, Da, acc);
   return fmaf(db * mt.y, Db, acc);
 }
+__device__ __forceinline__ float q8_group(const uint8_t* hp, int g, const uint8_t* a0p, const uint8_t* a1p,
+                                          const float* mtp, float acc) {
+  i32x4 A[4];
+  load_a(a0p, a1p, A);
+  return q8_sb(hp, g, A, *(const float4*)mtp, acc);
+}
 
 // Per-format pieces of the MFMA GEMV: bytes per 256 weights and the 16-row
-// super-block step.
+// super-block step (A operands from LDS, or already in registers).
 template <int QT>
 struct MfmaFmt;
 template <>
@@ -232,6 +249,9 @@ struct MfmaFmt<QT_Q4_K> {
                                float acc) {
     return q4k_superblock(hp, g, a0p, a1p, mtp, acc);
   }
+  __device__ static float step_reg(const uint8_t* hp, int g, const i32x4 (&A)[4], const float4 mt, float acc) {
+    return q4k_sb(hp, g, A, mt, acc);
+  }
 };
 template <>
 struct MfmaFmt<QT_Q5_K> {
@@ -240,6 +260,9 @@ struct MfmaFmt<QT_Q5_K> {
                                float acc) {
     return q5k_superblock(hp, g, a0p, a1p, mtp, acc);
   }
+  __device__ static float step_reg(const uint8_t* hp, int g, const i32x4 (&A)[4], const float4 mt, float acc) {
+    return q5k_sb(hp, g, A, mt, acc);
+  }
 };
 template <>
 struct MfmaFmt<QT_Q8_0> {
@@ -247,6 +270,9 @@ struct MfmaFmt<QT_Q8_0> {
   __device__ static float step(const uint8_t* hp, int g, const uint8_t* a0p, const uint8_t* a1p, const float* mtp,
                                float acc) {
     return q8_group(hp, g, a0p, a1p, mtp, acc);
+  }
+  __device__ static float step_reg(const uint8_t* hp, int g, const i32x4 (&A)[4], const float4 mt, float acc) {
+    return q8_sb(hp, g, A, mt, acc);
   }
 };
 

@@ -338,6 +338,7 @@ int launch_dense(const void* W, const float* x, float* y, int N, int K, hipStrea
 
 int qgemv_q4k(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s);
 int qgemv_q4k_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s);
+int qgemv_q5k_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s);
 bool qgemv_mfma_fits(const void* W, int qtype, size_t rb, int K);
 bool qgemv_q6k_fits(const void* W, size_t rb, int N, int K);
 int qgemv_q6k(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s);
@@ -357,7 +358,8 @@ int qgemv_dispatch(const void* W, int qtype, size_t rb, const float* x, float* y
       if (qgemv_mfma_fits(W, qtype, rb, K)) return qgemv_mfma(W, qtype, rb, x, y, N, K, s);
       if (staged_fits(W, rb, K)) return launch_staged<QT_Q8_0>(W, rb, x, y, N, K, s);
       return launch_generic<QT_Q8_0>(W, rb, x, y, N, K, s);
-    case QT_Q5_K:
+    case QT_Q5_K:  // tall matrices on the whole-tile kernel, the rest on the per-wave one
+      if (qgemv_mfma_fits(W, qtype, rb, K) && K <= 8192 && (N + 15) / 16 >= 640) return qgemv_q5k_ws(W, rb, x, y, N, K, s);
       if (qgemv_mfma_fits(W, qtype, rb, K)) return qgemv_mfma(W, qtype, rb, x, y, N, K, s);
       return launch_generic<QT_Q5_K>(W, rb, x, y, N, K, s);
     case QT_Q6_K:

@@ -1,5 +1,5 @@
-// qgemv_q4k_ws.hip -- Q4_K decode GEMV for tall matrices: a workgroup streams
-// one 16-row tile at a time through producer waves.
+// qgemv_q4k_ws.hip -- Q4_K (and Q5_K) decode GEMV for tall matrices: a workgroup
+// streams one 16-row tile at a time through producer waves.
 //
 // Same arithmetic and x digit layout as qgemv_q4k.hip (gemv_q, tier.cpp:299-306;
 // q_val Q4_K, quant.h:83-84); q4k_mfma.h holds the shared pieces.
@@ -68,10 +68,10 @@ __device__ __forceinline__ void poll_ge(const int* f, int v) {
   asm volatile("" ::: "memory");
 }
 
-template <int NC, int NS, int R>
+template <int QT, int NC, int NS, int R>
 struct WsLayout {
   static constexpr int GS = NC;                                 // super-blocks per stage
-  static constexpr int GRP = GS * SB_BYTES;                     // one row's segment
+  static constexpr int GRP = GS * MfmaFmt<QT>::SBB;             // one row's segment
   static constexpr int SLOT = PROWS * GRP;                      // one producer's part of a stage
   static constexpr int NLD = (SLOT + 1023) / 1024;              // 1 KiB loads per part
   static constexpr int LAST = (SLOT - (NLD - 1) * 1024) / 16;   // lanes of the last load
@@ -80,46 +80,12 @@ struct WsLayout {
   static constexpr size_t LDS = RING + NS * NP * 4 + NS * NCP * 4 + (size_t)R * NC * 16 * 4;
 };
 
-// The q4k_superblock arithmetic with this lane's A operands (x digits of the
-// super-block column) and x metadata already in registers.
-__device__ __forceinline__ float q4k_superblock_reg(const uint8_t* hp, int g, const i32x4 (&A)[4], const float4 mt,
-                                                    float acc) {
-  const u32x4 H = *(const u32x4*)hp;
-  const u32x4 cA = *(const u32x4*)(hp + 16 + 16 * g);
-  const u32x4 cB = *(const u32x4*)(hp + 80 + 16 * g);
-  i32x4 B0, B1, B2, B3;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    B0[w] = (int)(cA[w] & 0x0f0f0f0fu);
-    B1[w] = (int)((cA[w] >> 4) & 0x0f0f0f0fu);
-    B2[w] = (int)(cB[w] & 0x0f0f0f0fu);
-    B3[w] = (int)((cB[w] >> 4) & 0x0f0f0f0fu);
-  }
-  const i32x4 z = {0, 0, 0, 0};
-  i32x4 Ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], B0, z, 0, 0, 0);
-  Ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[1], B1, Ca, 0, 0, 0);
-  i32x4 Cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[2], B2, z, 0, 0, 0);
-  Cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[3], B3, Cb, 0, 0, 0);
-  // |C| <= 32*15*128: both halves below 2^24, so the two conversions are exact
-  const float Da = fmaf((float)(Ca[3] * 256 + Ca[2]), 65536.f, (float)(Ca[1] * 256 + Ca[0]));
-  const float Db = fmaf((float)(Cb[3] * 256 + Cb[2]), 65536.f, (float)(Cb[1] * 256 + Cb[0]));
-  const int sh = 8 * g;  // scale byte of sub-blocks g and 4+g (quant.h:47-48)
-  const uint32_t hy = H[1], hz = H[2], hw = H[3];
-  const int sca = (hy >> sh) & 63, mna = (hz >> sh) & 63;
-  const int scb = ((hw >> sh) & 15) | (((hy >> (sh + 6)) & 3) << 4);
-  const int mnb = ((hw >> (sh + 4)) & 15) | (((hz >> (sh + 6)) & 3) << 4);
-  const float d = h2f(H[0] & 0xffffu), dmin = h2f(H[0] >> 16);
-  const float u = fmaf((float)scb * mt.y, Db, (float)sca * mt.x * Da);
-  const float m = fmaf((float)mnb, mt.w, (float)mna * mt.z);
-  acc = fmaf(d, u, acc);
-  return fmaf(-dmin, m, acc);
-}
-
-template <int R, int NC, int NS, int D, int XP, int XK>
+template <int QT, int R, int NC, int NS, int D, int XP, int XK>
 __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __restrict__ W, size_t rb,
                                                             const float* __restrict__ x, float* __restrict__ y,
                                                             int N, int K) {
-  using L = WsLayout<NC, NS, R>;
+  using L = WsLayout<QT, NC, NS, R>;
+  constexpr int SBB = MfmaFmt<QT>::SBB;
   constexpr int GS = L::GS, GRP = L::GRP, SLOT = L::SLOT, NLD = L::NLD, NCP = L::NCP;
   constexpr int MS = (XK / 256 + GS - 1) / GS;  // super-block columns per consumer
   static_assert(NLD * D <= 63, "vmcnt counts at most 63 loads");
@@ -159,7 +125,7 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
       const int tile = min((int)blockIdx.x + r * (int)gridDim.x, tiles - 1);
       const int rbase = min(tile * 16 + PROWS * p, N - 1), rmax = min(PROWS - 1, N - 1 - rbase);
       // bytes past the row's last super-block re-read the last valid 16 bytes
-      const int lastb = min(GS, nsb - GS * gi) * SB_BYTES - 16;
+      const int lastb = min(GS, nsb - GS * gi) * SBB - 16;
       const uint8_t* b = W + (size_t)rbase * rb + (size_t)gi * GRP;
       const uint32_t dst = ring_lds + (q % NS) * SLOT;
 #pragma unroll
@@ -226,7 +192,7 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
       mt[m] = *(const float4*)(meta + sb * 16 + g * 4);
     }
     // row n of a stage: producer n / 4's slot, row n % 4 of it; column c
-    const uint8_t* rowbase = ring + (n / PROWS) * NS * SLOT + (n % PROWS) * GRP + c * SB_BYTES;
+    const uint8_t* rowbase = ring + (n / PROWS) * NS * SLOT + (n % PROWS) * GRP + c * SBB;
     for (int r = 0; r < R; ++r) {
       float acc = 0.f;
 #pragma unroll
@@ -235,7 +201,7 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
           const int q = r * ngrp + gi, slot = q % NS;
           if (GS * gi + c < nsb) {
             poll_ge<NP>(full + NP * slot, q);
-            acc = q4k_superblock_reg(rowbase + slot * SLOT, g, A[gi], mt[gi], acc);
+            acc = MfmaFmt<QT>::step_reg(rowbase + slot * SLOT, g, A[gi], mt[gi], acc);
           }
           if (lane == 0) lds_rel(&done[slot * NCP + c], q);
         }
@@ -258,33 +224,33 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
   }
 }
 
-template <int R, int NC, int NS, int D, int XP, int XK>
+template <int QT, int R, int NC, int NS, int D, int XP, int XK>
 int launch_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
-  using L = WsLayout<NC, NS, R>;
+  using L = WsLayout<QT, NC, NS, R>;
   static_assert(xq_bytes(XK) + L::LDS <= 160 * 1024, "LDS budget");
   static_assert(XK / 16 <= 64 * NC * XP, "x preparation: one thread per 16 elements");
   const int tiles = (N + 15) / 16;
   const unsigned grid = (unsigned)((tiles + R - 1) / R);
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)qgemv_q4k_ws<R, NC, NS, D, XP, XK>,
+    hipError_t e = hipFuncSetAttribute((const void*)qgemv_q4k_ws<QT, R, NC, NS, D, XP, XK>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)L::LDS);
     if (e != hipSuccess) return hip_fail(e, "tiermm_qgemv: q4_K LDS attribute");
     attr_set = true;
   }
-  qgemv_q4k_ws<R, NC, NS, D, XP, XK><<<grid, 64 * (NC + NP), L::LDS, s>>>((const uint8_t*)W, rb, x, y, N, K);
+  qgemv_q4k_ws<QT, R, NC, NS, D, XP, XK><<<grid, 64 * (NC + NP), L::LDS, s>>>((const uint8_t*)W, rb, x, y, N, K);
   TM_LAUNCH_CHECK("tiermm_qgemv: q4_K launch");
   return TIERMM_OK;
 }
 
-template <int NC, int NS, int D, int XP, int XK>
+template <int QT, int NC, int NS, int D, int XP, int XK>
 int launch_ws_r(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
   const int tiles = (N + 15) / 16, r = (tiles + GTILE - 1) / GTILE;
-  if (r <= 3) return launch_ws<3, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
-  if (r == 4) return launch_ws<4, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
-  if (r == 5) return launch_ws<5, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
-  if (r == 6) return launch_ws<6, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
-  return launch_ws<8, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
+  if (r <= 3) return launch_ws<QT, 3, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
+  if (r == 4) return launch_ws<QT, 4, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
+  if (r == 5) return launch_ws<QT, 5, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
+  if (r == 6) return launch_ws<QT, 6, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
+  return launch_ws<QT, 8, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
 }
 
 }  // namespace
@@ -294,9 +260,20 @@ int launch_ws_r(const void* W, size_t rb, const float* x, float* y, int N, int K
 // ragged one).  Stages of 12 super-blocks up to K = 5120 (x digits of two
 // columns per consumer), of 8 up to 8192 (four columns).
 int qgemv_q4k_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
-  if (K <= 5120) return launch_ws_r<12, 4, 2, 1, 5120>(W, rb, x, y, N, K, s);
-  if (K <= 8192) return launch_ws_r<8, 4, 2, 1, 8192>(W, rb, x, y, N, K, s);
+  if (K <= 5120) return launch_ws_r<QT_Q4_K, 12, 4, 2, 1, 5120>(W, rb, x, y, N, K, s);
+  if (K <= 8192) return launch_ws_r<QT_Q4_K, 8, 4, 2, 1, 8192>(W, rb, x, y, N, K, s);
   return set_error(TIERMM_UNSUPPORTED, "tiermm_qgemv: q4_K K=%d above %d", K, 8192);
+}
+
+// The same kernel on Q5_K (176-byte super-blocks; stages of 10 super-blocks up
+// to K = 5120 keep the ring within the LDS).  Against the per-wave kernel:
+// 13824x5120 10.8 against 12.5 us, 10240x8192 12.0 against 15.4 us.  Q8_0 (272-byte
+// groups) gained nothing this way (a 3-slot ring: 17.5 against 17.1 us at
+// 13824x5120, 36.6 against 22.2 us at 10240x8192) and keeps the per-wave kernel.
+int qgemv_q5k_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
+  if (K <= 5120) return launch_ws_r<QT_Q5_K, 10, 4, 2, 1, 5120>(W, rb, x, y, N, K, s);
+  if (K <= 8192) return launch_ws_r<QT_Q5_K, 8, 4, 2, 1, 8192>(W, rb, x, y, N, K, s);
+  return set_error(TIERMM_UNSUPPORTED, "tiermm_qgemv: q5_K K=%d above %d", K, 8192);
 }
 
 }  // namespace tiermm
