@@ -153,6 +153,31 @@ def test_qgemm_x3ref(gpu, name, t, M, N, K):
     assert oracle.rel_fro(got, ref) <= BAR
 
 
+@pytest.mark.parametrize("t,beta", [(tier_amd.Q4_K, 0.0), (tier_amd.Q5_K, 1.0), (tier_amd.Q6_K, 0.0)])
+def test_qgemm_big_tiles_k_tiled_planes(gpu, t, beta):
+    """Large M (the fp16 staging + big-tile x3-ref path, whose planes are K-tiled): a
+    partial last column tile, beta = 1; an x that is only 4-byte aligned takes the
+    row-major planes instead, and both give the same bits."""
+    M, N, K = 4096, 4000, 512
+    blocks = quantized_weight(t, N, K, seed=40 + t)
+    x = activations(M, K, seed=41)
+    y0 = np.random.default_rng(42).standard_normal((M, N)).astype(np.float32)
+    W = hip.to_device(blocks)
+    X = hip.to_device(x)
+    Xu = hip.DeviceBuffer(x.nbytes + 16).upload(x, offset=4)
+    Y, Yu = hip.to_device(y0), hip.to_device(y0)
+    rb = tier_amd.q_row_bytes(t, K)
+    tier_amd.qgemm(W.ptr, t, rb, X.ptr, Y.ptr, M, N, K, beta=beta)
+    tier_amd.qgemm(W.ptr, t, rb, Xu.ptr + 4, Yu.ptr, M, N, K, beta=beta)
+    hip.synchronize()
+    got = Y.download(np.float32, M * N).reshape(M, N)
+    got_u = Yu.download(np.float32, M * N).reshape(M, N)
+    assert np.array_equal(got.view(np.uint32), got_u.view(np.uint32))
+    w16 = oracle.h2f(oracle.dequant(blocks, t, K, oracle.OUT_F16)).reshape(N, K)
+    ref = x.astype(np.float64) @ w16.astype(np.float64).T + beta * y0.astype(np.float64)
+    assert oracle.rel_fro(got, ref) <= BAR
+
+
 @pytest.mark.parametrize("M,N,K,beta", [(130, 100, 768, 0.0), (1, 50, 256, 0.0), (257, 1000, 2048, 1.0),
                                          (512, 5120, 1024, 0.0)])
 def test_qgemm_q4k_fused_shapes(gpu, M, N, K, beta):

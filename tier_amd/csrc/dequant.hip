@@ -9,14 +9,22 @@
 namespace tiermm {
 namespace {
 
+// trows > 0: fp16 output in the K-tiled layout of a plane of trows rows (ktile_index),
+// written in unit order.
 template <int QT, int OUT>
 __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ W, size_t rb, int cols, size_t r0,
-                                                      size_t n8, void* __restrict__ out) {
+                                                      size_t n8, void* __restrict__ out, size_t trows = 0) {
   const size_t stride = (size_t)gridDim.x * blockDim.x;
   for (size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x; t < n8; t += stride) {
-    const size_t e = t * 8;
-    const size_t row = e / (size_t)cols;
-    const int col = (int)(e - row * (size_t)cols);
+    const size_t e = t * 8;  // output offset: unit t in row-major or K-tiled order
+    size_t row;
+    int col;
+    if (trows) {
+      ktile_unit(t, trows, row, col);
+    } else {
+      row = e / (size_t)cols;
+      col = (int)(e - row * (size_t)cols);
+    }
     float v[8];
     Dec<QT>::run(W + (r0 + row) * rb, col, v);
     if (OUT == TIERMM_OUT_F32) {
@@ -62,14 +70,21 @@ struct DqGroup {
 };
 
 template <int QT>
-__global__ __launch_bounds__(256) void dequant_f16_group_kernel(const DqGroup g, size_t rb, int cols, size_t n8) {
+__global__ __launch_bounds__(256) void dequant_f16_group_kernel(const DqGroup g, size_t rb, int cols, size_t n8,
+                                                                size_t trows) {
   const uint8_t* W = g.W[blockIdx.y];
   uint16_t* out = g.out[blockIdx.y];
   const size_t stride = (size_t)gridDim.x * blockDim.x;
   for (size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x; t < n8; t += stride) {
-    const size_t e = t * 8;
-    const size_t row = e / (size_t)cols;
-    const int col = (int)(e - row * (size_t)cols);
+    const size_t e = t * 8;  // output offset: unit t in row-major or K-tiled order
+    size_t row;
+    int col;
+    if (trows) {
+      ktile_unit(t, trows, row, col);
+    } else {
+      row = e / (size_t)cols;
+      col = (int)(e - row * (size_t)cols);
+    }
     float v[8];
     Dec<QT>::run(W + row * rb, col, v);
     uint32_t p[4];
@@ -110,16 +125,30 @@ int check_qweight(const char* who, const void* W, int qtype, size_t rb, int cols
   return TIERMM_OK;
 }
 
-// Whole rows to fp16 for the quantized GEMM (dq_launch<tier_fp16>, tier.cpp:515).
-int dequant_f16_rows(const void* W, int qtype, size_t rb, int cols, size_t nrows, uint16_t* out, hipStream_t s) {
-  return with_qtype(qtype, [&](auto qt) {
-    return launch_dequant<decltype(qt)::value>(W, rb, cols, 0, nrows, out, TIERMM_OUT_F16, s);
+// Whole rows to fp16 for the quantized GEMM (dq_launch<tier_fp16>, tier.cpp:515),
+// row-major or (tiled, cols a multiple of 32) in the K-tiled layout.
+int dequant_f16_rows(const void* W, int qtype, size_t rb, int cols, size_t nrows, uint16_t* out, hipStream_t s,
+                     bool tiled) {
+  if (!tiled)
+    return with_qtype(qtype, [&](auto qt) {
+      return launch_dequant<decltype(qt)::value>(W, rb, cols, 0, nrows, out, TIERMM_OUT_F16, s);
+    });
+  const size_t n8 = nrows * (size_t)cols / 8;
+  if (n8 == 0) return TIERMM_OK;
+  const size_t want = (n8 + 255) / 256;
+  const unsigned grid = (unsigned)(want < 65536 ? want : 65536);
+  return with_qtype(qtype, [&](auto qt) -> int {
+    dequant_kernel<decltype(qt)::value, TIERMM_OUT_F16><<<grid, 256, 0, s>>>((const uint8_t*)W, rb, cols, 0, n8, out,
+                                                                            nrows);
+    TM_LAUNCH_CHECK("dequant_f16_rows: launch");
+    return TIERMM_OK;
   });
 }
 
-// n (<= 64) weights of one type, each nrows x cols, to fp16 rows at out[i].
+// n (<= 64) weights of one type, each nrows x cols, to fp16 at out[i], row-major or
+// (tiled) in the K-tiled layout.
 int dequant_f16_group(const void* const* W, uint16_t* const* out, int n, int qtype, size_t rb, int cols,
-                      size_t nrows, hipStream_t s) {
+                      size_t nrows, hipStream_t s, bool tiled) {
   if (n <= 0) return TIERMM_OK;
   if (n > DQ_GROUP) return set_error(TIERMM_EINVAL, "dequant_f16_group: %d weights (max %d)", n, DQ_GROUP);
   const size_t n8 = nrows * (size_t)cols / 8;
@@ -132,7 +161,7 @@ int dequant_f16_group(const void* const* W, uint16_t* const* out, int n, int qty
   const size_t want = (n8 + 255) / 256;
   const dim3 grid((unsigned)(want < 2048 ? want : 2048), (unsigned)n);
   return with_qtype(qtype, [&](auto qt) -> int {
-    dequant_f16_group_kernel<decltype(qt)::value><<<grid, 256, 0, s>>>(g, rb, cols, n8);
+    dequant_f16_group_kernel<decltype(qt)::value><<<grid, 256, 0, s>>>(g, rb, cols, n8, tiled ? nrows : 0);
     TM_LAUNCH_CHECK("dequant_f16_group: launch");
     return TIERMM_OK;
   });

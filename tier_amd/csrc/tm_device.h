@@ -434,6 +434,21 @@ __device__ __forceinline__ u32x4 gload16(const void* p) {
   asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p) : "memory");
   return r;
 }
+// K-tiled plane layout of the internal fp16 operands of the big-tile GEMM:
+// element (row, col) of a plane with `rows` rows at ((col / 32) * rows + row) * 32
+// + col % 32, so that the 64 bytes of one K step of 16 consecutive rows are one
+// contiguous kilobyte.
+__device__ __forceinline__ size_t ktile_index(size_t row, int col, size_t rows) {
+  return (((size_t)(col >> 5) * rows + row) << 5) + (size_t)(col & 31);
+}
+// The element (row, col) that starts 8-element unit u of a K-tiled plane of `rows`
+// rows: writers walk the units in order, so each wave stores contiguous kilobytes.
+__device__ __forceinline__ void ktile_unit(size_t u, size_t rows, size_t& row, int& col) {
+  const size_t kt = u / (rows * 4), rem = u - kt * rows * 4;
+  row = rem >> 2;
+  col = (int)(kt * 32 + (rem & 3) * 8);
+}
+
 // 16 bytes per lane from p into LDS at lds_addr + 16*lane (lds_addr wave-uniform, through M0).
 __device__ __forceinline__ void dma16(const void* p, uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(p),

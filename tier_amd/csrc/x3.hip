@@ -25,9 +25,10 @@
 namespace tiermm {
 
 int check_qweight(const char* who, const void* W, int qtype, size_t rb, int cols);
-int dequant_f16_rows(const void* W, int qtype, size_t rb, int cols, size_t nrows, uint16_t* out, hipStream_t s);
+int dequant_f16_rows(const void* W, int qtype, size_t rb, int cols, size_t nrows, uint16_t* out, hipStream_t s,
+                     bool tiled = false);
 int dequant_f16_group(const void* const* W, uint16_t* const* out, int n, int qtype, size_t rb, int cols,
-                      size_t nrows, hipStream_t s);
+                      size_t nrows, hipStream_t s, bool tiled = false);
 int qgemm_q4k_fused(const void* W, size_t rb, const uint16_t* xparts, size_t xs, float* Y, int ldy, int M, int N, int K,
                     float beta, int cus, hipStream_t s, const char* who, float* partials);
 int qgemm_q4k_fused_groups(const void* const* W, const int* row0, const int* rows, int n, size_t rb,
@@ -71,9 +72,12 @@ __global__ __launch_bounds__(256) void split3_kernel(const float* __restrict__ x
 
 // The same split, 8 consecutive elements per thread: two 16-byte loads, one
 // 16-byte store per part (n, stride multiples of 8; x and parts 16-byte aligned).
+// trows > 0: the parts in the K-tiled layout of planes of trows rows of cols
+// elements (ktile_index; cols a multiple of 32), written in unit order.
 template <bool BF>
 __global__ __launch_bounds__(256) void split3_vec8_kernel(const float* __restrict__ x, uint16_t* __restrict__ parts,
-                                                          size_t n8, size_t stride, int order) {
+                                                          size_t n8, size_t stride, int order, size_t trows = 0,
+                                                          int cols = 0) {
   const size_t step = (size_t)gridDim.x * blockDim.x;
   auto to16 = [](float f) __attribute__((always_inline)) { return BF ? f2bf(f) : f2h(f); };
   auto from16 = [](uint16_t u) __attribute__((always_inline)) {
@@ -83,7 +87,14 @@ __global__ __launch_bounds__(256) void split3_vec8_kernel(const float* __restric
   uint16_t* pm = parts + stride;
   uint16_t* pl = parts + (order == TIERMM_HML ? 2 * stride : 0);
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += step) {
-    const float4 a = ((const float4*)x)[2 * i], b = ((const float4*)x)[2 * i + 1];
+    size_t src = 8 * i;  // K-tiled: unit i of the output, gathered from its row
+    if (trows) {
+      size_t row;
+      int col;
+      ktile_unit(i, trows, row, col);
+      src = row * (size_t)cols + col;
+    }
+    const float4 a = *(const float4*)(x + src), b = *(const float4*)(x + src + 4);
     const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
     uint32_t h[4], m[4], l[4];
 #pragma unroll
@@ -99,9 +110,10 @@ __global__ __launch_bounds__(256) void split3_vec8_kernel(const float* __restric
         h[k >> 1] |= (uint32_t)hh << 16; m[k >> 1] |= (uint32_t)mm << 16; l[k >> 1] |= (uint32_t)ll << 16;
       }
     }
-    ((uint4*)ph)[i] = make_uint4(h[0], h[1], h[2], h[3]);
-    ((uint4*)pm)[i] = make_uint4(m[0], m[1], m[2], m[3]);
-    ((uint4*)pl)[i] = make_uint4(l[0], l[1], l[2], l[3]);
+    const size_t o = 8 * i;
+    *(uint4*)(ph + o) = make_uint4(h[0], h[1], h[2], h[3]);
+    *(uint4*)(pm + o) = make_uint4(m[0], m[1], m[2], m[3]);
+    *(uint4*)(pl + o) = make_uint4(l[0], l[1], l[2], l[3]);
   }
 }
 
@@ -251,6 +263,9 @@ struct X3Args {
   const uint16_t* A[3];  // [M][lda]
   const uint16_t* B[2];  // [N][ldb]
   int lda, ldb;
+  // Big-tile kernel only: K-tiled planes (ktile_index) when atile / btile is the
+  // plane's row count, row-major with lda / ldb when 0.
+  int atile, btile;
   float* C;
   int ldc;
   int M, N, K;
@@ -450,6 +465,7 @@ __device__ __forceinline__ void x3_big_tile(const X3Args& p, int t) {
   // also wait for the DMA).
   const uint16_t* gsrc[PER_WAVE];
   uint32_t loff[PER_WAVE];
+  size_t gstep[PER_WAVE];  // halfs between the K steps of a load's rows
   {
     const int drow = lane >> 2, dslot = lane & 3;
 #pragma unroll
@@ -461,12 +477,14 @@ __device__ __forceinline__ void x3_big_tile(const X3Args& p, int t) {
         const int q = t / A_INST;
         ch = t % A_INST;
         src = q == 0 ? p.A[0] : q == 1 ? p.A[1] : p.A[2];
-        ld = p.lda; lim = p.M; r0 = m0; base = q * A_PART;
+        ld = p.atile ? 32 : p.lda; lim = p.M; r0 = m0; base = q * A_PART;
+        gstep[u] = p.atile ? (size_t)p.atile * 32 : BK;
       } else {
         const int q = (t - NA * A_INST) / B_INST;
         ch = (t - NA * A_INST) % B_INST;
         src = q == 0 ? p.B[0] : p.B[1];
-        ld = p.ldb; lim = p.N; r0 = n0; base = NA * A_PART + q * B_PART;
+        ld = p.btile ? 32 : p.ldb; lim = p.N; r0 = n0; base = NA * A_PART + q * B_PART;
+        gstep[u] = p.btile ? (size_t)p.btile * 32 : BK;
       }
       const int row = ch * 16 + drow;
       const int kc = dslot ^ ((row >> 2) & 3);
@@ -475,10 +493,9 @@ __device__ __forceinline__ void x3_big_tile(const X3Args& p, int t) {
     }
   }
   auto issue = [&](int kt, int buf) __attribute__((always_inline)) {
-    const int k0 = kt * BK;
 #pragma unroll
     for (int u = 0; u < PER_WAVE; ++u)
-      if (wave + 8 * u < NINST) dma16(gsrc[u] + k0, lds0 + buf * STAGE + loff[u]);
+      if (wave + 8 * u < NINST) dma16(gsrc[u] + (size_t)kt * gstep[u], lds0 + buf * STAGE + loff[u]);
   };
 
   float16v acc[WM][WN];
@@ -594,7 +611,7 @@ __global__ __launch_bounds__(512) void gemm_x3_big_grouped(const X3Args p, const
   while (grp + 1 < g.n && b >= g.tile0[grp + 1]) ++grp;
   X3Args q = p;
   for (int k = 0; k < 3; ++k)
-    if (q.A[k]) q.A[k] += (size_t)g.row0[grp] * p.lda;
+    if (q.A[k]) q.A[k] += (size_t)g.row0[grp] * (p.atile ? 32 : p.lda);
   q.B[0] = g.B[grp];
   q.M = g.rows[grp];
   q.C = p.C + (size_t)g.row0[grp] * p.ldc;
@@ -743,8 +760,20 @@ void x3s_split_launch(const float* src, uint16_t* hi, uint16_t* lo, int32_t* exp
     x3s_split_kernel<<<rows, 256, 0, s>>>(src, hi, lo, exps, cols);
 }
 
-int split3_launch(const float* x, uint16_t* parts, size_t n, size_t stride, int order, hipStream_t s, bool bf16 = false) {
+// trows > 0: fp16 parts in the K-tiled layout of planes of trows rows of cols
+// elements (needs the vectorised kernel's alignment and cols % 32 == 0).
+int split3_launch(const float* x, uint16_t* parts, size_t n, size_t stride, int order, hipStream_t s, bool bf16 = false,
+                  size_t trows = 0, int cols = 0) {
   if (n == 0) return TIERMM_OK;
+  if (trows) {
+    if (n % 8 || stride % 8 || ((uintptr_t)x & 15) || ((uintptr_t)parts & 15) || cols % 32 || bf16)
+      return set_error(TIERMM_EINVAL, "split3: K-tiled parts need 16-byte aligned rows of a multiple of 32");
+    const size_t n8 = n / 8, want = (n8 + 255) / 256;
+    const unsigned grid = (unsigned)(want < 8192 ? want : 8192);
+    split3_vec8_kernel<false><<<grid, 256, 0, s>>>(x, parts, n8, stride, order, trows, cols);
+    TM_LAUNCH_CHECK("split3: launch");
+    return TIERMM_OK;
+  }
   if (n % 8 == 0 && stride % 8 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)parts & 15) == 0) {
     const size_t n8 = n / 8, want = (n8 + 255) / 256;
     const unsigned grid = (unsigned)(want < 8192 ? want : 8192);
@@ -972,11 +1001,20 @@ int tiermm_qgemm(const void* W, int qtype, size_t rb, const float* X, float* Y, 
   }
   uint16_t* w16 = (uint16_t*)w;
   uint16_t* parts = w16 + (size_t)N * K;
-  st = dequant_f16_rows(W, qtype, rb, K, (size_t)N, w16, s);
+  // The big-tile kernel reads the planes K-tiled (one contiguous kilobyte per load,
+  // ~4 % faster); the small-tile kernel reads them row-major.
+  const bool tiled = big_tiles(M, N) >= 192 && K % 32 == 0 && ((uintptr_t)X & 15) == 0;
+  st = dequant_f16_rows(W, qtype, rb, K, (size_t)N, w16, s, tiled);
   if (st) return st;
-  st = split3_launch(X, parts, mk, mk, TIERMM_HML, s);
+  st = split3_launch(X, parts, mk, mk, TIERMM_HML, s, false, tiled ? (size_t)M : 0, K);
   if (st) return st;
-  return x3ref_nt(parts, mk, w16, K, Y, ldy, M, N, K, beta, s, who);
+  if (!tiled) return x3ref_nt(parts, mk, w16, K, Y, ldy, M, N, K, beta, s, who);
+  X3Args a{};
+  a.A[0] = parts; a.A[1] = parts + mk; a.A[2] = parts + 2 * mk;
+  a.B[0] = w16;
+  a.lda = K; a.ldb = K; a.atile = M; a.btile = N;
+  a.C = Y; a.ldc = ldy; a.M = M; a.N = N; a.K = K; a.beta = beta;
+  return launch_x3_big<X3_REF>(a, s, who);
 }
 
 size_t tiermm_qgemm_grouped_ws_bytes(const int* qtype_e, const int* expert_offsets, int n_experts, int N, int K,
@@ -1041,14 +1079,20 @@ int tiermm_qgemm_grouped(const void* const* W_e, const int* qtype_e, const size_
   const size_t P = (size_t)expert_offsets[n_experts], pk = P * K;
   uint16_t* parts = (uint16_t*)w;
   uint16_t* w16 = (uint16_t*)((uint8_t*)w + al256(3 * pk * sizeof(uint16_t)));
-  st = split3_launch(X_sorted, parts, pk, pk, TIERMM_HML, s);
-  if (st) return st;
   const int chunk = big_group_chunk(expert_offsets, n_experts, N, K);
+  // the grouped big-tile launch reads K-tiled planes; the other paths row-major ones
+  const bool tiled = chunk && K % 32 == 0 && ((uintptr_t)X_sorted & 15) == 0;
+  st = split3_launch(X_sorted, parts, pk, pk, TIERMM_HML, s, false, tiled ? P : 0, K);
+  if (st) return st;
   if (chunk) {  // fp16 weights of up to `chunk` experts, then one grouped launch over their tiles
     const size_t per = al256((size_t)N * K * sizeof(uint16_t));
     X3Args a{};
     a.A[0] = parts; a.A[1] = parts + pk; a.A[2] = parts + 2 * pk;
     a.lda = K; a.ldb = K; a.C = Y_sorted; a.ldc = N; a.N = N; a.K = K;
+    if (tiled) {
+      a.atile = (int)P;
+      a.btile = N;
+    }
     std::vector<int> ex;
     for (int e = 0; e < n_experts; ++e)
       if (expert_offsets[e + 1] > expert_offsets[e]) ex.push_back(e);
@@ -1076,7 +1120,7 @@ int tiermm_qgemm_grouped(const void* const* W_e, const int* qtype_e, const size_
             src.push_back(W_e[ex[c0 + j]]);
             dst.push_back((uint16_t*)g.B[j]);
           }
-        st = dequant_f16_group(src.data(), dst.data(), (int)src.size(), qt, rb_e[ex[c0 + i]], K, (size_t)N, s);
+        st = dequant_f16_group(src.data(), dst.data(), (int)src.size(), qt, rb_e[ex[c0 + i]], K, (size_t)N, s, tiled);
         if (st) return st;
       }
       st = big_tn(N) == 352 ? launch_x3_big_grouped<X3_REF, 352>(a, g, s, who)
