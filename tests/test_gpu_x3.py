@@ -153,12 +153,13 @@ def test_qgemm_x3ref(gpu, name, t, M, N, K):
     assert oracle.rel_fro(got, ref) <= BAR
 
 
-@pytest.mark.parametrize("t,beta", [(tier_amd.Q4_K, 0.0), (tier_amd.Q5_K, 1.0), (tier_amd.Q6_K, 0.0)])
-def test_qgemm_big_tiles_k_tiled_planes(gpu, t, beta):
+@pytest.mark.parametrize("t,beta,M", [(tier_amd.Q4_K, 0.0, 4096), (tier_amd.Q5_K, 1.0, 4000), (tier_amd.Q6_K, 0.0, 4096)])
+def test_qgemm_big_tiles_k_tiled_planes(gpu, t, beta, M):
     """Large M (the fp16 staging + big-tile x3-ref path, whose planes are K-tiled): a
     partial last column tile, beta = 1; an x that is only 4-byte aligned takes the
-    row-major planes instead, and both give the same bits."""
-    M, N, K = 4096, 4000, 512
+    row-major planes instead, and both give the same bits (M = 4000: a partial last row
+    tile too)."""
+    N, K = 4000, 512
     blocks = quantized_weight(t, N, K, seed=40 + t)
     x = activations(M, K, seed=41)
     y0 = np.random.default_rng(42).standard_normal((M, N)).astype(np.float32)
@@ -220,6 +221,25 @@ def test_qgemm_q4k_tile_plans(gpu, monkeypatch, bn, ks, M, N, K, beta):
     ref = x.astype(np.float64) @ w16.astype(np.float64).T + beta * y0.astype(np.float64)
     assert np.all(np.isfinite(got))
     assert oracle.rel_fro(got, ref) <= BAR
+
+
+def test_qgemm_split_k_padded_rows(gpu, monkeypatch):
+    """Split-K into an output with padded rows (ldy > N) and beta = 1: the reduce keeps
+    the padding untouched and accumulates into the rows."""
+    monkeypatch.setenv("TIERMM_QGEMM_TILE", "160,4")
+    t, M, N, K, ldy = tier_amd.Q4_K, 200, 336, 1024, 352
+    rng = np.random.default_rng(44)
+    blocks = oracle.random_blocks(rng, t, N * (K // 256)).reshape(N, -1)
+    x = activations(M, K, seed=45)
+    y0 = rng.standard_normal((M, ldy)).astype(np.float32)
+    W, X, Y = hip.to_device(blocks), hip.to_device(x), hip.to_device(y0)
+    tier_amd.qgemm(W.ptr, t, tier_amd.q_row_bytes(t, K), X.ptr, Y.ptr, M, N, K, ldy=ldy, beta=1.0)
+    hip.synchronize()
+    got = Y.download(np.float32, M * ldy).reshape(M, ldy)
+    assert np.array_equal(got[:, N:], y0[:, N:])
+    w16 = oracle.h2f(oracle.dequant(blocks, t, K, oracle.OUT_F16)).reshape(N, K)
+    ref = x.astype(np.float64) @ w16.astype(np.float64).T + y0[:, :N].astype(np.float64)
+    assert oracle.rel_fro(got[:, :N], ref) <= BAR
 
 
 @pytest.mark.parametrize("N,K", [(5120, 5120), (5120, 14336)])
