@@ -80,7 +80,7 @@ def test_gemv_block32_rows_in_lds(gpu, t, N, K):
 
 
 @pytest.mark.parametrize("N,K", [(8, 256), (24, 768), (40, 5120), (1000, 2304), (1024, 4096), (10240, 5120),
-                                 (2000, 14336), (10240, 8192), (10240, 14336)])
+                                 (2000, 14336), (4096, 14336), (4100, 14336), (10240, 8192), (10240, 14336)])
 def test_gemv_q6k_mfma(gpu, N, K):
     """Q6_K on int8 MFMA: 210-byte super-blocks leave rows at every even shift in
     their 16-byte window; one to four K parts per row tile; every launch shape."""
@@ -158,6 +158,19 @@ def test_gemv_tall_tiles_per_workgroup(gpu, t, N, K):
     assert oracle.rel_fro(y, want) <= TOL
     # every row written, none left at the 0xff fill
     assert np.all(np.isfinite(y))
+
+
+@pytest.mark.parametrize("t", [tier_amd.Q4_K, tier_amd.Q5_K])
+@pytest.mark.parametrize("N", [1000, 4096, 4100])
+def test_gemv_long_k_launch_shapes(gpu, t, N):
+    """K = 14336 around the 256-tile boundary between one tile x eight K parts and two
+    tiles x four K parts per workgroup."""
+    K = 14336
+    rng = np.random.default_rng(N + t)
+    blocks = oracle.random_blocks(rng, t, N * (K // 256)).reshape(N, -1)
+    x = rng.standard_normal(K).astype(np.float32)
+    y = _gemv(blocks, t, x, N, K)
+    assert oracle.rel_fro(y, oracle.gemv_f64(blocks, t, x, N, K)) <= TOL
 
 
 def test_gemv_zero_and_extreme_inputs(gpu):

@@ -213,6 +213,9 @@ int qgemv_q4k(const void* W, size_t rb, const float* x, float* y, int N, int K, 
     return launch<QT_Q4_K, 2, 4, 2, 2, 1, 8192>(W, rb, x, y, N, K, s);
   }
   if (tiles >= 640) return launch<QT_Q4_K, 4, 1, 4, 2, 4, 14336>(W, rb, x, y, N, K, s);  // 24.2 against 25.5 us
+  // up to one tile per CU: one tile, K in eight parts (4096x14336: 9.4-9.6 against 11.7 us;
+  // 1024x14336: 7.1 against 9.4 us)
+  if (tiles <= 256) return launch<QT_Q4_K, 1, 8, 1, 2, 2, 14336>(W, rb, x, y, N, K, s);
   return launch<QT_Q4_K, 2, 4, 2, 2, 2, 14336>(W, rb, x, y, N, K, s);
 }
 
@@ -236,6 +239,7 @@ int qgemv_mfma(const void* W, int qtype, size_t rb, const float* x, float* y, in
       return launch<QT_Q5_K, 4, 2, 2, 2, 2, 8192>(W, rb, x, y, N, K, s);
     }
     if (tiles >= 640) return launch<QT_Q5_K, 4, 2, 1, 2, 2, 14336>(W, rb, x, y, N, K, s);
+    if (tiles <= 256) return launch<QT_Q5_K, 1, 8, 1, 2, 2, 14336>(W, rb, x, y, N, K, s);  // 4096x14336: 11.0 against 13.8 us
     return launch<QT_Q5_K, 2, 4, 2, 2, 2, 14336>(W, rb, x, y, N, K, s);
   }
   if (K <= 5120) {

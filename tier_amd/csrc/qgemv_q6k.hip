@@ -256,6 +256,7 @@ int qgemv_q6k(const void* W, size_t rb, const float* x, float* y, int N, int K, 
     if (tiles < 640) return launch<2, 4, 1, 2, 2, 8192>(W, rb, x, y, N, K, s);
     return launch<4, 2, 1, 2, 2, 8192>(W, rb, x, y, N, K, s);
   }
+  if (tiles <= 256) return launch<1, 8, 1, 2, 2, 14336>(W, rb, x, y, N, K, s);  // 1024x14336: 13.2 against 21.8 us
   if (tiles < 640) return launch<2, 4, 1, 2, 2, 14336>(W, rb, x, y, N, K, s);
   return launch<4, 2, 1, 2, 2, 14336>(W, rb, x, y, N, K, s);
 }
