@@ -18,6 +18,8 @@ TOL = 1e-5
 
 def _gemv(blocks, t, x, N, K):
     rb = tier_amd.q_row_bytes(t, K)
+    # the kernel reads N * rb bytes: a short host array is a test bug, stopped before the launch
+    assert blocks.nbytes == N * rb, (blocks.nbytes, N * rb)
     W = hip.to_device(blocks)
     X = hip.to_device(x)
     Y = hip.DeviceBuffer(N * 4)
@@ -160,15 +162,26 @@ def test_gemv_tall_tiles_per_workgroup(gpu, t, N, K):
     assert np.all(np.isfinite(y))
 
 
-@pytest.mark.parametrize("t", [tier_amd.Q4_K, tier_amd.Q5_K])
+@pytest.mark.parametrize("t", [tier_amd.Q4_K, tier_amd.Q5_K, tier_amd.Q8_0])
 @pytest.mark.parametrize("N", [1000, 4096, 4100])
 def test_gemv_long_k_launch_shapes(gpu, t, N):
     """K = 14336 around the 256-tile boundary between one tile x eight K parts and two
     tiles x four K parts per workgroup."""
     K = 14336
     rng = np.random.default_rng(N + t)
-    blocks = oracle.random_blocks(rng, t, N * (K // 256)).reshape(N, -1)
+    blocks = oracle.random_blocks(rng, t, N * (K // oracle.block(t)[0])).reshape(N, -1)
     x = rng.standard_normal(K).astype(np.float32)
+    y = _gemv(blocks, t, x, N, K)
+    assert oracle.rel_fro(y, oracle.gemv_f64(blocks, t, x, N, K)) <= TOL
+
+
+@pytest.mark.parametrize("N,K", [(17, 256), (1000, 768), (4096, 4096), (4096, 5120), (4100, 5120)])
+def test_gemv_q8_0_eight_k_parts(gpu, N, K):
+    """q8_0 at most 256 row tiles: one tile x eight K parts, down to K parts with no
+    group of eight blocks (K = 256, 768)."""
+    t = tier_amd.Q8_0
+    blocks = quantized_weight(t, N, K, seed=N + K)
+    x = activations(1, K, seed=K)[0]
     y = _gemv(blocks, t, x, N, K)
     assert oracle.rel_fro(y, oracle.gemv_f64(blocks, t, x, N, K)) <= TOL
 
