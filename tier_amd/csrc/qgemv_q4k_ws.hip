@@ -12,7 +12,9 @@
 // slots of its own with global_load_lds_dwordx4, D stages ahead.  Long row
 // segments and few concurrent tiles measured faster than 16 short segments
 // per wave from 864 tiles at once (13824x5120: 8.9 against 9.2 us; 10240x8192:
-// 10.4 against 11.8 us).
+// 10.4 against 11.8 us).  The loads carry the non-temporal hint: every weight
+// byte is read once (13824x5120: 8.9-9.2 against 9.3-9.5 us; 10240x8192: 10.2
+// against 10.7 us).
 //
 // Consumers.  GS == NC: consumer c owns super-block column c of every stage,
 // i.e. columns c, c + NC, ... of every row, so the x digits and the x metadata
@@ -131,7 +133,7 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
 #pragma unroll
       for (int j = 0; j < NLD; ++j)
         if (j < NLD - 1 || L::LAST == 64 || lane < L::LAST)
-          dma16(b + (size_t)min(roff[j], rmax) * rb + min(coff[j], lastb), dst + j * 1024);
+          dma16_nt(b + (size_t)min(roff[j], rmax) * rb + min(coff[j], lastb), dst + j * 1024);
     };
     const int pro = min(D, total);
     for (int q = 0; q < pro; ++q) issue(q);

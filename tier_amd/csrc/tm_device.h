@@ -455,6 +455,13 @@ __device__ __forceinline__ void dma16(const void* p, uint32_t lds_addr) {
                "s"(__builtin_amdgcn_readfirstlane(lds_addr))
                : "memory");
 }
+// The same with the non-temporal hint: the bytes are streamed once and should not
+// displace what the caches hold.
+__device__ __forceinline__ void dma16_nt(const void* p, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(p),
+               "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+               : "memory");
+}
 template <int N>
 __device__ __forceinline__ void vm_wait() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
