@@ -119,9 +119,12 @@ int tiermm_dequant(const void* W, int qtype, size_t rb, int cols, size_t r0, siz
 
 /* --------------------------------------------------------------- decode GEMV */
 /* gemv_q (tier.cpp:299-306, launched at 2357): y[r] = sum_k q_val(W_r, k) * x[k]
- * for r < N, fp32 accumulation.  W: N rows of rb bytes; x: K fp32; y: N fp32.
- * qtype: the GPU types of tiermm_dequant; dense rows (F32/F16/BF16) go to
- * tiermm_gemv's kernel and must start 16-byte aligned. */
+ * for r < N, fp32 accumulation.  W: N rows of rb bytes; x: K fp32, 16-byte
+ * aligned, any K; y: N fp32.  qtype: the GPU types of tiermm_dequant; dense
+ * rows (F32/F16/BF16) go to tiermm_gemv's kernel and must start 16-byte
+ * aligned.  Non-finite x: y takes gemv_q's fp32 result classes exactly -- NaN
+ * everywhere for a NaN in x, and for +-Inf at column k, +-Inf or NaN per row
+ * from the signs (and zeros) of q_val(W_r, k). */
 int tiermm_qgemv(const void* W, int qtype, size_t rb, const float* x, float* y, int N, int K,
                  tiermm_stream_t stream);
 
@@ -137,7 +140,7 @@ int tiermm_split3_f16(const float* x, uint16_t* parts, size_t n, size_t part_str
 /* gemv<T> (tier.cpp:2261-2268, launched at 2345, 2363, 2616 for the fp16/bf16
  * frozen matrices and the LM head): y[r] = sum_k float(W[r][k]) * x[k], fp32
  * accumulation.  wtype in {TIERMM_F32, TIERMM_F16 (tier_fp16 bits),
- * TIERMM_BF16}; W: N rows of K elements, 16-byte aligned; K <= 16384. */
+ * TIERMM_BF16}; W: N rows of K elements, 16-byte aligned; any K. */
 int tiermm_gemv(const void* W, int wtype, const float* x, float* y, int N, int K, tiermm_stream_t stream);
 
 /* split3_k (tier.cpp:866-867) / split3s (tier.cpp:2159-2161): the same split

@@ -81,8 +81,8 @@ def test_argument_checks_return_before_device_work():
     assert L.tiermm_qgemv(18, tier_amd.Q4_K, 144, 16, 16, 1, 256, None) == tier_amd.EINVAL
     # columns not whole blocks (F4: down_proj K=1408 cannot be Q4_K)
     assert L.tiermm_qgemv(16, tier_amd.Q4_K, 792, 16, 16, 1, 1408, None) == tier_amd.UNSUPPORTED
-    # K beyond the staged-x limit
-    assert L.tiermm_qgemv(16, tier_amd.Q8_0, 34 * 1024, 16, 16, 1, 32768, None) == tier_amd.UNSUPPORTED
+    # x must be 16-byte aligned (any K is taken: gemv_q has no K bound)
+    assert L.tiermm_qgemv(16, tier_amd.Q8_0, 34 * 1024, 20, 16, 1, 32768, None) == tier_amd.EINVAL
     # dX layout: lda must cover m (A is m x k column-major); unknown op / mode
     assert L.tiermm_x3_gemm(tier_amd.OP_N, 64, 64, 64, 16, 32, 16, 0.0, 16, 64, None, 0, None) == tier_amd.EINVAL
     assert L.tiermm_x3_gemm(7, 64, 64, 64, 16, 64, 16, 0.0, 16, 64, None, 0, None) == tier_amd.EINVAL

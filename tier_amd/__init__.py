@@ -349,11 +349,12 @@ def moe_combine(Y_sorted: int, token_pairs: int, pair_weight: int, out: int, T: 
 
 def qlinear(W: int, qtype: int, rb: int, x: int, y: int, M: int, N: int, K: int, ws: int | None = None,
             ws_bytes: int = 0, stream=None) -> None:
-    """The quantized branch of chat_lin (tier.cpp:2356-2359): GEMV at M=1, dequant-GEMM above."""
+    """The quantized branch of chat_lin (tier.cpp:2356-2359): GEMV at M=1; above, fp32
+    dequant and an fp32-accurate product (MODE_F32), as the engine's dequant + SGEMM."""
     if M == 1:
         gemv_q(W, qtype, rb, x, y, N, K, stream)
     else:
-        qgemm(W, qtype, rb, x, y, M, N, K, N, MODE_X3REF, 0.0, ws, ws_bytes, stream)
+        qgemm(W, qtype, rb, x, y, M, N, K, N, MODE_F32, 0.0, ws, ws_bytes, stream)
 
 
 # ------------------------------------------------- chat linears with streaming

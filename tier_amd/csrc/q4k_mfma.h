@@ -17,6 +17,29 @@ constexpr int XQ_T = 256;              // per MFMA step t
 constexpr int META_SB = 64;            // 4 g x float4 (f_g, f_4+g, S_g, S_4+g)
 constexpr int ZERO_BYTES = 4 * XQ_T;   // zero rows read by the A lanes that carry no digit
 
+// Whether one of the 16 values is NaN or +-Inf.  The digits below carry finite
+// x only; a workgroup whose x holds such a value replaces its rows by
+// nonfinite_terms (tm_device.h).
+__device__ __forceinline__ bool nonfinite16(const float (&v)[16]) {
+  bool any = false;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) any |= !__builtin_isfinite(v[i]);
+  return any;
+}
+
+// Publishes whether any lane of the calling wave saw a non-finite x value: every
+// lane of the wave calls it, lane 0 writes flags[wave].  Read back with
+// flags_any once a barrier has passed.
+__device__ __forceinline__ void publish_nonfinite(bool bad, int* flags, int wave, int lane) {
+  const bool wbad = __ballot(bad) != 0;
+  if (lane == 0) flags[wave] = wbad ? 1 : 0;
+}
+__device__ __forceinline__ bool flags_any(const int* flags, int n) {
+  int a = 0;
+  for (int i = 0; i < n; ++i) a |= flags[i];
+  return a != 0;
+}
+
 // Prepare x elements [16h, 16h+16) of sub-block s (h = half, values in v): the
 // partner thread (lane ^ 1) holds the other half; both reach this together.
 __device__ __forceinline__ void prep_half(int s, int h, const float (&v)[16], uint8_t* xq, float* meta) {

@@ -295,13 +295,9 @@ int launch_q(const QArgs& a, hipStream_t s, const char* who) {
   constexpr int PR = BN / 4, RSLOT = (PR * 48 + 1023) / 1024 * 1024;
   constexpr size_t lds = 3 * (size_t)BN * 64 + 4 * 8 * (size_t)RSLOT + 2 * 4 * 4 * 4;
   static_assert(lds <= 160 * 1024, "LDS budget");
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)qgemm_q4k_x3ref<BN, KS>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return hip_fail(e, who);
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> attr{0};
+  int st = lds_attr_once(attr, (const void*)qgemm_q4k_x3ref<BN, KS>, (int)lds, who);
+  if (st) return st;
   qgemm_q4k_x3ref<BN, KS><<<(unsigned)a.tile0[a.ngroups] * KS, 512, lds, s>>>(a);
   TM_LAUNCH_CHECK(who);
   return TIERMM_OK;
@@ -340,6 +336,7 @@ struct QPlan {
 
 bool plan_ok(int bn, int ks, int K, size_t rows_total, int N, bool split) {
   if (ks > 1 && (!split || (K / 256) % ks || (size_t)ks * rows_total * N * 4 > kMaxPartials)) return false;
+  if (ks < acc_chunks(K)) return false;  // each split's accumulator sums at most the chunk of the x3 GEMMs
   for (int b : kBns)
     if (b == bn) return ks == 1 || ks == 2 || ks == 4;
   return false;
@@ -355,7 +352,7 @@ QPlan q_plan(const int* rows, int n, int N, int K, int cus, bool split) {
     if (sscanf(e, "%d,%d", &bn, &ks) == 2 && plan_ok(bn, ks, K, rows_total, N, split)) return {bn, ks};
   }
   const int nk = K / QBK;
-  QPlan best{128, 1};
+  QPlan best{0, 0};  // none: the shape does not take the fused kernel
   double best_t = -1;
   for (int i = 0; i < 6; ++i)
     for (int ks = 1; ks <= 4; ks *= 2) {
@@ -387,6 +384,13 @@ size_t qgemm_q4k_partials_bytes(int M, int N, int K) {
   return pl.ks > 1 ? (size_t)pl.ks * M * N * sizeof(float) : 0;
 }
 
+// Whether the fused kernel takes n groups of these row counts: some (BN, KS) fits,
+// KS > 1 only when `split` (one group with a partial-sum workspace), and every
+// split short enough for one fp32 accumulator (acc_chunks).
+bool qgemm_q4k_fusable(const int* rows, int n, int N, int K, bool split) {
+  return q_plan(rows, n, N, K, cus_or_default(), split && n == 1).bn != 0;
+}
+
 // Fused q4_K x3-ref GEMM over n groups (rows[g] rows of x from row0[g], weight W[g]);
 // the x planes hold every group's rows (plane stride xs).  A single group may split K,
 // with `partials` (qgemm_q4k_partials_bytes) holding the partial sums.
@@ -394,6 +398,7 @@ int qgemm_q4k_fused_groups(const void* const* W, const int* row0, const int* row
                            const uint16_t* xparts, size_t xs, float* Y, int ldy, int N, int K, float beta, int cus,
                            hipStream_t s, const char* who, float* partials) {
   const QPlan pl = q_plan(rows, n, N, K, cus, n == 1 && partials != nullptr);
+  if (pl.bn == 0) return set_error(TIERMM_UNSUPPORTED, "%s: no fused q4_K plan for N=%d K=%d", who, N, K);
   for (int g0 = 0; g0 < n; g0 += QG) {
     QArgs a{};
     a.X = xparts; a.xs = xs; a.Y = Y; a.rb = rb; a.ldy = ldy; a.N = N; a.K = K; a.beta = beta;

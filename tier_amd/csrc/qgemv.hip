@@ -19,7 +19,7 @@ int check_qweight(const char* who, const void* W, int qtype, size_t rb, int cols
 
 namespace {
 
-constexpr int kMaxK = 16384;  // x staged whole in LDS: 64 KiB
+constexpr int kMaxLdsK = 16384;  // x staged whole in LDS (64 KiB) up to this K; read from global above
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -27,13 +27,18 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-template <int QT, int R>
+// XL: x staged in LDS (K <= kMaxLdsK); else read from global memory, where the
+// workgroups' repeated reads of the same K floats stay in L2.
+template <int QT, int R, bool XL>
 __global__ __launch_bounds__(256) void qgemv_generic(const uint8_t* __restrict__ W, size_t rb,
                                                      const float* __restrict__ x, float* __restrict__ y, int N,
                                                      int K) {
-  extern __shared__ float xs[];
-  for (int i = threadIdx.x * 4; i < K; i += 256 * 4) *(float4*)&xs[i] = *(const float4*)&x[i];
-  __syncthreads();
+  extern __shared__ float xsh[];
+  const float* xs = XL ? xsh : x;
+  if (XL) {
+    for (int i = threadIdx.x * 4; i < K; i += 256 * 4) *(float4*)&xsh[i] = *(const float4*)&x[i];
+    __syncthreads();
+  }
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int row0 = (blockIdx.x * 4 + wave) * R;
   if (row0 >= N) return;
@@ -65,7 +70,10 @@ template <int QT>
 int launch_generic(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
   constexpr int R = 2;
   const unsigned grid = (unsigned)((N + 4 * R - 1) / (4 * R));
-  qgemv_generic<QT, R><<<grid, 256, (size_t)K * 4, s>>>((const uint8_t*)W, rb, x, y, N, K);
+  if (K <= kMaxLdsK)
+    qgemv_generic<QT, R, true><<<grid, 256, (size_t)K * 4, s>>>((const uint8_t*)W, rb, x, y, N, K);
+  else
+    qgemv_generic<QT, R, false><<<grid, 256, 0, s>>>((const uint8_t*)W, rb, x, y, N, K);
   TM_LAUNCH_CHECK("tiermm_qgemv: launch");
   return TIERMM_OK;
 }
@@ -165,9 +173,34 @@ __global__ __launch_bounds__(256) void qgemv_staged(const uint8_t* __restrict__ 
     dma16(g0 + min(off, total - 16), l0 + (uint32_t)i * 1024);
   }
   float* xs = (float*)(smem + wbytes);
-  for (int i = tid * 4; i < K; i += 1024) *(float4*)&xs[i + (i >> 6) * 4] = *(const float4*)&x[i];
+  // per wave: x held a non-finite value (in the dynamic LDS, after x: the kernel
+  // opts into all 160 KiB of dynamic LDS, so it has no static LDS)
+  int* nf = (int*)(xs + (size_t)K / 64 * 68);
+  bool bad = false;
+  for (int i = tid * 4; i < K; i += 1024) {
+    const float4 v = *(const float4*)&x[i];
+    bad |= !__builtin_isfinite(v.x) || !__builtin_isfinite(v.y) || !__builtin_isfinite(v.z) ||
+           !__builtin_isfinite(v.w);
+    *(float4*)&xs[i + (i >> 6) * 4] = v;
+  }
+  {
+    const bool wbad = __ballot(bad) != 0;
+    if (lane == 0) nf[wave] = wbad ? 1 : 0;
+  }
   vm_wait<0>();
   __syncthreads();
+  if (nf[0] | nf[1] | nf[2] | nf[3]) {
+    // NaN or +-Inf in x: d * sum(q * x) + m * sum(x) would not give the per-element
+    // products' class (q = 0 times Inf), so the rows take gemv_q's non-finite sums
+    for (int r = wave; r < RW; r += 4) {
+      const int row = row0 + r;
+      if (row < N) {
+        const float s = nonfinite_terms<QT>(W + (size_t)row * rb, x, 0, K, lane);
+        if (lane == 0) y[row] = s;
+      }
+    }
+    return;
+  }
 
   const int U = K / 64;
   float acc[R];
@@ -206,8 +239,10 @@ __global__ __launch_bounds__(256) void qgemv_staged(const uint8_t* __restrict__ 
   }
 }
 
-// LDS of the staged kernel: the rows (whole KiB) plus padded x.
-size_t staged_lds(size_t rb, int K, int R) { return (4 * R * rb + 1023) / 1024 * 1024 + (size_t)K / 64 * 68 * 4; }
+// LDS of the staged kernel: the rows (whole KiB), padded x, four non-finite flags.
+size_t staged_lds(size_t rb, int K, int R) {
+  return (4 * R * rb + 1023) / 1024 * 1024 + (size_t)K / 64 * 68 * 4 + 4 * sizeof(int);
+}
 
 template <int QT>
 int launch_staged(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
@@ -216,14 +251,10 @@ int launch_staged(const void* W, size_t rb, const float* x, float* y, int N, int
   const size_t lds = staged_lds(rb, K, R);
   const uint32_t wbytes = (uint32_t)((4 * R * rb + 1023) / 1024 * 1024);
   const unsigned grid = (unsigned)((N + 4 * R - 1) / (4 * R));
-  static bool attr_set = false;
-  if (!attr_set) {
-    for (auto f : {(const void*)qgemv_staged<QT, 1>, (const void*)qgemv_staged<QT, 2>}) {
-      hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-      if (e != hipSuccess) return hip_fail(e, "tiermm_qgemv");
-    }
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> attr1{0}, attr2{0};
+  int st = lds_attr_once(attr1, (const void*)qgemv_staged<QT, 1>, 160 * 1024, "tiermm_qgemv");
+  if (!st) st = lds_attr_once(attr2, (const void*)qgemv_staged<QT, 2>, 160 * 1024, "tiermm_qgemv");
+  if (st) return st;
   if (R == 2)
     qgemv_staged<QT, 2><<<grid, 256, lds, s>>>((const uint8_t*)W, rb, x, y, N, K, wbytes);
   else
@@ -286,13 +317,16 @@ struct Dense<TIERMM_BF16> {
   }
 };
 
-template <int T, int R>
+template <int T, int R, bool XL>
 __global__ __launch_bounds__(256) void gemv_dense(const uint8_t* __restrict__ W, const float* __restrict__ x,
                                                   float* __restrict__ y, int N, int K) {
   using D = Dense<T>;
-  extern __shared__ float xs[];
-  for (int i = threadIdx.x; i < K; i += 256) xs[i] = x[i];
-  __syncthreads();
+  extern __shared__ float xsh[];  // x staged in LDS when XL (K <= kMaxLdsK), else read from global
+  const float* xs = XL ? xsh : x;
+  if (XL) {
+    for (int i = threadIdx.x; i < K; i += 256) xsh[i] = x[i];
+    __syncthreads();
+  }
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int row0 = (blockIdx.x * 4 + wave) * R;
   if (row0 >= N) return;
@@ -329,7 +363,10 @@ template <int T>
 int launch_dense(const void* W, const float* x, float* y, int N, int K, hipStream_t s) {
   constexpr int R = 4;
   const unsigned grid = (unsigned)((N + 4 * R - 1) / (4 * R));
-  gemv_dense<T, R><<<grid, 256, (size_t)K * 4, s>>>((const uint8_t*)W, x, y, N, K);
+  if (K <= kMaxLdsK)
+    gemv_dense<T, R, true><<<grid, 256, (size_t)K * 4, s>>>((const uint8_t*)W, x, y, N, K);
+  else
+    gemv_dense<T, R, false><<<grid, 256, 0, s>>>((const uint8_t*)W, x, y, N, K);
   TM_LAUNCH_CHECK("tiermm_gemv: launch");
   return TIERMM_OK;
 }
@@ -392,7 +429,6 @@ extern "C" int tiermm_qgemv(const void* W, int qtype, size_t rb, const float* x,
   if (st) return st;
   if (N < 0) return set_error(TIERMM_EINVAL, "tiermm_qgemv: N < 0");
   if (N == 0) return TIERMM_OK;
-  if (K > kMaxK) return set_error(TIERMM_UNSUPPORTED, "tiermm_qgemv: K=%d above %d", K, kMaxK);
   if (!x || !y || ((uintptr_t)x % 16)) return set_error(TIERMM_EINVAL, "tiermm_qgemv: x must be 16-byte aligned");
   if ((qtype == QT_F32 || qtype == QT_F16 || qtype == QT_BF16) && ((uintptr_t)W % 16))
     return set_error(TIERMM_EINVAL, "tiermm_qgemv: dense rows must start 16-byte aligned");
@@ -404,7 +440,6 @@ extern "C" int tiermm_gemv(const void* W, int wtype, const float* x, float* y, i
     return set_error(TIERMM_UNSUPPORTED, "tiermm_gemv: weight type %d", wtype);
   if (N < 0 || K < 0) return set_error(TIERMM_EINVAL, "tiermm_gemv: negative size");
   if (N == 0) return TIERMM_OK;
-  if (K > kMaxK) return set_error(TIERMM_UNSUPPORTED, "tiermm_gemv: K=%d above %d", K, kMaxK);
   if (!W || !x || !y || ((uintptr_t)W % 16))
     return set_error(TIERMM_EINVAL, "tiermm_gemv: W must be non-null and 16-byte aligned");
   hipStream_t s = (hipStream_t)stream;

@@ -104,7 +104,9 @@ __global__ __launch_bounds__(64 * RT * KS) void qgemv_q4k_mfma(const uint8_t* __
 #pragma unroll
     for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(xr[j][i]));
 
+  __shared__ int nf[RT * KS];  // per wave: x held a non-finite value
   for (int i = tid; i < ZERO_BYTES / 4; i += NT) ((uint32_t*)zero)[i] = 0u;
+  bool bad = false;
 #pragma unroll
   for (int j = 0; j < XP; ++j) {
     const int hh = tid + j * NT;  // K/16 is even: both threads of a pair are in range together
@@ -114,10 +116,13 @@ __global__ __launch_bounds__(64 * RT * KS) void qgemv_q4k_mfma(const uint8_t* __
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int w = 0; w < 4; ++w) v[4 * i + w] = __uint_as_float(xr[j][i][w]);
+      bad |= nonfinite16(v);
       prep_half(hh >> 1, hh & 1, v, xq, meta);
     }
   }
+  publish_nonfinite(bad, nf, wave, lane);
   __syncthreads();
+  const bool xbad = flags_any(nf, RT * KS);  // uniform over the workgroup
 
   // ---- per-lane constants
   // A operand: digits of virtual group g, live for MFMA parity p when n/4 == 2(g/2)+p.
@@ -153,6 +158,17 @@ __global__ __launch_bounds__(64 * RT * KS) void qgemv_q4k_mfma(const uint8_t* __
   }
   vm_wait<0>();  // drain the clamped tail loads before the wave ends
 
+  if (xbad) {  // NaN or +-Inf in x: the workgroup's rows take gemv_q's non-finite sums
+    for (int r = wave; r < RT * 16; r += RT * KS) {
+      const int row = blockIdx.x * RT * 16 + r;
+      if (row < N) {
+        const float s = nonfinite_terms<QT>(W + (size_t)row * rb, x, 0, K, lane);
+        if (lane == 0) y[row] = s;
+      }
+    }
+    return;
+  }
+
   // ---- reduce over the four lane groups of a row, then over the KS waves
   acc += __shfl_xor(acc, 16, 64);
   acc += __shfl_xor(acc, 32, 64);
@@ -173,17 +189,14 @@ __global__ __launch_bounds__(64 * RT * KS) void qgemv_q4k_mfma(const uint8_t* __
 template <int QT, int RT, int KS, int GS, int STAGES, int XP, int XK>
 int launch(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
   constexpr size_t lds = (size_t)RT * KS * (STAGES * Stage<GS, MfmaFmt<QT>::SBB>::BYTES + 64);  // plus the static x digits
-  static_assert(xq_bytes(XK) + lds <= 160 * 1024, "LDS budget");
+  static_assert(xq_bytes(XK) + 4 * RT * KS + lds <= 160 * 1024, "LDS budget (x digits, flags, ring)");
   static_assert(XK / 16 <= 64 * RT * KS * XP, "x preparation: one thread per 16 elements");
   const int tiles = (N + 15) / 16;
   const unsigned grid = (unsigned)((tiles + RT - 1) / RT);
-  static bool attr_set = false;  // dynamic LDS above 64 KiB is opted into once per instantiation
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)qgemv_q4k_mfma<QT, RT, KS, GS, STAGES, XP, XK>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return hip_fail(e, "tiermm_qgemv: q4_K LDS attribute");
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> attr{0};  // dynamic LDS above 64 KiB is opted into per device
+  int st = lds_attr_once(attr, (const void*)qgemv_q4k_mfma<QT, RT, KS, GS, STAGES, XP, XK>, (int)lds,
+                         "tiermm_qgemv: q4_K LDS attribute");
+  if (st) return st;
   qgemv_q4k_mfma<QT, RT, KS, GS, STAGES, XP, XK><<<grid, 64 * RT * KS, lds, s>>>((const uint8_t*)W, rb, x, y, N, K);
   TM_LAUNCH_CHECK("tiermm_qgemv: q4_K launch");
   return TIERMM_OK;

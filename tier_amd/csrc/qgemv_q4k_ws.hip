@@ -96,6 +96,7 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
   static_assert(SLOT % 16 == 0, "16-byte aligned slots");
   extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // L::LDS bytes
   __shared__ __attribute__((aligned(16))) uint8_t xlds[xq_bytes(XK)];
+  __shared__ int nf[NC];               // per consumer: x held a non-finite value
   int* full = (int*)(ring + L::RING);  // [NS][NP]
   int* done = full + NS * NP;          // [NS][NCP]
   float* red = (float*)(done + NS * NCP);  // [R][NC][16]
@@ -163,6 +164,7 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
       for (int i = 0; i < 4; ++i) xr[j][i] = *(const u32x4*)(x + hh * 16 + 4 * i);
     }
     for (int i = tid; i < ZERO_BYTES / 4; i += NT) ((uint32_t*)zero)[i] = 0u;
+    bool bad = false;
 #pragma unroll
     for (int j = 0; j < XP; ++j) {
       const int hh = tid + j * NT;
@@ -172,9 +174,11 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
         for (int i = 0; i < 4; ++i)
 #pragma unroll
           for (int w = 0; w < 4; ++w) v[4 * i + w] = __uint_as_float(xr[j][i][w]);
+        bad |= nonfinite16(v);
         prep_half(hh >> 1, hh & 1, v, xq, meta);
       }
     }
+    publish_nonfinite(bad, nf, c, lane);
     __syncthreads();
     // this lane's A operands of its columns c + GS*m (zeros where it carries no digit)
     i32x4 A[MS][4];
@@ -214,6 +218,17 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
     }
     __syncthreads();
   }
+  if (flags_any(nf, NC)) {  // NaN or +-Inf in x: the rows take gemv_q's non-finite sums
+    for (int i = wave; i < R * 16; i += NC + NP) {
+      const int r = i >> 4, n = i & 15;
+      const int tile = (int)blockIdx.x + r * (int)gridDim.x;
+      if (tile < tiles && tile * 16 + n < N) {
+        const float s = nonfinite_terms<QT>(W + (size_t)(tile * 16 + n) * rb, x, 0, K, lane);
+        if (lane == 0) y[tile * 16 + n] = s;
+      }
+    }
+    return;
+  }
   for (int i = tid; i < R * 16; i += 64 * (NC + NP)) {
     const int r = i >> 4, n = i & 15;
     const int tile = (int)blockIdx.x + r * (int)gridDim.x;
@@ -229,17 +244,14 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
 template <int QT, int R, int NC, int NS, int D, int XP, int XK>
 int launch_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
   using L = WsLayout<QT, NC, NS, R>;
-  static_assert(xq_bytes(XK) + L::LDS <= 160 * 1024, "LDS budget");
+  static_assert(xq_bytes(XK) + 4 * NC + L::LDS <= 160 * 1024, "LDS budget (x digits, flags, ring)");
   static_assert(XK / 16 <= 64 * NC * XP, "x preparation: one thread per 16 elements");
   const int tiles = (N + 15) / 16;
   const unsigned grid = (unsigned)((tiles + R - 1) / R);
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)qgemv_q4k_ws<QT, R, NC, NS, D, XP, XK>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)L::LDS);
-    if (e != hipSuccess) return hip_fail(e, "tiermm_qgemv: q4_K LDS attribute");
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> attr{0};
+  int st = lds_attr_once(attr, (const void*)qgemv_q4k_ws<QT, R, NC, NS, D, XP, XK>, (int)L::LDS,
+                         "tiermm_qgemv: q4_K LDS attribute");
+  if (st) return st;
   qgemv_q4k_ws<QT, R, NC, NS, D, XP, XK><<<grid, 64 * (NC + NP), L::LDS, s>>>((const uint8_t*)W, rb, x, y, N, K);
   TM_LAUNCH_CHECK("tiermm_qgemv: q4_K launch");
   return TIERMM_OK;

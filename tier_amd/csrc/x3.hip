@@ -35,6 +35,7 @@ int qgemm_q4k_fused_groups(const void* const* W, const int* row0, const int* row
                            const uint16_t* xparts, size_t xs, float* Y, int ldy, int N, int K, float beta, int cus,
                            hipStream_t s, const char* who, float* partials);
 size_t qgemm_q4k_partials_bytes(int M, int N, int K);
+bool qgemm_q4k_fusable(const int* rows, int n, int N, int K, bool split);
 int device_cus(int* cus);
 
 namespace {
@@ -629,17 +630,54 @@ constexpr size_t big_lds() {
   return 2 * (size_t)(X3Mode<MODE>::NA * XB_M + X3Mode<MODE>::NB * TN) * 64;
 }
 
+// ---- K chunks.  The fp32 accumulator's rounding error grows like sqrt(K): one
+// accumulator over K = 14336 measured 1.4e-6 relative Frobenius error against
+// fp64 (x3-ref, config-4 down_proj), above the 2^-20 bar, against ~8e-7 at
+// K = 5120.  Above kAccChunkFrom a product therefore runs as balanced chunks of
+// at most kAccChunkMax columns, each summed from zero and added to C in fp32
+// (beta = 1 after the first chunk): chunks of 3584 bring K = 14336 to ~7e-7 (a
+// CPU model of the accumulation scaled to the measured error).  Each extra
+// chunk reads and writes C once more.
+int k_chunks(int K) { return acc_chunks(K); }
+
+// Element offset of column k0 (a multiple of 32) in a plane: k0 in a row-major
+// plane, k0 / 32 tiles of `tile` rows x 32 in a K-tiled one (ktile_index).
+size_t k_offset(int k0, int tile) { return tile ? (size_t)(k0 / 32) * tile * 32 : (size_t)k0; }
+
+// Runs launch(q) over the K chunks of a (one call when K <= kChunkFrom); shift(q, k0)
+// moves operands a launch reads beyond q.A / q.B (the grouped weights) to column k0.
+template <class L, class S>
+int run_k_chunks(const X3Args& a, L&& launch, S&& shift) {
+  const int P = k_chunks(a.K);
+  if (P == 1) return launch(a);
+  const int steps = a.K / BK;
+  for (int c = 0; c < P; ++c) {
+    const int s0 = (int)((long)c * steps / P), s1 = (int)((long)(c + 1) * steps / P);
+    X3Args q = a;
+    for (int i = 0; i < 3; ++i)
+      if (q.A[i]) q.A[i] += k_offset(s0 * BK, q.atile);
+    for (int i = 0; i < 2; ++i)
+      if (q.B[i]) q.B[i] += k_offset(s0 * BK, q.btile);
+    shift(s0 * BK);
+    q.K = (s1 - s0) * BK;
+    if (c > 0) q.beta = 1.f;
+    const int st = launch(q);
+    if (st) return st;
+  }
+  return TIERMM_OK;
+}
+template <class L>
+int run_k_chunks(const X3Args& a, L&& launch) {
+  return run_k_chunks(a, launch, [](int) {});
+}
+
 template <int MODE, int TN>
 int launch_x3_big_tn(const X3Args& a, hipStream_t s, const char* who) {
   constexpr size_t lds = big_lds<MODE, TN>();
   static_assert(lds <= 160 * 1024, "LDS budget");
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)gemm_x3_big<MODE, TN>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)lds);
-    if (e != hipSuccess) return hip_fail(e, who);
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> attr{0};
+  int st = lds_attr_once(attr, (const void*)gemm_x3_big<MODE, TN>, (int)lds, who);
+  if (st) return st;
   const int nt = ((a.M + XB_M - 1) / XB_M) * ((a.N + TN - 1) / TN);
   gemm_x3_big<MODE, TN><<<nt, 512, lds, s>>>(a);
   TM_LAUNCH_CHECK(who);
@@ -648,41 +686,48 @@ int launch_x3_big_tn(const X3Args& a, hipStream_t s, const char* who) {
 
 template <int MODE>
 int launch_x3_big(const X3Args& a, hipStream_t s, const char* who) {
-  return big_tn(a.N) == 352 ? launch_x3_big_tn<MODE, 352>(a, s, who) : launch_x3_big_tn<MODE, 320>(a, s, who);
+  return run_k_chunks(a, [&](const X3Args& q) {
+    return big_tn(q.N) == 352 ? launch_x3_big_tn<MODE, 352>(q, s, who) : launch_x3_big_tn<MODE, 320>(q, s, who);
+  });
 }
 
 // g.tile0 counts tiles of width TN.
 template <int MODE, int TN>
 int launch_x3_big_grouped(const X3Args& a, const X3Groups& g, hipStream_t s, const char* who) {
   constexpr size_t lds = big_lds<MODE, TN>();
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)gemm_x3_big_grouped<MODE, TN>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return hip_fail(e, who);
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> attr{0};
+  int st = lds_attr_once(attr, (const void*)gemm_x3_big_grouped<MODE, TN>, (int)lds, who);
+  if (st) return st;
   if (g.tile0[g.n] == 0) return TIERMM_OK;
-  gemm_x3_big_grouped<MODE, TN><<<g.tile0[g.n], 512, lds, s>>>(a, g);
+  X3Groups gk = g;  // the groups' weights (ldb = K, or K-tiled) move with the K chunks
+  return run_k_chunks(
+      a,
+      [&](const X3Args& q) {
+        gemm_x3_big_grouped<MODE, TN><<<gk.tile0[gk.n], 512, lds, s>>>(q, gk);
+        TM_LAUNCH_CHECK(who);
+        return (int)TIERMM_OK;
+      },
+      [&](int k0) {
+        for (int i = 0; i < g.n; ++i) gk.B[i] = g.B[i] + k_offset(k0, a.btile);
+      });
+}
+
+template <int BM, int BN, int MODE>
+int launch_x3_one(const X3Args& a, hipStream_t s, const char* who) {
+  using Md = X3Mode<MODE>;
+  const int nt = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+  constexpr size_t lds = 2 * (size_t)(Md::NA * BM + Md::NB * BN) * LDS_ROW * sizeof(uint16_t);
+  static std::atomic<uint64_t> attr{0};  // dynamic LDS above 64 KiB is opted into per device
+  int st = lds_attr_once(attr, (const void*)gemm_x3_kernel<BM, BN, MODE>, (int)lds, who);
+  if (st) return st;
+  gemm_x3_kernel<BM, BN, MODE><<<nt, 256, lds, s>>>(a);
   TM_LAUNCH_CHECK(who);
   return TIERMM_OK;
 }
 
 template <int BM, int BN, int MODE>
 int launch_x3(const X3Args& a, hipStream_t s, const char* who) {
-  using Md = X3Mode<MODE>;
-  const int nt = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-  constexpr size_t lds = 2 * (size_t)(Md::NA * BM + Md::NB * BN) * LDS_ROW * sizeof(uint16_t);
-  static bool attr_set = false;  // dynamic LDS above 64 KiB must be opted into once per kernel
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)gemm_x3_kernel<BM, BN, MODE>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return hip_fail(e, who);
-    attr_set = true;
-  }
-  gemm_x3_kernel<BM, BN, MODE><<<nt, 256, lds, s>>>(a);
-  TM_LAUNCH_CHECK(who);
-  return TIERMM_OK;
+  return run_k_chunks(a, [&](const X3Args& q) { return launch_x3_one<BM, BN, MODE>(q, s, who); });
 }
 
 // Tiles of the 256x320 kernel: it pays off once they occupy most of the CUs.
@@ -700,6 +745,16 @@ int check_nt(const char* who, int M, int N, int K) {
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// Whether the routed q4_K experts take the fused kernel in one launch (one group
+// per expert, no split-K: K <= kAccChunkFrom); otherwise they are staged in fp16
+// like the other types.
+bool grouped_q4k_fused(const int* qt, const int* offs, int n_experts, int N, int K) {
+  std::vector<int> rows;
+  for (int e = 0; e < n_experts; ++e)
+    if (offs[e + 1] > offs[e] && qt[e] == TIERMM_Q4_K) rows.push_back(offs[e + 1] - offs[e]);
+  return rows.empty() || qgemm_q4k_fusable(rows.data(), (int)rows.size(), N, K, false);
+}
 
 // Routed experts through the grouped 256x320 launch: the number of experts whose
 // fp16 weights are decoded at once (at most 64 and 1 GiB), or 0 when the experts'
@@ -944,8 +999,8 @@ size_t tiermm_qgemm_ws_bytes(int qtype, int M, int N, int K, int mode) {
     return al256((size_t)N * K * 4) + 2 * al256((size_t)N * K * 2) + al256((size_t)N * 4) +
            2 * al256((size_t)M * K * 2) + al256((size_t)M * 4);
   const size_t parts = (size_t)3 * M * K * sizeof(uint16_t);  // x split in three fp16 planes
-  if (qtype == TIERMM_Q4_K && big_tiles(M, N) < 192)  // W decoded inside the GEMM; split-K partial sums
-    return al256(parts) + qgemm_q4k_partials_bytes(M, N, K);
+  if (qtype == TIERMM_Q4_K && big_tiles(M, N) < 192 && qgemm_q4k_fusable(&M, 1, N, K, true))
+    return al256(parts) + qgemm_q4k_partials_bytes(M, N, K);  // W decoded inside the GEMM; split-K partial sums
   return (size_t)N * K * sizeof(uint16_t) + parts;                   // W16 staged in the workspace
 }
 
@@ -989,7 +1044,7 @@ int tiermm_qgemm(const void* W, int qtype, size_t rb, const float* X, float* Y, 
     if (big_tiles(M, N) >= 192) return launch_x3_big<X3_2X2>(a, s, who);
     return launch_x3<128, 128, X3_2X2>(a, s, who);
   }
-  if (qtype == TIERMM_Q4_K && big_tiles(M, N) < 192) {  // small M: decode W inside the GEMM
+  if (qtype == TIERMM_Q4_K && big_tiles(M, N) < 192 && qgemm_q4k_fusable(&M, 1, N, K, true)) {  // small M: decode W inside the GEMM
     uint16_t* parts = (uint16_t*)w;
     float* partials = (float*)((uint8_t*)w + al256(3 * mk * sizeof(uint16_t)));
     st = split3_launch(X, parts, mk, mk, TIERMM_HML, s);
@@ -1033,10 +1088,11 @@ size_t tiermm_qgemm_grouped_ws_bytes(const int* qtype_e, const int* expert_offse
   const size_t P = n_experts > 0 ? (size_t)expert_offsets[n_experts] : 0;
   const int chunk = n_experts > 0 ? big_group_chunk(expert_offsets, n_experts, N, K) : 0;
   if (chunk) return al256(3 * P * K * sizeof(uint16_t)) + chunk * al256((size_t)N * K * sizeof(uint16_t));
+  const bool fused = grouped_q4k_fused(qtype_e, expert_offsets, n_experts, N, K);
   bool staged = false;
   for (int e = 0; e < n_experts; ++e) {
     const int Me = expert_offsets[e + 1] - expert_offsets[e];
-    if (Me > 0 && qtype_e[e] != TIERMM_Q4_K) staged = true;
+    if (Me > 0 && (qtype_e[e] != TIERMM_Q4_K || !fused)) staged = true;
   }
   return al256(3 * P * K * sizeof(uint16_t)) + (staged ? (size_t)N * K * sizeof(uint16_t) : 0);
 }
@@ -1133,12 +1189,13 @@ int tiermm_qgemm_grouped(const void* const* W_e, const int* qtype_e, const size_
   st = device_cus(&cus);
   if (st) return st;
   // q4_K experts: one launch (per 64 experts) whose workgroups cover every expert's tiles
+  const bool fused = grouped_q4k_fused(qtype_e, expert_offsets, n_experts, N, K);
   std::vector<const void*> gw;
   std::vector<int> g0, gr;
   size_t grb = 0;
   for (int e = 0; e < n_experts; ++e) {
     const int o = expert_offsets[e], Me = expert_offsets[e + 1] - o;
-    if (Me == 0 || qtype_e[e] != TIERMM_Q4_K) continue;
+    if (Me == 0 || qtype_e[e] != TIERMM_Q4_K || !fused) continue;
     if (grb && rb_e[e] != grb) return set_error(TIERMM_EINVAL, "%s: q4_K experts with different row bytes", who);
     grb = rb_e[e];
     gw.push_back(W_e[e]);
@@ -1153,7 +1210,7 @@ int tiermm_qgemm_grouped(const void* const* W_e, const int* qtype_e, const size_
   // other types: fp16 W staged per expert, then the x3-ref GEMM on the expert's rows
   for (int e = 0; e < n_experts; ++e) {
     const int o = expert_offsets[e], Me = expert_offsets[e + 1] - o;
-    if (Me == 0 || qtype_e[e] == TIERMM_Q4_K) continue;
+    if (Me == 0 || (qtype_e[e] == TIERMM_Q4_K && fused)) continue;
     st = dequant_f16_rows(W_e[e], qtype_e[e], rb_e[e], K, (size_t)N, w16, s);
     if (!st) st = x3ref_nt(parts + (size_t)o * K, pk, w16, K, Y_sorted + (size_t)o * N, N, Me, N, K, 0.f, s, who);
     if (st) return st;

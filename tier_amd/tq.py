@@ -1,110 +1,36 @@
-""".tq quantized-base container: the Python side of tierlm's format.
+""".tq quantized-base container, Python side, over the library's reader and writer.
 
-``write_tq`` and ``info`` keep the interface of quant.py's writer and reader
-(quant.py:60-105 and 314-334: the same item tuples, the same header bytes, the
-same result keys) so tierlm.py code can call them unchanged; ``TqFile`` reads
-a base through the library's parser (tiermm_tq_*, the checks of tq_load,
-tier.cpp:273-292) and hands rows to device memory.
+The container (the engine reads it in tq_load / tq_of, tier.cpp:273-292; the
+engine and quant.py write it, tier.cpp:2716-2744, quant.py:60-105) is a
+NUL-padded text header -- ``TQB1 <hb> <n>``, ``#key value`` meta lines, one
+``name type rows cols offset bytes err`` line per matrix -- followed by the
+matrices at 4096-aligned offsets.  The layout, header and checks live in C
+(``tiermm_tq_write`` / ``tiermm_tq_open``); this module adapts Python callers:
 
-Format: a NUL-padded text header of hb bytes -- ``TQB1 <hb> <n>``, ``#key
-value`` meta lines, one ``name type rows cols offset bytes err`` line per
-matrix -- with hb = ceil((n*200 + 4096) / 4096) * 4096, then the matrices at
-4096-aligned offsets.
+* ``write_tq(out, items, meta)`` and ``info(path)`` take and return what
+  quant.py's functions of the same names do (item tuples with a byte source,
+  the result keys ``мета``, ``матриц``, ``типы``, ``байт``, ``ошибки``), so
+  tierlm.py code can call them unchanged;
+* ``TqFile`` opens a base for lookups by name and row reads;
+* ``check`` is the engine's ``--tq-check`` comparison of a base with its
+  bf16 source model.
 """
 from __future__ import annotations
 
+import collections
 import ctypes
 import os
-import re
 
 import numpy as np
 
-from . import _L, _check, q_info
+from . import _L, _check, q_row_bytes
 
-# block geometry by type name (quant.h:26-30)
-_TYPES = {"F32": 0, "F16": 1, "BF16": 30, "Q4_0": 2, "Q4_1": 3, "Q5_0": 6, "Q5_1": 7, "Q8_0": 8, "Q2_K": 10,
-          "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "IQ4_NL": 20, "IQ4_XS": 23, "TQ1_0": 34, "TQ2_0": 35,
-          "MXFP4": 39, "NF4": 200, "FP4": 201}
-
-
-_NAMES = {v: k for k, v in _TYPES.items()}
-
-
-def _geometry(ty: str):
-    if ty not in _TYPES:
-        raise ValueError(f"unknown type {ty}")
-    return q_info(_TYPES[ty])
-
-
-def write_tq(out: str, items, meta: dict) -> None:
-    """quant.py:60-105: items are (name, type, rows, cols, src); src is a callable returning
-    the matrix bytes or a (file, offset, size) triple to copy from.  Written through
-    ``out + '.part'`` and renamed."""
-    items = list(items)
-    hb = (len(items) * 200 + 4096 + 4095) // 4096 * 4096
-    off, lay = hb, []
-    for nm, ty, rows, cols, src in items:
-        b, by = _geometry(ty)
-        if cols % b:
-            raise ValueError(f"{nm}: {cols} columns are not whole {ty} blocks of {b}")
-        size = cols // b * by * rows
-        lay.append((nm, ty, rows, cols, off, size, src))
-        off += (size + 4095) // 4096 * 4096
-    tmp = out + ".part"
-    with open(tmp, "wb") as f:
-        f.truncate(off)
-        for nm, ty, rows, cols, o, size, src in lay:
-            f.seek(o)
-            if callable(src):
-                data = src()
-                if len(data) != size:
-                    raise ValueError(f"{nm}: {len(data)} bytes given, {size} needed")
-                f.write(data)
-            else:
-                fn, so, sn = src
-                if sn != size:
-                    raise ValueError(f"{nm}: the source holds {sn} bytes, {ty} {rows}x{cols} needs {size}")
-                with open(fn, "rb") as g:
-                    g.seek(so)
-                    left = size
-                    while left:
-                        chunk = g.read(min(left, 64 << 20))
-                        if not chunk:
-                            raise ValueError(f"{nm}: the source ends early")
-                        f.write(chunk)
-                        left -= len(chunk)
-        head = f"TQB1 {hb} {len(lay)}\n" + "".join(f"#{k} {v}\n" for k, v in meta.items())
-        head += "".join(f"{nm} {ty} {rows} {cols} {o} {size} -1\n" for nm, ty, rows, cols, o, size, _ in lay)
-        raw = head.encode()
-        if len(raw) >= hb:
-            raise ValueError("the header does not fit its reserved space")
-        f.seek(0)
-        f.write(raw.ljust(hb, b"\0"))
-    os.replace(tmp, out)
-
-
-def info(path: str) -> dict:
-    """quant.py:314-334: meta, matrix count, types, file size and the per-matrix errors."""
-    with open(path, "rb") as f:
-        first = f.readline().decode()
-        m = re.match(r"^TQB1 (\d+) (\d+)", first)
-        if not m:
-            raise ValueError(f"{path} is not a .tq file")
-        f.seek(0)
-        h = f.read(int(m.group(1))).split(b"\0", 1)[0].decode()
-    meta, mats, types, errs = {}, 0, {}, {}
-    for line in h.splitlines()[1:]:
-        if line.startswith("#"):
-            k, _, v = line[1:].partition(" ")
-            meta[k] = v
-            continue
-        p = line.split()
-        if len(p) >= 6:
-            mats += 1
-            types[p[1]] = types.get(p[1], 0) + 1
-            if len(p) >= 7 and float(p[6]) >= 0:
-                errs[p[0]] = float(p[6])
-    return {"мета": meta, "матриц": mats, "типы": types, "байт": os.path.getsize(path), "ошибки": errs}
+# type names of the container's lines (quant.h:26-30: the ggml ids)
+TYPE_IDS = {"F32": 0, "F16": 1, "Q4_0": 2, "Q4_1": 3, "Q5_0": 6, "Q5_1": 7, "Q8_0": 8, "Q2_K": 10, "Q3_K": 11,
+            "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "IQ2_XXS": 16, "IQ2_XS": 17, "IQ3_XXS": 18, "IQ1_S": 19,
+            "IQ4_NL": 20, "IQ3_S": 21, "IQ2_S": 22, "IQ4_XS": 23, "IQ1_M": 29, "BF16": 30, "TQ1_0": 34,
+            "TQ2_0": 35, "MXFP4": 39, "NF4": 200, "FP4": 201}
+TYPE_NAMES = {v: k for k, v in TYPE_IDS.items()}
 
 
 class TqFile:
@@ -145,9 +71,12 @@ class TqFile:
         off, size, rb, err = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_size_t(), ctypes.c_double()
         _check(_L.tiermm_tq_info(self._h, i, ctypes.byref(nm), ctypes.byref(qt), ctypes.byref(rows), ctypes.byref(cols),
                                  ctypes.byref(off), ctypes.byref(size), ctypes.byref(rb), ctypes.byref(err)))
-        return {"name": nm.value.decode(), "qtype": qt.value, "type": _NAMES.get(qt.value, str(qt.value)),
+        return {"name": nm.value.decode(), "qtype": qt.value, "type": TYPE_NAMES.get(qt.value, str(qt.value)),
                 "rows": rows.value, "cols": cols.value, "offset": off.value, "bytes": size.value, "rb": rb.value,
                 "err": err.value}
+
+    def entries(self) -> list[dict]:
+        return [self.entry(i) for i in range(len(self))]
 
     def meta(self) -> dict:
         out = {}
@@ -167,7 +96,7 @@ class TqFile:
 
 def write_tq_arrays(out: str, mats, meta: dict | None = None, errs=None) -> None:
     """Write (name, qtype id, rows, cols, uint8 array) matrices with the library writer
-    (tiermm_tq_write: the engine's byte layout, errors with 6 decimals)."""
+    (tiermm_tq_write: the engine's byte layout, errors with 6 decimals, "-1" without)."""
     mats = list(mats)
     n = len(mats)
     meta = meta or {}
@@ -183,6 +112,51 @@ def write_tq_arrays(out: str, mats, meta: dict | None = None, errs=None) -> None
     _check(_L.tiermm_tq_write(out.encode(), n, names, qt, rows, cols, data, e, len(meta), keys, vals))
 
 
+def _source(name: str, ty: str, rows: int, cols: int, src) -> tuple[int, np.ndarray]:
+    """(type id, bytes) of one write_tq item: src is a callable returning the matrix bytes, or a
+    (file, offset, size) range of another file, mapped rather than read into memory."""
+    if ty not in TYPE_IDS:
+        raise ValueError(f"{name}: unknown type {ty}")
+    qt = TYPE_IDS[ty]
+    try:
+        need = q_row_bytes(qt, cols) * rows
+    except Exception as e:
+        raise ValueError(f"{name}: {cols} columns are not whole {ty} blocks") from e
+    if callable(src):
+        data = src()
+        if len(data) != need:
+            raise ValueError(f"{name}: {len(data)} bytes given, {ty} {rows}x{cols} takes {need}")
+        return qt, np.frombuffer(data, np.uint8)
+    path, offset, size = src
+    if size != need:
+        raise ValueError(f"{name}: the source range holds {size} bytes, {ty} {rows}x{cols} takes {need}")
+    if need == 0:
+        return qt, np.zeros(0, np.uint8)
+    if os.path.getsize(path) < offset + size:
+        raise ValueError(f"{name}: {path} ends before byte {offset + size}")
+    return qt, np.memmap(path, np.uint8, mode="r", offset=offset, shape=(size,))
+
+
+def write_tq(out: str, items, meta: dict) -> None:
+    """quant.py:60-105's writer: items are (name, type name, rows, cols, src) with src as in
+    _source; meta goes to the #key lines.  Written through out + '.part' and renamed, by
+    tiermm_tq_write."""
+    mats = []
+    for name, ty, rows, cols, src in items:
+        qt, data = _source(name, ty, rows, cols, src)
+        mats.append((name, qt, rows, cols, data))
+    write_tq_arrays(out, mats, meta)
+
+
+def info(path: str) -> dict:
+    """quant.py:314-334's summary of a base: its meta, matrix count, count per type, file size
+    and the recorded per-matrix errors (those >= 0), read through tiermm_tq_open."""
+    with TqFile(path) as f:
+        meta, ents = f.meta(), f.entries()
+    return {"мета": meta, "матриц": len(ents), "типы": dict(collections.Counter(e["type"] for e in ents)),
+            "байт": os.path.getsize(path), "ошибки": {e["name"]: e["err"] for e in ents if e["err"] >= 0}}
+
+
 def _safetensors_index(path: str) -> tuple[dict, int]:
     """Tensor table of a safetensors file: {name: (dtype, shape, begin, end)}, data start."""
     import json
@@ -195,52 +169,62 @@ def _safetensors_index(path: str) -> tuple[dict, int]:
     return tab, 8 + n
 
 
+def _sampled_rows(rows: int) -> list[int]:
+    """The rows the engine compares: at most 48, spread evenly from the first to the last."""
+    s = min(rows, 48)
+    return [j * (rows - 1) // max(1, s - 1) for j in range(s)]
+
+
+def _agreement(x: np.ndarray, y: np.ndarray) -> tuple[float, float, float]:
+    """Squared error, squared source norm and Pearson correlation of two sample matrices
+    (fp64; the correlation is 0 when either side is constant)."""
+    d = y - x
+    se, ss = float(np.sum(d * d)), float(np.sum(x * x))
+    n = x.size
+    cx, cy = x - x.sum() / n, y - y.sum() / n
+    vx, vy = float(np.sum(cx * cx)), float(np.sum(cy * cy))
+    cr = float(np.sum(cx * cy)) / (vx * vy) ** 0.5 if vx > 0 and vy > 0 else 0.0
+    return se, ss, cr
+
+
 def check(model: str, base: str, say=print) -> int:
-    """tier --tq-check (tier.cpp:2749-2765): for every matrix of the base (by name order),
-    up to 48 rows spread evenly over the matrix are dequantized (q_val) and compared with the
-    bf16 source tensor: relative error and correlation per matrix, then the total error and
-    the worst correlation.  Returns 2 when a matrix is missing from the model, has another
-    shape, or correlates below 0.5 (a base of another model), else 0.  The last line keeps
-    the engine's wording, which quant.py's check (quant.py:337-358) parses."""
+    """tier --tq-check (tier.cpp:2749-2765): each matrix of the base (in name order) against the
+    bf16 tensor of the same name in the source model, on the sampled rows: relative error and
+    correlation per matrix, then the total relative error and the worst correlation.  Returns 2
+    when a matrix is missing from the model or has another shape, or correlates below 0.5 (a
+    base of another model), else 0.  The printed lines keep the engine's wording; quant.py
+    (quant.py:337-358) parses the last one."""
     from . import dequant_host
     tab, data0 = _safetensors_index(model)
-    SE = SS = 0.0
-    worst, wname, bad = 1.0, "", 0
     with TqFile(base) as f, open(model, "rb") as src:
-        entries = sorted((f.entry(i) for i in range(len(f))), key=lambda e: e["name"].encode())
-        for k, e in enumerate(entries, 1):
+        ents = sorted(f.entries(), key=lambda e: e["name"].encode())
+        total_se = total_ss = 0.0
+        worst, worst_name, bad = 1.0, "", 0
+        for k, e in enumerate(ents, 1):
+            head = f"Сверка {k}/{len(ents)} {e['name']}"
             t = tab.get(e["name"])
-            cols_ok = t is not None and (len(t[1]) < 2 or t[1][-1] == e["cols"])
-            if t is None or t[3] - t[2] != e["rows"] * e["cols"] * 2 or not cols_ok:
-                say(f"Сверка {k}/{len(entries)} {e['name']}: в модели нет такой матрицы или у неё другая форма.")
+            if (t is None or t[3] - t[2] != e["rows"] * e["cols"] * 2
+                    or (len(t[1]) >= 2 and t[1][-1] != e["cols"])):
+                say(f"{head}: в модели нет такой матрицы или у неё другая форма.")
                 bad += 1
                 continue
-            S = min(e["rows"], 48)
-            rows = [j * (e["rows"] - 1) // max(1, S - 1) for j in range(S)]
-            se = ss = sx = sy = sxy = sxx = syy = 0.0
-            n = 0
+            rows = _sampled_rows(e["rows"])
             i = f.find(e["name"])
+            xs, ys = [], []
             for r in rows:
                 src.seek(data0 + t[2] + r * e["cols"] * 2)
-                raw = np.frombuffer(src.read(e["cols"] * 2), np.uint16)
-                x = (raw.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
-                y = dequant_host(f.read_rows(i, r, 1), e["qtype"], e["cols"])[0].astype(np.float64)
-                d = y - x
-                se += float(d @ d); ss += float(x @ x); sx += float(x.sum()); sy += float(y.sum())
-                sxy += float(x @ y); sxx += float(x @ x); syy += float(y @ y)
-                n += x.size
-            cov, vx, vy = sxy - sx * sy / n, sxx - sx * sx / n, syy - sy * sy / n
-            cr = cov / (vx * vy) ** 0.5 if vx > 0 and vy > 0 else 0.0
-            er = (se / ss) ** 0.5 if ss > 0 else 0.0
-            SE += se
-            SS += ss
+                xs.append(np.frombuffer(src.read(e["cols"] * 2), np.uint16))
+                ys.append(dequant_host(f.read_rows(i, r, 1), e["qtype"], e["cols"])[0])
+            x = (np.stack(xs).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+            se, ss, cr = _agreement(x, np.stack(ys).astype(np.float64))
+            total_se += se
+            total_ss += ss
             if cr < worst:
-                worst, wname = cr, e["name"]
-            if cr < 0.5:
-                bad += 1
-            say(f"Сверка {k}/{len(entries)} {e['name']} {e['type']}, ошибка {100 * er:.2f}%, "
-                f"корреляция {cr:.4f}")
-    total = 100 * (SE / SS) ** 0.5 if SS > 0 else 0.0
-    say(f"Итог: ошибка весов {total:.2f}%, худшая корреляция {worst:.4f} ({wname})"
+                worst, worst_name = cr, e["name"]
+            bad += cr < 0.5
+            rel = (se / ss) ** 0.5 if ss > 0 else 0.0
+            say(f"{head} {e['type']}, ошибка {100 * rel:.2f}%, корреляция {cr:.4f}")
+    total = 100 * (total_se / total_ss) ** 0.5 if total_ss > 0 else 0.0
+    say(f"Итог: ошибка весов {total:.2f}%, худшая корреляция {worst:.4f} ({worst_name})"
         f"{', обнаружены матрицы от другой модели' if bad else ''}")
     return 2 if bad else 0
