@@ -180,6 +180,19 @@ size_t tiermm_x3_rows_ws_bytes(int M, int K, int N);
 int tiermm_x3_rows_bf16(const uint16_t* W, const float* x, float* y, int M, int K, int N, int ldo,
                         void* ws, size_t ws_bytes, tiermm_stream_t stream);
 
+/* No counterpart in the reference: tiermm_x3_rows for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same product, kernels and accuracy; no
+ * workspace argument and no allocation on any call: the three fp16 planes of x
+ * live in a static device scratch of TIERMM_NOALLOC_SCRATCH_BYTES per GPU, held
+ * until the process ends (its device address is looked up by tiermm_init, or by
+ * the first call on a device).  TIERMM_UNSUPPORTED when 3 * M * K * 2 bytes
+ * exceed it, or K is not a multiple of 32.  Calls that overlap on one GPU share
+ * the scratch and race: order them on one stream. */
+#define TIERMM_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int tiermm_x3_rows_noalloc(const uint16_t* W, const float* x, float* y, int M, int K, int N, int ldo,
+                           tiermm_stream_t stream);
+
 /* ------------------------------------------------------------ x3-2x2 GEMM */
 /* Two-part split with a power-of-two exponent per row (the storage of the 2x2
  * x3 GEMM; README.md:21 describes it, no reference function exists):

@@ -58,7 +58,7 @@ EXPORTS = (
     "tiermm_tq_count", "tiermm_tq_find", "tiermm_tq_info", "tiermm_tq_meta_count", "tiermm_tq_meta",
     "tiermm_tq_read_rows", "tiermm_tq_write", "tiermm_dequant_host", "tiermm_chat_create", "tiermm_chat_destroy",
     "tiermm_chat_add", "tiermm_chat_place", "tiermm_chat_lin", "tiermm_chat_restart", "tiermm_chat_info",
-    "tiermm_host_alloc", "tiermm_host_free",
+    "tiermm_host_alloc", "tiermm_host_free", "tiermm_x3_rows_noalloc",
 )
 
 
@@ -137,6 +137,17 @@ _sig("tiermm_chat_restart", [_vp, _i])
 _sig("tiermm_chat_info", [_vp, _i, _pi, ctypes.POINTER(_sz), ctypes.POINTER(_sz), ctypes.POINTER(ctypes.c_longlong)])
 _sig("tiermm_host_alloc", [_sz, ctypes.POINTER(_vp)])
 _sig("tiermm_host_free", [_vp])
+_sig("tiermm_x3_rows_noalloc", [_vp, _vp, _vp, _i, _i, _i, _i, _vp])
+NOALLOC_SCRATCH_BYTES = 32 << 20  # TIERMM_NOALLOC_SCRATCH_BYTES
+
+
+def chat_fp3_noalloc(W: int, x: int, y: int, M: int, K: int, N: int, ldo: int, stream=None) -> bool:
+    """chat_fp3 without any device allocation (static scratch): False when x does not fit it."""
+    code = _L.tiermm_x3_rows_noalloc(W, x, y, M, K, N, ldo, _s(stream))
+    if code == UNSUPPORTED:
+        return False
+    _check(code)
+    return True
 
 
 def lib():

@@ -130,7 +130,7 @@ int tiermm_init(int device) {
   if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
     return set_error(TIERMM_UNSUPPORTED, "tiermm_init: device %d is %s; this library is built for gfx950", device,
                      prop.gcnArchName);
-  return TIERMM_OK;
+  return noalloc_scratch_init();  // the device address of tiermm_x3_rows_noalloc's scratch
 }
 
 void tiermm_shutdown(void) {

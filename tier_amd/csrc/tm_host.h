@@ -35,4 +35,8 @@ int get_workspace(void* ws, size_t ws_bytes, size_t need, void** out, const char
 
 int quantize_rows(int qtype, const float* x, void* out, size_t rows, int cols, int nthreads);
 
+// Device address of tiermm_x3_rows_noalloc's static scratch on the current device,
+// looked up once per device (x3.hip).
+int noalloc_scratch_init();
+
 }  // namespace tiermm
