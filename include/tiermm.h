@@ -335,6 +335,26 @@ int tiermm_chat_place(tiermm_chat* c, size_t budget, size_t reserve, size_t* res
  * device fp32, x 16-byte aligned.  A streamed matrix waits for its copy and
  * then refills its slot with the use nslots ahead (tier.cpp:2377). */
 int tiermm_chat_lin(tiermm_chat* c, int id, const float* x, float* y, int M, int mode);
+/* Trained rows over matrix id's output (chat_heads, tier.cpp:2339-2350; set up at
+ * tier.cpp:2514-2526): after the base product, hr rows of htype (TIERMM_F16 or
+ * TIERMM_BF16, the engine's storage type) at hd -- device memory, 16-byte aligned,
+ * [hr][cols], kept by the caller -- replace output rows ri[j] (a device int array
+ * of hr row indices), or rows 0..hr-1 when ri is NULL.  They are computed as
+ * gemv<T> at M = 1 and with fp32 semantics (expand + SGEMM) above.  hr = 0 or
+ * hd = NULL removes them. */
+int tiermm_chat_set_heads(tiermm_chat* c, int id, int hr, int htype, const void* hd, const int* ri);
+/* Apply the trained rows (on != 0, the default) or not: the engine's g_chat_heads,
+ * switched with the trained/base mode (tier.cpp:2338, 2669). */
+int tiermm_chat_heads(tiermm_chat* c, int on);
+/* LoRA adapter of matrix id (chat_lora, tier.cpp:2333-2337; loaded at 2420-2429,
+ * 2476-2477): after the base product and the trained rows, y += s * (x A^T) B^T
+ * with A [r][cols] and B [rows][r] fp32 device arrays kept by the caller, both
+ * products fp32-accurate.  r = 0 or a NULL array removes it. */
+int tiermm_chat_set_lora(tiermm_chat* c, int id, int r, const float* A, const float* B);
+/* The adapters' scale s = on ? k * alpha / r : 0 (g_chat_lalpha, g_chat_lk and
+ * g_chat_lon, tier.cpp:2332, 2651, 2668); s == 0 skips them.  Defaults: alpha 0
+ * (adapters off until set), k 1, on. */
+int tiermm_chat_lora_scale(tiermm_chat* c, float alpha, float k, int on);
 /* After the host rows of streamed matrices changed (or to rewind the cyclic
  * order, rewind != 0): wait for the set's streams and issue the pending copies
  * again (the engine's chat_issue(qi), chat_issue(qi+1), tier.cpp:2666-2676). */

@@ -103,11 +103,14 @@ def test_argument_checks_return_before_device_work():
     assert L.tiermm_x3s_gemm(16, 16, 16, 16, 16, 16, 16, 4, 4, 48, 4, None) == tier_amd.UNSUPPORTED
     assert L.tiermm_split3_f16(16, 16, 10, 5, 0, None) == tier_amd.EINVAL
     assert "part_stride" in tier_amd.last_error()
-    # chat_fp3 mirror: unsupported shape -> False, not an exception
-    assert tier_amd.chat_fp3(16, 16, 16, 4, 48, 4, 4) is False
-    # legacy 32-blocks and dense rows are GPU types now; dense rows decode 8 columns at a time
+    # chat_fp3 mirrors: an unsupported shape -> False, not an exception (the allocation-free
+    # variant keeps K a multiple of 32: it has no workspace to pad into)
+    assert tier_amd.chat_fp3_noalloc(16, 16, 16, 4, 48, 4, 4) is False
+    # legacy 32-blocks and dense rows are GPU types now; dense rows of any length, written
+    # element by element to an output of their natural alignment
     assert L.tiermm_dequant(16, tier_amd.Q4_1, 19, 32, 0, 1, 16, tier_amd.OUT_F16, None) == tier_amd.EINVAL
-    assert L.tiermm_dequant(16, tier_amd.F16, 24, 12, 0, 1, 16, tier_amd.OUT_F16, None) == tier_amd.UNSUPPORTED
+    assert L.tiermm_dequant(16, tier_amd.F16, 24, 12, 0, 1, 17, tier_amd.OUT_F16, None) == tier_amd.EINVAL
+    assert "2-byte aligned" in tier_amd.last_error()
     assert L.tiermm_qgemv(18, tier_amd.F16, 128, 16, 16, 1, 64, None) == tier_amd.EINVAL  # dense rows 16-aligned
     # chat set: slot count, null handles, registration checks (no HIP call on these paths)
     out = ctypes.c_void_p()

@@ -226,3 +226,60 @@ def test_caller_resident_rows(gpu):
     y = Y.download(np.float32, N)
     assert oracle.rel_fro(y, oracle.gemv_f64(rows, t, np.arange(K, dtype=np.float32) / K, N, K)) <= 1e-5
     assert W.download(np.uint8, rows.size).tobytes() == rows.tobytes()
+
+
+@pytest.mark.parametrize("M", [1, 48])
+@pytest.mark.parametrize("streamed", [False, True])
+def test_trained_rows_and_lora(gpu, M, streamed):
+    """chat_lin's additions after the base product (tier.cpp:2375-2376): trained fp16 rows over
+    chosen output rows (chat_heads with a row index, 2339-2343) and over the first rows (no
+    index, 2344-2350), then a LoRA adapter's s (x A^T) B^T (chat_lora, 2333-2337); switched off
+    by the trained/base mode (g_chat_heads, g_chat_lon, 2668-2669).  fp64 references; bars:
+    1e-5 at M = 1 (gemv_q / gemv<T>), 2^-20 at M = 48 (fp32 semantics)."""
+    t, N, K, r, hr = tier_amd.Q4_K, 300, 512, 8, 40
+    rows = quantized_weight(t, N, K, seed=41)
+    mats = [(t, N, K, rows), (t, N, K, rows)]
+    rig = Rig(mats, M, 2, budget=0 if streamed else None)
+    rng = np.random.default_rng(42)
+    hd = oracle.f2h((rng.standard_normal((2, hr, K)) * 0.02).astype(np.float32)).reshape(2, hr, K)
+    hdf = oracle.h2f_array(hd).astype(np.float64)
+    ri = rng.choice(N, hr, replace=False).astype(np.int32)
+    A = (rng.standard_normal((r, K)) * 0.05).astype(np.float32)
+    B = (rng.standard_normal((N, r)) * 0.05).astype(np.float32)
+    HD, RI, DA, DB = hip.to_device(hd), hip.to_device(ri), hip.to_device(A), hip.to_device(B)
+    try:
+        # matrix 0: trained rows at ri; matrix 1: the first hr rows; both with the adapter
+        rig.chat.set_heads(rig.ids[0], hr, tier_amd.F16, HD.ptr, RI.ptr)
+        rig.chat.set_heads(rig.ids[1], hr, tier_amd.F16, HD.ptr + hr * K * 2, None)
+        for i in rig.ids:
+            rig.chat.set_lora(i, r, DA.ptr, DB.ptr)
+        alpha, k = 16.0, 0.5
+        s = k * alpha / r
+        wf = oracle.dequant(rows, t, K).astype(np.float64)
+        bar = 1e-5 if M == 1 else 2.0 ** -20
+
+        def want(i, heads, lora):
+            x = rig.x[i].astype(np.float64)
+            y = x @ wf.T
+            if heads:
+                cols = ri if i == 0 else np.arange(hr)
+                y[:, cols] = x @ hdf[i].T
+            if lora:
+                y += s * (x @ A.astype(np.float64).T) @ B.astype(np.float64).T
+            return y
+
+        for heads, lora_on in ((True, True), (False, True), (True, False)):
+            rig.chat.heads(heads)
+            rig.chat.lora_scale(alpha, k, lora_on)
+            got = rig.run()
+            for i in range(2):
+                g = got[i].reshape(M, N)
+                assert oracle.rel_fro(g, want(i, heads, lora_on)) <= bar, (heads, lora_on, i)
+        # alpha 0 (the default before an adapter is loaded) leaves the base product alone
+        rig.chat.heads(False)
+        rig.chat.lora_scale(0.0)
+        got = rig.run()
+        for i in range(2):
+            assert _same(got[i], rig.direct(i)), i
+    finally:
+        rig.close()

@@ -58,7 +58,8 @@ EXPORTS = (
     "tiermm_tq_count", "tiermm_tq_find", "tiermm_tq_info", "tiermm_tq_meta_count", "tiermm_tq_meta",
     "tiermm_tq_read_rows", "tiermm_tq_write", "tiermm_dequant_host", "tiermm_chat_create", "tiermm_chat_destroy",
     "tiermm_chat_add", "tiermm_chat_place", "tiermm_chat_lin", "tiermm_chat_restart", "tiermm_chat_info",
-    "tiermm_host_alloc", "tiermm_host_free", "tiermm_x3_rows_noalloc",
+    "tiermm_host_alloc", "tiermm_host_free", "tiermm_x3_rows_noalloc", "tiermm_chat_set_heads",
+    "tiermm_chat_heads", "tiermm_chat_set_lora", "tiermm_chat_lora_scale",
 )
 
 
@@ -135,6 +136,10 @@ _sig("tiermm_chat_place", [_vp, _sz, _sz, ctypes.POINTER(_sz), ctypes.POINTER(_s
 _sig("tiermm_chat_lin", [_vp, _i, _vp, _vp, _i, _i])
 _sig("tiermm_chat_restart", [_vp, _i])
 _sig("tiermm_chat_info", [_vp, _i, _pi, ctypes.POINTER(_sz), ctypes.POINTER(_sz), ctypes.POINTER(ctypes.c_longlong)])
+_sig("tiermm_chat_set_heads", [_vp, _i, _i, _i, _vp, _vp])
+_sig("tiermm_chat_heads", [_vp, _i])
+_sig("tiermm_chat_set_lora", [_vp, _i, _i, _vp, _vp])
+_sig("tiermm_chat_lora_scale", [_vp, _f, _f, _i])
 _sig("tiermm_host_alloc", [_sz, ctypes.POINTER(_vp)])
 _sig("tiermm_host_free", [_vp])
 _sig("tiermm_x3_rows_noalloc", [_vp, _vp, _vp, _i, _i, _i, _i, _vp])
@@ -423,6 +428,21 @@ class Chat:
 
     def restart(self, rewind: bool = False) -> None:
         _check(_L.tiermm_chat_restart(self._h, int(rewind)))
+
+    def set_heads(self, i: int, hr: int, htype: int, hd: int | None, ri: int | None = None) -> None:
+        """chat_heads (tier.cpp:2339-2350): hr trained rows (device, F16 or BF16) over output
+        rows ri (device int array) or rows 0..hr-1."""
+        _check(_L.tiermm_chat_set_heads(self._h, i, hr, htype, hd, ri))
+
+    def heads(self, on: bool) -> None:
+        _check(_L.tiermm_chat_heads(self._h, int(on)))
+
+    def set_lora(self, i: int, r: int, A: int | None, B: int | None) -> None:
+        """chat_lora (tier.cpp:2333-2337): y += s (x A^T) B^T, A [r][cols], B [rows][r] fp32."""
+        _check(_L.tiermm_chat_set_lora(self._h, i, r, A, B))
+
+    def lora_scale(self, alpha: float, k: float = 1.0, on: bool = True) -> None:
+        _check(_L.tiermm_chat_lora_scale(self._h, alpha, k, int(on)))
 
     def info(self, i: int = -1) -> dict:
         st, r, s, u = _i(), _sz(), _sz(), ctypes.c_longlong()

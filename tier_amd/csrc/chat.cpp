@@ -12,6 +12,10 @@
 // resident while it fits beside the reserve, and every matrix after the first
 // one that does not fit is streamed.
 //
+// After the base product a matrix may get the engine's two additions: trained
+// rows written over their rows of the output (chat_heads, tier.cpp:2339-2350)
+// and a LoRA adapter's s * (x A^T) B^T (chat_lora, tier.cpp:2333-2337).
+//
 // Differences from the engine, on purpose: the number of slots is a parameter
 // (2 in the engine); a streamed matrix used out of the cyclic order is refused
 // instead of computing with another matrix's rows; streamed host memory must be
@@ -25,6 +29,8 @@
 
 namespace tiermm {
 bool gpu_type(int qtype);
+int chat_scatter_cols(const float* src, float* y, const int* idx, int M, int r, int ld, hipStream_t s);
+int chat_scale(float* u, size_t n, float f, hipStream_t s);
 }
 
 using namespace tiermm;
@@ -38,6 +44,16 @@ struct tiermm_chat {
     const void* host;  // host rows (the streaming source), may be null for caller-resident rows
     void* dev;         // device rows; null while the matrix is streamed or not yet placed
     bool owned;        // dev was allocated by tiermm_chat_place
+    // trained rows (chat_heads, tier.cpp:2339-2350): hr rows of htype at hd replace
+    // output rows ri[j] (rows 0..hr-1 without ri); caller-owned device memory
+    int hr = 0, htype = 0;
+    const void* hd = nullptr;
+    const int* ri = nullptr;
+    // LoRA adapter (chat_lora, tier.cpp:2333-2337): y += s * (x A^T) B^T, A [lr][cols],
+    // B [rows][lr] fp32, caller-owned device memory
+    int lr = 0;
+    const float* la = nullptr;
+    const float* lb = nullptr;
   };
   int device = 0;
   int nslots = 2;
@@ -50,6 +66,13 @@ struct tiermm_chat {
   long long qi = 0;  // uses of streamed matrices so far
   bool placed = false;
   size_t resident = 0, streamed = 0;
+  bool heads_on = true;                   // g_chat_heads (tier.cpp:2338)
+  float lora_alpha = 0.f, lora_k = 1.f;   // g_chat_lalpha, g_chat_lk (tier.cpp:2332)
+  bool lora_on = true;                    // g_chat_lon
+  float* htmp = nullptr;                  // trained rows' outputs before the scatter
+  size_t htmp_n = 0;
+  float* lu = nullptr;                    // x A^T of the LoRA adapter
+  size_t lu_n = 0;
 };
 
 namespace {
@@ -91,6 +114,8 @@ void release(tiermm_chat* c) {
     if (m.owned && m.dev) (void)hipFree(m.dev);
   for (void* p : c->slot)
     if (p) (void)hipFree(p);
+  if (c->htmp) (void)hipFree(c->htmp);
+  if (c->lu) (void)hipFree(c->lu);
   for (auto e : c->ev_cp)
     if (e) (void)hipEventDestroy(e);
   for (auto e : c->ev_done)
@@ -116,6 +141,64 @@ int compute(const tiermm_chat::Mat& m, const void* W, const float* x, float* y, 
   // fp32 fallback of the dense types (expand + SGEMM, tier.cpp:2372-2374)
   const int md = dense(m.qtype) ? TIERMM_MODE_F32 : mode;
   return tiermm_qgemm(W, m.qtype, m.rb, x, y, M, m.rows, m.cols, m.rows, md, 0.f, nullptr, 0, st);
+}
+
+// A float buffer of at least n elements on the set's device, grown as the
+// engine's g_chat_htmp / g_chat_lu are (tier.cpp:2335, 2341); the old one may
+// still be read by queued work, so the stream is drained before it is freed.
+int grow(tiermm_chat* c, float*& buf, size_t& have, size_t n, const char* who) {
+  if (n <= have) return TIERMM_OK;
+  hipError_t e = hipSuccess;
+  if (buf) {
+    e = hipStreamSynchronize(c->cs);
+    if (e == hipSuccess) e = hipFree(buf);
+    buf = nullptr;
+    have = 0;
+    if (e != hipSuccess) return hip_fail(e, who);
+  }
+  e = hipMalloc(&buf, n * sizeof(float));
+  if (e != hipSuccess) {
+    buf = nullptr;
+    return hip_fail(e, who);
+  }
+  have = n;
+  return TIERMM_OK;
+}
+
+// chat_heads (tier.cpp:2339-2350): the trained rows' product -- gemv<T> at M = 1,
+// the fp32 expand + SGEMM semantics above -- written over their rows of y.
+int apply_heads(tiermm_chat* c, const tiermm_chat::Mat& m, const float* x, float* y, int M) {
+  const char* who = "tiermm_chat_lin: trained rows";
+  const tiermm_stream_t st = (tiermm_stream_t)c->cs;
+  float* dst = y;
+  int ld = m.rows;
+  if (m.ri) {
+    const int r = grow(c, c->htmp, c->htmp_n, (size_t)M * m.hr, who);
+    if (r) return r;
+    dst = c->htmp;
+    ld = m.hr;
+  }
+  int r = M == 1 ? tiermm_gemv(m.hd, m.htype, x, dst, m.hr, m.cols, st)
+                 : tiermm_qgemm(m.hd, m.htype, (size_t)m.cols * 2, x, dst, M, m.hr, m.cols, ld, TIERMM_MODE_F32, 0.f,
+                                nullptr, 0, st);
+  if (r || !m.ri) return r;
+  return chat_scatter_cols(c->htmp, y, m.ri, M, m.hr, m.rows, c->cs);
+}
+
+// chat_lora (tier.cpp:2333-2337): y += s * (x A^T) B^T with s = k * alpha / r while the
+// adapter is on (0 skips it), both products fp32-accurate (TIERMM_MODE_F32).
+int apply_lora(tiermm_chat* c, const tiermm_chat::Mat& m, const float* x, float* y, int M) {
+  const float s = c->lora_on ? c->lora_k * c->lora_alpha / (float)m.lr : 0.f;
+  if (s == 0.f) return TIERMM_OK;
+  const char* who = "tiermm_chat_lin: lora";
+  const tiermm_stream_t st = (tiermm_stream_t)c->cs;
+  int r = grow(c, c->lu, c->lu_n, (size_t)M * m.lr, who);
+  if (!r) r = tiermm_qgemm(m.la, QT_F32, (size_t)m.cols * 4, x, c->lu, M, m.lr, m.cols, m.lr, TIERMM_MODE_F32, 0.f,
+                           nullptr, 0, st);
+  if (!r) r = chat_scale(c->lu, (size_t)M * m.lr, s, c->cs);
+  if (!r) r = tiermm_qgemm(m.lb, QT_F32, (size_t)m.lr * 4, c->lu, y, M, m.rows, m.lr, m.rows, TIERMM_MODE_F32, 1.f,
+                           nullptr, 0, st);
+  return r;
 }
 
 }  // namespace
@@ -275,6 +358,8 @@ int tiermm_chat_lin(tiermm_chat* c, int id, const float* x, float* y, int M, int
     W = c->slot[(size_t)(my % c->nslots)];
   }
   st = compute(m, W, x, y, M, mode, c->cs);
+  if (!st && m.hr && c->heads_on) st = apply_heads(c, m, x, y, M);  // tier.cpp:2375
+  if (!st && m.lr) st = apply_lora(c, m, x, y, M);                   // tier.cpp:2376
   if (my >= 0) {  // release the slot and refill it with the use nslots ahead (tier.cpp:2377)
     hipError_t e = hipEventRecord(c->ev_done[(size_t)(my % c->nslots)], c->cs);
     const int r = e == hipSuccess ? issue(c, my + c->nslots) : hip_fail(e, who);
@@ -305,6 +390,57 @@ int tiermm_chat_info(const tiermm_chat* c, int id, int* streamed, size_t* reside
   if (resident_bytes) *resident_bytes = c->resident;
   if (streamed_bytes) *streamed_bytes = c->streamed;
   if (uses) *uses = c->qi;
+  return TIERMM_OK;
+}
+
+int tiermm_chat_set_heads(tiermm_chat* c, int id, int hr, int htype, const void* hd, const int* ri) {
+  const char* who = "tiermm_chat_set_heads";
+  if (!c || id < 0 || id >= (int)c->mats.size()) return set_error(TIERMM_EINVAL, "%s: matrix %d", who, id);
+  auto& m = c->mats[(size_t)id];
+  if (hr == 0 || !hd) {
+    m.hr = 0;
+    m.hd = nullptr;
+    m.ri = nullptr;
+    return TIERMM_OK;
+  }
+  if (hr < 0 || hr > m.rows) return set_error(TIERMM_EINVAL, "%s: %d rows of %d", who, hr, m.rows);
+  if (htype != QT_F16 && htype != QT_BF16) return set_error(TIERMM_EINVAL, "%s: row type %d (F16 or BF16)", who, htype);
+  if ((uintptr_t)hd % 16) return set_error(TIERMM_EINVAL, "%s: rows must be 16-byte aligned", who);
+  m.hr = hr;
+  m.htype = htype;
+  m.hd = hd;
+  m.ri = ri;
+  return TIERMM_OK;
+}
+
+int tiermm_chat_heads(tiermm_chat* c, int on) {
+  if (!c) return set_error(TIERMM_EINVAL, "tiermm_chat_heads: null set");
+  c->heads_on = on != 0;
+  return TIERMM_OK;
+}
+
+int tiermm_chat_set_lora(tiermm_chat* c, int id, int r, const float* A, const float* B) {
+  const char* who = "tiermm_chat_set_lora";
+  if (!c || id < 0 || id >= (int)c->mats.size()) return set_error(TIERMM_EINVAL, "%s: matrix %d", who, id);
+  auto& m = c->mats[(size_t)id];
+  if (r == 0 || !A || !B) {
+    m.lr = 0;
+    m.la = m.lb = nullptr;
+    return TIERMM_OK;
+  }
+  if (r < 0) return set_error(TIERMM_EINVAL, "%s: rank %d", who, r);
+  if (((uintptr_t)A | (uintptr_t)B) % 4) return set_error(TIERMM_EINVAL, "%s: A and B must be 4-byte aligned", who);
+  m.lr = r;
+  m.la = A;
+  m.lb = B;
+  return TIERMM_OK;
+}
+
+int tiermm_chat_lora_scale(tiermm_chat* c, float alpha, float k, int on) {
+  if (!c) return set_error(TIERMM_EINVAL, "tiermm_chat_lora_scale: null set");
+  c->lora_alpha = alpha;
+  c->lora_k = k;
+  c->lora_on = on != 0;
   return TIERMM_OK;
 }
 

@@ -61,6 +61,45 @@ int launch_dequant(const void* W, size_t rb, int cols, size_t r0, size_t nrows, 
   return TIERMM_OK;
 }
 
+// Dense rows (F32 / F16 / BF16) one element per thread: out[i] = T(q_val(row, col)),
+// i < n = nrows * cols, for row lengths that are not whole 8-element chunks.
+template <int QT, int OUT>
+__global__ __launch_bounds__(256) void dequant_elem_kernel(const uint8_t* __restrict__ W, size_t rb, int cols,
+                                                           size_t r0, size_t n, void* __restrict__ out) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const size_t row = i / (size_t)cols;
+    const float v = dense_val<QT>(W + (r0 + row) * rb, i - row * (size_t)cols);
+    if (OUT == TIERMM_OUT_F32) ((float*)out)[i] = v;
+    else ((uint16_t*)out)[i] = OUT == TIERMM_OUT_F16 ? f2h(v) : f2bf(v);
+  }
+}
+
+template <int QT>
+int launch_dequant_elems(const void* W, size_t rb, int cols, size_t r0, size_t nrows, void* out, int out_dtype,
+                         hipStream_t s) {
+  const size_t n = nrows * (size_t)cols;
+  if (n == 0) return TIERMM_OK;
+  const size_t want = (n + 255) / 256;
+  const unsigned grid = (unsigned)(want < 65536 ? want : 65536);
+  const uint8_t* w = (const uint8_t*)W;
+  switch (out_dtype) {
+    case TIERMM_OUT_F32: dequant_elem_kernel<QT, TIERMM_OUT_F32><<<grid, 256, 0, s>>>(w, rb, cols, r0, n, out); break;
+    case TIERMM_OUT_F16: dequant_elem_kernel<QT, TIERMM_OUT_F16><<<grid, 256, 0, s>>>(w, rb, cols, r0, n, out); break;
+    default: dequant_elem_kernel<QT, TIERMM_OUT_BF16><<<grid, 256, 0, s>>>(w, rb, cols, r0, n, out); break;
+  }
+  TM_LAUNCH_CHECK("tiermm_dequant: launch");
+  return TIERMM_OK;
+}
+
+// f(std::integral_constant<int, QT>{}) for a dense type F32 / F16 / BF16.
+template <class F>
+auto with_dense(int qtype, F&& f) {
+  if (qtype == QT_F32) return f(std::integral_constant<int, QT_F32>{});
+  if (qtype == QT_F16) return f(std::integral_constant<int, QT_F16>{});
+  return f(std::integral_constant<int, QT_BF16>{});
+}
+
 // Several weights of one type and shape to fp16 in one launch: blockIdx.y picks
 // the weight (routed experts before their grouped GEMM).
 constexpr int DQ_GROUP = 64;
@@ -107,11 +146,13 @@ bool gpu_type(int qtype) {
   }
 }
 
-int check_qweight(const char* who, const void* W, int qtype, size_t rb, int cols) {
+// dense_unit: the column granularity the caller needs for dense rows (F32 / F16 /
+// BF16): 8 where its kernels decode 8 consecutive elements at a time, 1 where it
+// has an element-wise path for other lengths.
+int check_qweight(const char* who, const void* W, int qtype, size_t rb, int cols, int dense_unit) {
   const BlockInfo* bi = block_info(qtype);
   if (!bi || !gpu_type(qtype)) return set_error(TIERMM_UNSUPPORTED, "%s: type %d is not handled on the GPU", who, qtype);
-  // the kernels decode 8 consecutive elements of one row at a time
-  const int whole = bi->elems > 8 ? bi->elems : 8;
+  const int whole = bi->elems > 1 ? (bi->elems > 8 ? bi->elems : 8) : dense_unit;
   if (cols <= 0 || cols % whole)
     return set_error(TIERMM_UNSUPPORTED, "%s: %d columns are not whole %s blocks of %d", who, cols, bi->name, whole);
   if (rb != (size_t)cols / bi->elems * bi->bytes)
@@ -173,13 +214,24 @@ using namespace tiermm;
 
 extern "C" int tiermm_dequant(const void* W, int qtype, size_t rb, int cols, size_t r0, size_t nrows, void* out,
                               int out_dtype, tiermm_stream_t stream) {
-  int st = check_qweight("tiermm_dequant", W, qtype, rb, cols);
+  int st = check_qweight("tiermm_dequant", W, qtype, rb, cols, 1);
   if (st) return st;
   if (out_dtype != TIERMM_OUT_F32 && out_dtype != TIERMM_OUT_F16 && out_dtype != TIERMM_OUT_BF16)
     return set_error(TIERMM_EINVAL, "tiermm_dequant: unknown output dtype %d", out_dtype);
+  hipStream_t s = (hipStream_t)stream;
+  const bool dense = qtype == QT_F32 || qtype == QT_F16 || qtype == QT_BF16;
+  if (dense && nrows && (cols % 8 || ((uintptr_t)out % 16))) {
+    // dq_k's one element per thread (tier.cpp:294-296) for rows that are not whole
+    // 8-element chunks, or an output that is not 16-byte aligned
+    const size_t align = out_dtype == TIERMM_OUT_F32 ? 4 : 2;
+    if (!out || ((uintptr_t)out % align))
+      return set_error(TIERMM_EINVAL, "tiermm_dequant: output must be %zu-byte aligned", align);
+    return with_dense(qtype, [&](auto qt) {
+      return launch_dequant_elems<decltype(qt)::value>(W, rb, cols, r0, nrows, out, out_dtype, s);
+    });
+  }
   if (nrows && (!out || ((uintptr_t)out % 16)))
     return set_error(TIERMM_EINVAL, "tiermm_dequant: output must be 16-byte aligned");
-  hipStream_t s = (hipStream_t)stream;
   return with_qtype(qtype, [&](auto qt) {
     return launch_dequant<decltype(qt)::value>(W, rb, cols, r0, nrows, out, out_dtype, s);
   });

@@ -15,7 +15,7 @@
 
 namespace tiermm {
 
-int check_qweight(const char* who, const void* W, int qtype, size_t rb, int cols);
+int check_qweight(const char* who, const void* W, int qtype, size_t rb, int cols, int dense_unit);
 
 namespace {
 
@@ -425,7 +425,7 @@ using namespace tiermm;
 
 extern "C" int tiermm_qgemv(const void* W, int qtype, size_t rb, const float* x, float* y, int N, int K,
                             tiermm_stream_t stream) {
-  int st = check_qweight("tiermm_qgemv", W, qtype, rb, K);
+  int st = check_qweight("tiermm_qgemv", W, qtype, rb, K, 1);
   if (st) return st;
   if (N < 0) return set_error(TIERMM_EINVAL, "tiermm_qgemv: N < 0");
   if (N == 0) return TIERMM_OK;

@@ -24,7 +24,7 @@
 
 namespace tiermm {
 
-int check_qweight(const char* who, const void* W, int qtype, size_t rb, int cols);
+int check_qweight(const char* who, const void* W, int qtype, size_t rb, int cols, int dense_unit);
 int dequant_f16_rows(const void* W, int qtype, size_t rb, int cols, size_t nrows, uint16_t* out, hipStream_t s,
                      bool tiled = false);
 int dequant_f16_group(const void* const* W, uint16_t* const* out, int n, int qtype, size_t rb, int cols,
@@ -195,9 +195,10 @@ __global__ __launch_bounds__(256) void x3s_split_kernel(const float* __restrict_
 }
 
 // fp16 transpose: dst[c][r] = src[r][c] for r < rows, c < cols (src row stride ld,
-// dst row stride rows), through a 64x64 LDS tile (odd column stride: no bank conflicts).
+// dst row stride dld >= rows), through a 64x64 LDS tile (odd column stride: no bank
+// conflicts).
 __global__ __launch_bounds__(256) void transpose16_kernel(const uint16_t* __restrict__ src, int ld,
-                                                          uint16_t* __restrict__ dst, int rows, int cols) {
+                                                          uint16_t* __restrict__ dst, int rows, int cols, int dld) {
   __shared__ uint16_t t[64][65];
   const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
@@ -208,7 +209,82 @@ __global__ __launch_bounds__(256) void transpose16_kernel(const uint16_t* __rest
   __syncthreads();
   for (int i = ty; i < 64; i += 4) {
     const int c = c0 + i, r = r0 + tx;
-    if (r < rows && c < cols) dst[(size_t)c * rows + r] = t[tx][i];
+    if (r < rows && c < cols) dst[(size_t)c * dld + r] = t[tx][i];
+  }
+}
+
+// ---- K padding.  The GEMMs step K by 32; when K is not a multiple of 32 the
+// operands are copied into the workspace as rows of Kp = roundup(K, 32) with
+// zeros in columns [K, Kp), which add nothing to any product.  These copies are
+// element-wise: only such shapes use them.
+
+// dst[r][k] = k < K ? src[r * ld + k] : 0 for 16-bit elements, rows x Kp.
+__global__ __launch_bounds__(256) void pad16_kernel(const uint16_t* __restrict__ src, size_t ld,
+                                                    uint16_t* __restrict__ dst, size_t rows, int K, int Kp) {
+  const size_t n = rows * (size_t)Kp, step = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) {
+    const size_t r = i / (size_t)Kp;
+    const int k = (int)(i - r * (size_t)Kp);
+    dst[i] = k < K ? src[r * ld + k] : (uint16_t)0;
+  }
+}
+
+// The same for fp32 rows.
+__global__ __launch_bounds__(256) void pad32_kernel(const float* __restrict__ src, size_t ld, float* __restrict__ dst,
+                                                    size_t rows, int K, int Kp) {
+  const size_t n = rows * (size_t)Kp, step = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) {
+    const size_t r = i / (size_t)Kp;
+    const int k = (int)(i - r * (size_t)Kp);
+    dst[i] = k < K ? src[r * ld + k] : 0.f;
+  }
+}
+
+// Columns [K, Kp) of rows x Kp 16-bit rows set to zero (after a transpose into them).
+__global__ __launch_bounds__(256) void zero_tail16_kernel(uint16_t* __restrict__ dst, size_t rows, int K, int Kp) {
+  const int w = Kp - K;
+  const size_t n = rows * (size_t)w, step = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) {
+    const size_t r = i / (size_t)w;
+    dst[r * Kp + K + (i - r * (size_t)w)] = 0;
+  }
+}
+
+// The three-part split (split3_fp_k / split3_k) of x[rows][K] (row stride ldx)
+// into HML planes of rows x Kp at parts + {0, n, 2n}, n = rows * Kp, zeros past K.
+template <bool BF>
+__global__ __launch_bounds__(256) void pad_split3_kernel(const float* __restrict__ x, size_t ldx,
+                                                         uint16_t* __restrict__ parts, size_t rows, int K, int Kp) {
+  auto to16 = [](float f) __attribute__((always_inline)) { return BF ? f2bf(f) : f2h(f); };
+  auto from16 = [](uint16_t u) __attribute__((always_inline)) {
+    return BF ? __uint_as_float((uint32_t)u << 16) : h2f(u);
+  };
+  const size_t n = rows * (size_t)Kp, step = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) {
+    const size_t r = i / (size_t)Kp;
+    const int k = (int)(i - r * (size_t)Kp);
+    const float v = k < K ? x[r * ldx + k] : 0.f;
+    const uint16_t h = to16(v);
+    const float d = v - from16(h);
+    const uint16_t m = to16(d);
+    parts[i] = h;
+    parts[n + i] = m;
+    parts[2 * n + i] = to16(d - from16(m));
+  }
+}
+
+// Dense q_val rows (F32 / F16 / BF16, row bytes rb) to fp16 (F16OUT: RNE, as
+// dq_k<tier_fp16>) or fp32 rows of Kp elements, zeros past K.
+template <int QT, bool F16OUT>
+__global__ __launch_bounds__(256) void dense_pad_kernel(const uint8_t* __restrict__ W, size_t rb,
+                                                        void* __restrict__ out, size_t rows, int K, int Kp) {
+  const size_t n = rows * (size_t)Kp, step = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) {
+    const size_t r = i / (size_t)Kp;
+    const int k = (int)(i - r * (size_t)Kp);
+    const float v = k < K ? dense_val<QT>(W + r * rb, (size_t)k) : 0.f;
+    if (F16OUT) ((uint16_t*)out)[i] = f2h(v);
+    else ((float*)out)[i] = v;
   }
 }
 
@@ -736,10 +812,25 @@ long big_tiles(int M, int N) {
   return (long)((M + XB_M - 1) / XB_M) * ((N + tn - 1) / tn);
 }
 
-int check_nt(const char* who, int M, int N, int K) {
+int check_sizes(const char* who, int M, int N, int K) {
   if (M < 0 || N < 0 || K < 0) return set_error(TIERMM_EINVAL, "%s: negative size", who);
+  return TIERMM_OK;
+}
+
+// Entry points whose operands come pre-split (no copy to pad them) need K in whole steps.
+int check_nt(const char* who, int M, int N, int K) {
+  const int st = check_sizes(who, M, N, K);
+  if (st) return st;
   if (K % BK) return set_error(TIERMM_UNSUPPORTED, "%s: K=%d is not a multiple of %d", who, K, BK);
   return TIERMM_OK;
+}
+
+int pad32(int K) { return (K + BK - 1) / BK * BK; }
+
+// Grid of the element-wise kernels (grid-stride loops).
+unsigned elem_grid(size_t n) {
+  const size_t want = (n + 255) / 256;
+  return (unsigned)(want < 16384 ? (want ? want : 1) : 16384);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -913,42 +1004,62 @@ int tiermm_x3s_gemm(const uint16_t* Xhi, const uint16_t* Xlo, const int32_t* xex
 }
 
 size_t tiermm_x3_gemm_ws_bytes(int m, int n, int k) {
-  // three fp16 planes of B, and for TIERMM_OP_N the transposed weight
-  return (size_t)3 * (size_t)n * (size_t)k * sizeof(uint16_t) + (size_t)m * (size_t)k * sizeof(uint16_t);
+  // three fp16 planes of B, and the weight rows for TIERMM_OP_N (transposed) or an
+  // odd k (padded), both with rows of k rounded up to 32
+  const size_t kp = (size_t)pad32(k);
+  return (size_t)3 * (size_t)n * kp * sizeof(uint16_t) + (size_t)m * kp * sizeof(uint16_t);
 }
 
 static int x3_gemm_impl(int opA, int m, int n, int k, const uint16_t* A, int lda, const float* B, float beta, float* C,
                         int ldc, void* ws, size_t ws_bytes, tiermm_stream_t stream, bool bf16, const char* who) {
   if (opA != TIERMM_OP_T && opA != TIERMM_OP_N) return set_error(TIERMM_EINVAL, "%s: opA %d", who, opA);
-  int st = check_nt(who, n, m, k);
+  int st = check_sizes(who, n, m, k);
   if (st) return st;
   if ((opA == TIERMM_OP_T && lda < k) || (opA == TIERMM_OP_N && lda < m) || ldc < m)
     return set_error(TIERMM_EINVAL, "%s: lda or ldc too small", who);
   if (m == 0 || n == 0) return TIERMM_OK;
-  if (!A || !B || !C || (opA == TIERMM_OP_T && (!aligned16(A) || (lda % 8))))
+  const int kp = pad32(k);
+  if (!A || !B || !C || (opA == TIERMM_OP_T && kp == k && (!aligned16(A) || (lda % 8))))
     return set_error(TIERMM_EINVAL, "%s: A must be 16-byte aligned with lda a multiple of 8", who);
   void* w = nullptr;
-  const size_t nk = (size_t)n * k;
+  const size_t nk = (size_t)n * kp;
   st = get_workspace(ws, ws_bytes, tiermm_x3_gemm_ws_bytes(m, n, k), &w, who);
   if (st) return st;
   hipStream_t s = (hipStream_t)stream;
   uint16_t* parts = (uint16_t*)w;
-  st = split3_launch(B, parts, nk, nk, TIERMM_HML, s, bf16);
+  uint16_t* t = parts + 3 * nk;  // transposed or padded weight rows
+  if (kp == k) {
+    st = split3_launch(B, parts, nk, nk, TIERMM_HML, s, bf16);
+  } else {  // rows of kp with zeros past k (k not a multiple of the 32-wide K step)
+    if (bf16)
+      pad_split3_kernel<true><<<elem_grid(nk), 256, 0, s>>>(B, (size_t)k, parts, (size_t)n, k, kp);
+    else
+      pad_split3_kernel<false><<<elem_grid(nk), 256, 0, s>>>(B, (size_t)k, parts, (size_t)n, k, kp);
+    TM_LAUNCH_CHECK("tiermm_x3_gemm: padded split");
+  }
   if (st) return st;
   const uint16_t* At = A;
   int ldt = lda;
   if (opA == TIERMM_OP_N) {
     // A is m x k column-major ([k][lda] in memory, the dX layout of tier.cpp:1226):
-    // transpose it to [m][k] so the product runs in the NT form below
-    uint16_t* t = parts + 3 * nk;
+    // transpose it to [m][kp] so the product runs in the NT form below
     dim3 grid((unsigned)((m + 63) / 64), (unsigned)((k + 63) / 64));
-    transpose16_kernel<<<grid, 256, 0, s>>>(A, lda, t, k, m);
+    transpose16_kernel<<<grid, 256, 0, s>>>(A, lda, t, k, m, kp);
     TM_LAUNCH_CHECK("tiermm_x3_gemm: transpose");
+    if (kp != k) {
+      zero_tail16_kernel<<<elem_grid((size_t)m * (kp - k)), 256, 0, s>>>(t, (size_t)m, k, kp);
+      TM_LAUNCH_CHECK("tiermm_x3_gemm: padding");
+    }
     At = t;
-    ldt = k;
+    ldt = kp;
+  } else if (kp != k) {
+    pad16_kernel<<<elem_grid((size_t)m * kp), 256, 0, s>>>(A, (size_t)lda, t, (size_t)m, k, kp);
+    TM_LAUNCH_CHECK("tiermm_x3_gemm: padding");
+    At = t;
+    ldt = kp;
   }
   // column-major C(m x n) with ldc == row-major out[n][ldc] = x[n][k] * W[m][k]^T
-  return x3ref_nt(parts, nk, At, ldt, C, ldc, n, m, k, beta, s, who, bf16);
+  return x3ref_nt(parts, nk, At, ldt, C, ldc, n, m, kp, beta, s, who, bf16);
 }
 
 int tiermm_x3_gemm(int opA, int m, int n, int k, const uint16_t* A, int lda, const float* B, float beta, float* C,
@@ -962,13 +1073,15 @@ int tiermm_x3_gemm_bf16(int opA, int m, int n, int k, const uint16_t* A, int lda
 }
 
 size_t tiermm_x3_rows_ws_bytes(int M, int K, int N) {
-  (void)N;
-  return (size_t)3 * (size_t)M * (size_t)K * sizeof(uint16_t);
+  // three fp16 planes of x; for an odd K (not a multiple of 32) rows padded to a
+  // multiple of 32, and the weight copied to such rows
+  const size_t kp = (size_t)pad32(K);
+  return (size_t)3 * (size_t)M * kp * sizeof(uint16_t) + (kp != (size_t)K ? (size_t)N * kp * sizeof(uint16_t) : 0);
 }
 
 static int x3_rows_impl(const uint16_t* W, const float* x, float* y, int M, int K, int N, int ldo, void* ws,
                         size_t ws_bytes, tiermm_stream_t stream, bool bf16, const char* who) {
-  int st = check_nt(who, M, N, K);
+  int st = check_sizes(who, M, N, K);
   if (st) return st;
   if (ldo < N) return set_error(TIERMM_EINVAL, "%s: ldo < N", who);
   if (M == 0 || N == 0) return TIERMM_OK;
@@ -977,10 +1090,23 @@ static int x3_rows_impl(const uint16_t* W, const float* x, float* y, int M, int 
   st = get_workspace(ws, ws_bytes, tiermm_x3_rows_ws_bytes(M, K, N), &w, who);
   if (st) return st;
   hipStream_t s = (hipStream_t)stream;
-  const size_t mk = (size_t)M * K;
-  st = split3_launch(x, (uint16_t*)w, mk, mk, TIERMM_HML, s, bf16);
-  if (st) return st;
-  return x3ref_nt((const uint16_t*)w, mk, W, K, y, ldo, M, N, K, 0.f, s, who, bf16);
+  const int kp = pad32(K);
+  const size_t mk = (size_t)M * kp;
+  if (kp == K) {
+    st = split3_launch(x, (uint16_t*)w, mk, mk, TIERMM_HML, s, bf16);
+    if (st) return st;
+    return x3ref_nt((const uint16_t*)w, mk, W, K, y, ldo, M, N, K, 0.f, s, who, bf16);
+  }
+  uint16_t* parts = (uint16_t*)w;
+  uint16_t* wp = parts + 3 * mk;
+  if (bf16)
+    pad_split3_kernel<true><<<elem_grid(mk), 256, 0, s>>>(x, (size_t)K, parts, (size_t)M, K, kp);
+  else
+    pad_split3_kernel<false><<<elem_grid(mk), 256, 0, s>>>(x, (size_t)K, parts, (size_t)M, K, kp);
+  TM_LAUNCH_CHECK("x3_rows: padded split");
+  pad16_kernel<<<elem_grid((size_t)N * kp), 256, 0, s>>>(W, (size_t)K, wp, (size_t)N, K, kp);
+  TM_LAUNCH_CHECK("x3_rows: padding");
+  return x3ref_nt(parts, mk, wp, kp, y, ldo, M, N, kp, 0.f, s, who, bf16);
 }
 
 int tiermm_x3_rows(const uint16_t* W, const float* x, float* y, int M, int K, int N, int ldo, void* ws,
@@ -994,7 +1120,71 @@ int tiermm_x3_rows_bf16(const uint16_t* W, const float* x, float* y, int M, int 
 }
 
 
+// tiermm_qgemm for dense rows (F32 / F16 / BF16) whose length K is not a multiple of
+// the 32-wide K step (every block type is): W and x are copied into the workspace
+// as rows of Kp = roundup(K, 32) with zeros past K, then multiplied as usual.
+static int qgemm_padded(const void* W, int qtype, size_t rb, const float* X, float* Y, int M, int N, int K, int ldy,
+                        int mode, float beta, void* w, hipStream_t s, const char* who) {
+  if (qtype != TIERMM_F32 && qtype != TIERMM_F16 && qtype != TIERMM_BF16)
+    return set_error(TIERMM_EINVAL, "%s: K=%d is not whole blocks of type %d", who, K, qtype);
+  const int kp = pad32(K);
+  const size_t nkp = (size_t)N * kp, mkp = (size_t)M * kp;
+  const uint8_t* wq = (const uint8_t*)W;
+  auto dense_pad = [&](void* out, bool f16) {
+    const unsigned g = elem_grid(nkp);
+    if (qtype == TIERMM_F32) {
+      if (f16) dense_pad_kernel<QT_F32, true><<<g, 256, 0, s>>>(wq, rb, out, (size_t)N, K, kp);
+      else dense_pad_kernel<QT_F32, false><<<g, 256, 0, s>>>(wq, rb, out, (size_t)N, K, kp);
+    } else if (qtype == TIERMM_F16) {
+      if (f16) dense_pad_kernel<QT_F16, true><<<g, 256, 0, s>>>(wq, rb, out, (size_t)N, K, kp);
+      else dense_pad_kernel<QT_F16, false><<<g, 256, 0, s>>>(wq, rb, out, (size_t)N, K, kp);
+    } else {
+      if (f16) dense_pad_kernel<QT_BF16, true><<<g, 256, 0, s>>>(wq, rb, out, (size_t)N, K, kp);
+      else dense_pad_kernel<QT_BF16, false><<<g, 256, 0, s>>>(wq, rb, out, (size_t)N, K, kp);
+    }
+  };
+  if (mode == TIERMM_MODE_F32) {
+    uint8_t* b = (uint8_t*)w;
+    float* wf = (float*)b;       b += al256(nkp * 4);
+    uint16_t* whi = (uint16_t*)b; b += al256(nkp * 2);
+    uint16_t* wlo = (uint16_t*)b; b += al256(nkp * 2);
+    int32_t* wexp = (int32_t*)b;  b += al256((size_t)N * 4);
+    float* xf = (float*)b;        b += al256(mkp * 4);
+    uint16_t* xhi = (uint16_t*)b; b += al256(mkp * 2);
+    uint16_t* xlo = (uint16_t*)b; b += al256(mkp * 2);
+    int32_t* xexp = (int32_t*)b;
+    dense_pad(wf, false);
+    TM_LAUNCH_CHECK("tiermm_qgemm: padded W");
+    pad32_kernel<<<elem_grid(mkp), 256, 0, s>>>(X, (size_t)K, xf, (size_t)M, K, kp);
+    TM_LAUNCH_CHECK("tiermm_qgemm: padded x");
+    x3s_split_launch(wf, whi, wlo, wexp, N, kp, s);
+    TM_LAUNCH_CHECK("tiermm_qgemm: split W");
+    x3s_split_launch(xf, xhi, xlo, xexp, M, kp, s);
+    TM_LAUNCH_CHECK("tiermm_qgemm: split x");
+    X3Args a{};
+    a.A[0] = xhi; a.A[1] = xlo; a.B[0] = whi; a.B[1] = wlo;
+    a.lda = kp; a.ldb = kp; a.C = Y; a.ldc = ldy; a.M = M; a.N = N; a.K = kp;
+    a.aexp = xexp; a.bexp = wexp; a.beta = beta;
+    if (big_tiles(M, N) >= 192) return launch_x3_big<X3_2X2>(a, s, who);
+    return launch_x3<128, 128, X3_2X2>(a, s, who);
+  }
+  uint16_t* w16 = (uint16_t*)w;
+  uint16_t* parts = (uint16_t*)((uint8_t*)w + al256(nkp * 2));
+  dense_pad(w16, true);
+  TM_LAUNCH_CHECK("tiermm_qgemm: padded W");
+  pad_split3_kernel<false><<<elem_grid(mkp), 256, 0, s>>>(X, (size_t)K, parts, (size_t)M, K, kp);
+  TM_LAUNCH_CHECK("tiermm_qgemm: padded split");
+  return x3ref_nt(parts, mkp, w16, kp, Y, ldy, M, N, kp, beta, s, who);
+}
+
 size_t tiermm_qgemm_ws_bytes(int qtype, int M, int N, int K, int mode) {
+  if (K % BK) {  // dense rows of an odd length: W and x padded to rows of Kp
+    const size_t kp = (size_t)pad32(K);
+    if (mode == TIERMM_MODE_F32)  // padded fp32 W and x, their two-part splits
+      return al256((size_t)N * kp * 4) + 2 * al256((size_t)N * kp * 2) + al256((size_t)N * 4) +
+             al256((size_t)M * kp * 4) + 2 * al256((size_t)M * kp * 2) + al256((size_t)M * 4);
+    return al256((size_t)N * kp * 2) + (size_t)3 * M * kp * sizeof(uint16_t);  // padded W16, x planes
+  }
   if (mode == TIERMM_MODE_F32)  // fp32 W, its two-part split, and x's
     return al256((size_t)N * K * 4) + 2 * al256((size_t)N * K * 2) + al256((size_t)N * 4) +
            2 * al256((size_t)M * K * 2) + al256((size_t)M * 4);
@@ -1007,10 +1197,10 @@ size_t tiermm_qgemm_ws_bytes(int qtype, int M, int N, int K, int mode) {
 int tiermm_qgemm(const void* W, int qtype, size_t rb, const float* X, float* Y, int M, int N, int K, int ldy,
                  int mode, float beta, void* ws, size_t ws_bytes, tiermm_stream_t stream) {
   const char* who = "tiermm_qgemm";
-  int st = check_qweight(who, W, qtype, rb, K);
+  int st = check_qweight(who, W, qtype, rb, K, 1);
   if (st) return st;
   if (mode != TIERMM_MODE_X3REF && mode != TIERMM_MODE_F32) return set_error(TIERMM_EINVAL, "%s: mode %d", who, mode);
-  st = check_nt(who, M, N, K);
+  st = check_sizes(who, M, N, K);
   if (st) return st;
   if (ldy < N) return set_error(TIERMM_EINVAL, "%s: ldy < N", who);
   if (M == 0 || N == 0) return TIERMM_OK;
@@ -1019,6 +1209,7 @@ int tiermm_qgemm(const void* W, int qtype, size_t rb, const float* X, float* Y, 
   st = get_workspace(ws, ws_bytes, tiermm_qgemm_ws_bytes(qtype, M, N, K, mode), &w, who);
   if (st) return st;
   hipStream_t s = (hipStream_t)stream;
+  if (K % BK) return qgemm_padded(W, qtype, rb, X, Y, M, N, K, ldy, mode, beta, w, s, who);
   const size_t mk = (size_t)M * K;
   if (mode == TIERMM_MODE_F32) {
     // chat prefill semantics (tier.cpp:2358-2359): fp32 dequant, fp32-accurate
@@ -1111,7 +1302,7 @@ int tiermm_qgemm_grouped(const void* const* W_e, const int* qtype_e, const size_
   if (st) return st;
   for (int e = 0; e < n_experts; ++e) {
     if (expert_offsets[e + 1] == expert_offsets[e]) continue;
-    st = check_qweight(who, W_e[e], qtype_e[e], rb_e[e], K);
+    st = check_qweight(who, W_e[e], qtype_e[e], rb_e[e], K, 8);
     if (st) return st;
   }
   if (n_experts == 0 || expert_offsets[n_experts] == 0 || N == 0) return TIERMM_OK;
