@@ -62,8 +62,15 @@ enum {
   TIERMM_Q4_K = 12,
   TIERMM_Q5_K = 13,
   TIERMM_Q6_K = 14,
+  TIERMM_IQ2_XXS = 16,
+  TIERMM_IQ2_XS = 17,
+  TIERMM_IQ3_XXS = 18,
+  TIERMM_IQ1_S = 19,
   TIERMM_IQ4_NL = 20,
+  TIERMM_IQ3_S = 21,
+  TIERMM_IQ2_S = 22,
   TIERMM_IQ4_XS = 23,
+  TIERMM_IQ1_M = 29,
   TIERMM_BF16 = 30,
   TIERMM_TQ1_0 = 34,
   TIERMM_TQ2_0 = 35,
@@ -109,10 +116,10 @@ int tiermm_q_row_bytes(int qtype, int cols, size_t* rb);
 /* dq_k<T> / dq_launch (tier.cpp:293-298): for i < nrows*cols,
  * out[i] = T(q_val(W + (r0 + i/cols)*rb, qtype, i%cols)), T = fp32, fp16
  * (round to nearest even, subnormals kept, as tier_fp16) or bf16 (RNE, as
- * hip_bfloat16).  qtype: every q_val type but the lattice-grid IQ2_*, IQ3_* and
- * IQ1_* families -- F32, F16, BF16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K,
- * Q5_K, Q6_K, IQ4_NL, IQ4_XS, TQ1_0, TQ2_0, MXFP4, NF4, FP4; cols a multiple of 8
- * and of the block.
+ * hip_bfloat16).  qtype: every q_val type -- F32, F16, BF16, Q4_0, Q4_1, Q5_0,
+ * Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S,
+ * IQ1_S, IQ1_M, IQ4_NL, IQ4_XS, TQ1_0, TQ2_0, MXFP4, NF4, FP4; cols a multiple of
+ * the block (dense rows: any cols).
  * Bit-exact with the reference's q_val for finite block scales. */
 int tiermm_dequant(const void* W, int qtype, size_t rb, int cols, size_t r0, size_t nrows,
                    void* out, int out_dtype, tiermm_stream_t stream);

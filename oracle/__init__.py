@@ -28,6 +28,7 @@ REF_PATH = os.path.join(HERE, "_ref", "libtqref.so")
 F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, BF16 = (
     0, 1, 2, 3, 6, 7, 8, 10, 11, 12, 13, 14, 30)
 IQ4_NL, IQ4_XS, TQ1_0, TQ2_0, MXFP4, NF4, FP4 = 20, 23, 34, 35, 39, 200, 201
+IQ2_XXS, IQ2_XS, IQ3_XXS, IQ1_S, IQ3_S, IQ2_S, IQ1_M = 16, 17, 18, 19, 21, 22, 29
 OUT_F32, OUT_F16, OUT_BF16 = 0, 1, 2
 
 _u8p = ctypes.POINTER(ctypes.c_uint8)
@@ -245,10 +246,18 @@ def random_blocks(rng: np.random.Generator, qtype: int, nblocks: int, moderate: 
     b = rng.integers(0, 256, size=(nblocks, bb), dtype=np.uint8)
     halfs = {Q4_0: [0], Q4_1: [0, 2], Q5_0: [0], Q5_1: [0, 2], Q8_0: [0], Q2_K: [80, 82], Q3_K: [108],
              Q4_K: [0, 2], Q5_K: [0, 2], Q6_K: [208], IQ4_NL: [0], IQ4_XS: [0], TQ1_0: [52],
-             TQ2_0: [64]}.get(qtype, [])
+             TQ2_0: [64], IQ2_XXS: [0], IQ2_XS: [0], IQ2_S: [0], IQ3_XXS: [0], IQ3_S: [0],
+             IQ1_S: [0]}.get(qtype, [])
     for o in halfs:
         h = (rng.standard_normal(nblocks) * 0.02).astype(np.float16).view(np.uint8).reshape(nblocks, 2)
         b[:, o:o + 2] = h
+    if qtype == IQ1_M:  # the fp16 d sits in the top nibbles of the four u16 scale words at 48
+        h = (rng.standard_normal(nblocks) * 0.02).astype(np.float16).view(np.uint16).astype(np.uint32)
+        for j in range(4):
+            w = b[:, 48 + 2 * j].astype(np.uint32) | (b[:, 49 + 2 * j].astype(np.uint32) << 8)
+            w = (w & 0x0fff) | (((h >> (4 * j)) & 15) << 12)
+            b[:, 48 + 2 * j] = (w & 255).astype(np.uint8)
+            b[:, 49 + 2 * j] = (w >> 8).astype(np.uint8)
     if qtype in (NF4, FP4):
         b[:, 0:4] = (rng.standard_normal(nblocks) * 0.02).astype(np.float32).view(np.uint8).reshape(nblocks, 4)
     if qtype == MXFP4 and moderate:

@@ -7,6 +7,7 @@
  * the written C rounds.  See tq_oracle.h for what pins each function.
  */
 #include "tq_oracle.h"
+#include "../tier_amd/csrc/iq_grids.h"
 
 #include <math.h>
 #include <string.h>
@@ -14,6 +15,21 @@
 static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
 static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
 static inline uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+/* lattice-grid helpers: magnitude of element e of a packed IQ2 point, value of
+ * element e of an IQ1 point, the sign byte of a 7-bit index (its parity in bit 7)
+ * and the sign of element e */
+static inline float iq2_mag(uint16_t w, int e) {
+  const int c = (w >> (2 * e)) & 3;
+  return c == 0 ? 8.f : c == 1 ? 25.f : 43.f;
+}
+static inline int iq1_val(uint16_t w, int e) { return ((w >> (2 * e)) & 3) - 1; }
+static inline uint32_t parity_byte(uint32_t idx) {
+  uint32_t p = 0;
+  for (int b = 0; b < 7; ++b) p ^= (idx >> b) & 1u;
+  return idx | (p << 7);
+}
+static inline float sign_of(uint32_t s, int e) { return (s >> e) & 1u ? -1.f : 1.f; }
 static inline uint32_t rd32(const uint8_t* p) {
   return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
 }
@@ -249,6 +265,69 @@ float orc_q_val(const uint8_t* row, int type, int col) {
       else x = (uint8_t)(b[48 + (i - 240) % 4] * pow3[(i - 240) / 4]);
       const int trit = ((int)x * 3) >> 8;
       return fp16_at(b + 52) * (float)(trit - 1);
+    }
+    /* The lattice-grid types (quant.h:95-115).  A grid point holds 8 (IQ2, IQ1) or 4
+     * (IQ3) magnitudes; iq_grids.h packs each point into codes (its header gives the
+     * value of each code).  Signs: a 7-bit index whose parity is the eighth bit, or
+     * a sign byte; bit e of it negates element e of the 8-element group. */
+    case ORC_IQ2_XXS: { /* 66 bytes: d @0, then per 32 elements 4 point bytes and a u32 of 4 x 7-bit sign indices + 4-bit scale */
+      const uint8_t* b = row + (size_t)(col / 256) * 66;
+      const int grp = i / 32, sub = (i % 32) / 8, e = i % 8;
+      const uint32_t pts = rd32(b + 2 + 8 * grp), aux = rd32(b + 6 + 8 * grp);
+      const float db = fp16_at(b) * (0.5f + (float)(aux >> 28)) * 0.25f;
+      const float mag = iq2_mag(tm_iq2xxs_grid[(pts >> (8 * sub)) & 255], e);
+      return (db * mag) * sign_of(parity_byte((aux >> (7 * sub)) & 127), e);
+    }
+    case ORC_IQ2_XS: { /* 74 bytes: d @0, 32 x u16 @2 (9-bit point, 7-bit sign index), 4-bit scales @66 */
+      const uint8_t* b = row + (size_t)(col / 256) * 74;
+      const int k = i / 8, e = i % 8, s16 = i / 16;
+      const uint32_t q = rd16(b + 2 + 2 * k);
+      const float db = fp16_at(b) * (0.5f + (float)((b[66 + s16 / 2] >> (4 * (s16 % 2))) & 15)) * 0.25f;
+      return (db * iq2_mag(tm_iq2xs_grid[q % 512], e)) * sign_of(parity_byte(q >> 9), e);
+    }
+    case ORC_IQ2_S: { /* 82 bytes: d @0, point low bytes @2, sign bytes @34, point high 2-bit pairs @66, scales @74 */
+      const uint8_t* b = row + (size_t)(col / 256) * 82;
+      const int k = i / 8, e = i % 8, s16 = i / 16;
+      const float db = fp16_at(b) * (0.5f + (float)((b[74 + s16 / 2] >> (4 * (s16 % 2))) & 15)) * 0.25f;
+      const int pt = b[2 + k] + 256 * ((b[66 + k / 4] >> (2 * (k % 4))) & 3);
+      return (db * iq2_mag(tm_iq2s_grid[pt], e)) * sign_of(b[34 + k], e);
+    }
+    case ORC_IQ3_XXS: { /* 98 bytes: d @0, point bytes @2 (4 elements each), per 32 elements a u32 @66 */
+      const uint8_t* b = row + (size_t)(col / 256) * 98;
+      const int grp = i / 32, sub = (i % 32) / 8, e = i % 8;
+      const uint32_t aux = rd32(b + 66 + 4 * grp);
+      const float db = fp16_at(b) * (0.5f + (float)(aux >> 28)) * 0.5f;
+      const int code = (tm_iq3xxs_grid[b[2 + i / 4]] >> (3 * (i % 4))) & 7;
+      const float mag = code == 7 ? 62.f : (float)(8 * code + 4);
+      return (db * mag) * sign_of(parity_byte((aux >> (7 * sub)) & 127), e);
+    }
+    case ORC_IQ3_S: { /* 110 bytes: d @0, point low bytes @2, point high bits @66, sign bytes @74, 4-bit scales @106 */
+      const uint8_t* b = row + (size_t)(col / 256) * 110;
+      const int grp = i / 32, k = i / 4;
+      const float db = fp16_at(b) * (float)(1 + 2 * ((b[106 + grp / 2] >> (4 * (grp % 2))) & 15));
+      const int pt = b[2 + k] + 256 * ((b[66 + k / 8] >> (k % 8)) & 1);
+      const int code = (tm_iq3s_grid[pt] >> (3 * (i % 4))) & 7;
+      return (db * (float)(2 * code + 1)) * sign_of(b[74 + i / 8], i % 8);
+    }
+    case ORC_IQ1_S: { /* 50 bytes: d @0, point low bytes @2, per 32 elements a u16 @34 (3 x 3 high bits ..., scale, delta sign) */
+      const uint8_t* b = row + (size_t)(col / 256) * 50;
+      const int grp = i / 32, k = i / 8, e = i % 8;
+      const uint32_t qh = rd16(b + 34 + 2 * grp);
+      const float dl = fp16_at(b) * (float)(2 * ((qh >> 12) & 7) + 1);
+      const float delta = (qh & 0x8000u) ? -0.125f : 0.125f;
+      const int pt = b[2 + k] + 256 * (int)((qh >> (3 * (k % 4))) & 7);
+      return dl * ((float)iq1_val(tm_iq1s_grid[pt], e) + delta);
+    }
+    case ORC_IQ1_M: { /* 56 bytes: point low bytes @0, high nibbles @32, 4 x u16 @48: 3-bit scales + fp16 d in the top nibbles */
+      const uint8_t* b = row + (size_t)(col / 256) * 56;
+      const int k = i / 8, e = i % 8, s16 = i / 16;
+      const uint32_t d16 = (rd16(b + 48) >> 12) | ((rd16(b + 50) >> 12) << 4) | ((rd16(b + 52) >> 12) << 8) |
+                           ((rd16(b + 54) >> 12) << 12);
+      const float dl = orc_h2f((uint16_t)d16) * (float)(2 * ((rd16(b + 48 + 2 * (s16 / 4)) >> (3 * (s16 % 4))) & 7) + 1);
+      const int hi = (b[32 + k / 2] >> (4 * (k % 2))) & 15;
+      const float delta = (hi & 8) ? -0.125f : 0.125f;
+      const int pt = b[k] + 256 * (hi & 7);
+      return dl * ((float)iq1_val(tm_iq1s_grid[pt], e) + delta);
     }
     default: return 0.f;
   }

@@ -25,7 +25,9 @@ enum {
   ORC_F32 = 0, ORC_F16 = 1, ORC_Q4_0 = 2, ORC_Q4_1 = 3, ORC_Q5_0 = 6, ORC_Q5_1 = 7,
   ORC_Q8_0 = 8, ORC_Q2_K = 10, ORC_Q3_K = 11, ORC_Q4_K = 12, ORC_Q5_K = 13,
   ORC_Q6_K = 14, ORC_IQ4_NL = 20, ORC_IQ4_XS = 23, ORC_BF16 = 30, ORC_TQ1_0 = 34,
-  ORC_TQ2_0 = 35, ORC_MXFP4 = 39, ORC_NF4 = 200, ORC_FP4 = 201
+  ORC_TQ2_0 = 35, ORC_MXFP4 = 39, ORC_NF4 = 200, ORC_FP4 = 201,
+  ORC_IQ2_XXS = 16, ORC_IQ2_XS = 17, ORC_IQ3_XXS = 18, ORC_IQ1_S = 19, ORC_IQ3_S = 21, ORC_IQ2_S = 22,
+  ORC_IQ1_M = 29
 };
 /* output dtypes of the dequant (dq_k<T>, tier.cpp:294): float, tier_fp16, hip_bfloat16 */
 enum { ORC_OUT_F32 = 0, ORC_OUT_F16 = 1, ORC_OUT_BF16 = 2 };

@@ -8,7 +8,8 @@ outputs are stored here):
     python tests/golden/make_golden.py
 
 Fixtures (numpy .npz, no pickles):
-  dequant_golden.npz   for each type: random blocks built as check_quant.py:31-48
+  dequant_golden.npz   for each type (the eight k-quant / legacy types, then the seven
+                       lattice-grid IQ types): random blocks built as check_quant.py:31-48
                        builds them (seed 7, 8 rows x 512 cols, fp16 scale fields
                        ~N(0,0.02)) and the reference q_val of every element (fp32 bits)
   quant_golden.npz     x ~N(0,0.02) [8][1024] (seed 11) and the bytes the
@@ -25,7 +26,10 @@ sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
 import oracle  # noqa: E402
 
 TYPES = {"q4_0": oracle.Q4_0, "q4_1": oracle.Q4_1, "q5_0": oracle.Q5_0, "q5_1": oracle.Q5_1,
-         "q8_0": oracle.Q8_0, "q4_K": oracle.Q4_K, "q5_K": oracle.Q5_K, "q6_K": oracle.Q6_K}
+         "q8_0": oracle.Q8_0, "q4_K": oracle.Q4_K, "q5_K": oracle.Q5_K, "q6_K": oracle.Q6_K,
+         # appended later: the random draws of the types above stay as they were
+         "iq2_xxs": oracle.IQ2_XXS, "iq2_xs": oracle.IQ2_XS, "iq2_s": oracle.IQ2_S, "iq3_xxs": oracle.IQ3_XXS,
+         "iq3_s": oracle.IQ3_S, "iq1_s": oracle.IQ1_S, "iq1_m": oracle.IQ1_M}
 COLS, ROWS = 512, 8
 
 

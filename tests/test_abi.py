@@ -73,8 +73,8 @@ def test_quantizer_error_bounds(t, lim):
 
 def test_argument_checks_return_before_device_work():
     L = tier_amd.lib()
-    # unknown / unhandled type
-    assert L.tiermm_dequant(16, 16, 66, 256, 0, 1, 16, tier_amd.OUT_F16, None) == tier_amd.UNSUPPORTED
+    # unknown type id
+    assert L.tiermm_dequant(16, 99, 66, 256, 0, 1, 16, tier_amd.OUT_F16, None) == tier_amd.UNSUPPORTED
     # rb inconsistent with cols
     assert L.tiermm_dequant(16, tier_amd.Q4_K, 100, 256, 0, 1, 16, tier_amd.OUT_F16, None) == tier_amd.EINVAL
     # misaligned Q4_K rows

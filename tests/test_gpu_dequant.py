@@ -167,3 +167,25 @@ def test_dequant_more_types_bit_exact(gpu, name, outname):
     got = _run(gpu, blocks.reshape(512 * bb // tier_amd.q_row_bytes(t, cols), -1), t, cols, out)
     want = _expect(blocks, t, cols, out)
     assert np.array_equal(got, want)
+
+
+LATTICE = {"iq2_xxs": tier_amd.IQ2_XXS, "iq2_xs": tier_amd.IQ2_XS, "iq2_s": tier_amd.IQ2_S,
+           "iq3_xxs": tier_amd.IQ3_XXS, "iq3_s": tier_amd.IQ3_S, "iq1_s": tier_amd.IQ1_S, "iq1_m": tier_amd.IQ1_M}
+
+
+@pytest.mark.parametrize("name", list(LATTICE))
+@pytest.mark.parametrize("outname", list(OUTS))
+def test_dequant_lattice_types_bit_exact(gpu, golden, name, outname):
+    """The lattice-grid types (quant.h:95-115): the golden blocks against the reference's own values,
+    and 3000 random blocks -- enough that every grid point is read (test_oracle checks that on the
+    same construction) -- against the oracle, which is pinned to the reference build."""
+    t, out = LATTICE[name], OUTS[outname][0]
+    blocks = golden["dequant"][f"{name}_blocks"]
+    got = _run(gpu, blocks, t, 512, out)
+    want = _expect(blocks, t, 512, out)
+    if out == tier_amd.OUT_F32:
+        assert np.array_equal(want, golden["dequant"][f"{name}_f32bits"].ravel())
+    assert np.array_equal(got, want)
+    rng = np.random.default_rng(300 + t)
+    blocks = oracle.random_blocks(rng, t, 3000).reshape(300, -1)
+    assert np.array_equal(_run(gpu, blocks, t, 2560, out), _expect(blocks, t, 2560, out))

@@ -56,7 +56,8 @@ def test_gemv_config_shapes(gpu, name, t, N, K):
 @pytest.mark.parametrize("t", [tier_amd.Q8_0, tier_amd.Q5_0, tier_amd.Q4_K, tier_amd.Q5_K, tier_amd.Q6_K,
                                tier_amd.Q4_0, tier_amd.Q4_1, tier_amd.Q5_1, tier_amd.Q2_K, tier_amd.Q3_K,
                                tier_amd.IQ4_NL, tier_amd.IQ4_XS, tier_amd.TQ1_0, tier_amd.TQ2_0, tier_amd.MXFP4,
-                               tier_amd.NF4, tier_amd.FP4])
+                               tier_amd.NF4, tier_amd.FP4, tier_amd.IQ2_XXS, tier_amd.IQ2_XS, tier_amd.IQ2_S,
+                               tier_amd.IQ3_XXS, tier_amd.IQ3_S, tier_amd.IQ1_S, tier_amd.IQ1_M])
 @pytest.mark.parametrize("N,K", [(1, 256), (13, 512), (7, 768), (65, 2304)])
 def test_gemv_ragged_shapes(gpu, t, N, K):
     """Row counts that do not fill a wave or a block; one super-block rows; K not a multiple of 512."""

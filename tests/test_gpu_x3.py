@@ -307,7 +307,8 @@ def test_qgemm_f32_mode(gpu, name, t, M, N, K):
 
 
 @pytest.mark.parametrize("t", [tier_amd.Q4_0, tier_amd.Q4_1, tier_amd.Q5_1, tier_amd.F32, tier_amd.F16, tier_amd.BF16,
-                               tier_amd.Q3_K, tier_amd.IQ4_XS, tier_amd.NF4])
+                               tier_amd.Q3_K, tier_amd.IQ4_XS, tier_amd.NF4, tier_amd.IQ2_XS, tier_amd.IQ3_S,
+                               tier_amd.IQ1_M])
 @pytest.mark.parametrize("mode", [tier_amd.MODE_X3REF, tier_amd.MODE_F32])
 def test_qgemm_more_types(gpu, t, mode):
     """The legacy 32-blocks and dense rows through tiermm_qgemm, both semantics, against fp64."""

@@ -11,7 +11,9 @@ import pytest
 import oracle
 
 NAMES = {"q4_0": oracle.Q4_0, "q4_1": oracle.Q4_1, "q5_0": oracle.Q5_0, "q5_1": oracle.Q5_1,
-         "q8_0": oracle.Q8_0, "q4_K": oracle.Q4_K, "q5_K": oracle.Q5_K, "q6_K": oracle.Q6_K}
+         "q8_0": oracle.Q8_0, "q4_K": oracle.Q4_K, "q5_K": oracle.Q5_K, "q6_K": oracle.Q6_K,
+         "iq2_xxs": oracle.IQ2_XXS, "iq2_xs": oracle.IQ2_XS, "iq2_s": oracle.IQ2_S, "iq3_xxs": oracle.IQ3_XXS,
+         "iq3_s": oracle.IQ3_S, "iq1_s": oracle.IQ1_S, "iq1_m": oracle.IQ1_M}
 
 
 # ------------------------------------------------------------------ golden vectors
@@ -348,3 +350,43 @@ def test_mxfp4_levels_are_twice_e2m1():
         for c in range(8):
             assert v[c] == np.float32(2.0 ** (e - 127) * e2m1[c])
             assert v[16 + c] == np.float32(-(2.0 ** (e - 127)) * e2m1[c])
+
+
+LATTICE = {"iq2_xxs": (oracle.IQ2_XXS, 256), "iq2_xs": (oracle.IQ2_XS, 512), "iq2_s": (oracle.IQ2_S, 1024),
+           "iq3_xxs": (oracle.IQ3_XXS, 256), "iq3_s": (oracle.IQ3_S, 512), "iq1_s": (oracle.IQ1_S, 2048),
+           "iq1_m": (oracle.IQ1_M, 2048)}
+
+
+def _grid_points(t, b):
+    """The grid-point indices the blocks b [n][bytes] read (quant.h:95-115's index arithmetic)."""
+    b = b.astype(np.int64)
+    u16 = lambda o: b[:, o] | (b[:, o + 1] << 8)  # noqa: E731
+    if t == oracle.IQ2_XXS:
+        return b[:, 2:66].reshape(len(b), 8, 8)[:, :, :4].ravel()
+    if t == oracle.IQ2_XS:
+        return np.concatenate([u16(2 + 2 * k) & 511 for k in range(32)])
+    if t == oracle.IQ2_S:
+        return np.concatenate([b[:, 2 + k] + 256 * ((b[:, 66 + k // 4] >> (2 * (k % 4))) & 3) for k in range(32)])
+    if t == oracle.IQ3_XXS:
+        return b[:, 2:66].ravel()
+    if t == oracle.IQ3_S:
+        return np.concatenate([b[:, 2 + k] + 256 * ((b[:, 66 + k // 8] >> (k % 8)) & 1) for k in range(64)])
+    if t == oracle.IQ1_S:
+        return np.concatenate([b[:, 2 + k] + 256 * ((u16(34 + 2 * (k // 4)) >> (3 * (k % 4))) & 7) for k in range(32)])
+    return np.concatenate([b[:, k] + 256 * ((b[:, 32 + k // 2] >> (4 * (k % 2))) & 7) for k in range(32)])
+
+
+@pytest.mark.skipif(not oracle.ref_available(), reason="oracle/_ref not built (no reference checkout)")
+@pytest.mark.parametrize("name", list(LATTICE))
+def test_lattice_types_every_grid_point_against_reference_build(name):
+    """The lattice-grid types (quant.h:95-115) on random blocks (finite fp16 scales) that read every
+    point of their grid: bit-exact with the reference's own quant.h and quant_tables.h, which pins
+    both the decode and the packed grids it reads (iq_grids.h)."""
+    t, npts = LATTICE[name]
+    be, bb = oracle.block(t)
+    blocks = oracle.random_blocks(np.random.default_rng(300 + t), t, 3000)
+    assert len(np.unique(_grid_points(t, blocks))) == npts
+    got = oracle.dequant(blocks, t, 256)
+    want = oracle.ref_dequant(blocks, t, 256)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.all(np.isfinite(want))

@@ -116,7 +116,8 @@ def test_python_writer_copies_from_a_source_file(tmp_path):
         tq.write_tq(p, [("w", "Q4_K", 2, 256, (str(src), 1000, 280))], {})
 
 
-@pytest.mark.parametrize("name", ["q4_0", "q4_1", "q5_0", "q5_1", "q8_0", "q4_K", "q5_K", "q6_K"])
+@pytest.mark.parametrize("name", ["q4_0", "q4_1", "q5_0", "q5_1", "q8_0", "q4_K", "q5_K", "q6_K", "iq2_xxs", "iq2_xs",
+                                  "iq2_s", "iq3_xxs", "iq3_s", "iq1_s", "iq1_m"])
 def test_host_dequant_matches_reference_golden(golden, name):
     """tiermm_dequant_host against q_val values written by the reference's quant.h (fixtures)."""
     g = golden["dequant"]
@@ -183,7 +184,9 @@ def test_tq_check_metrics(tmp_path):
 
 @pytest.mark.parametrize("t", [tier_amd.Q8_0, tier_amd.Q5_0, tier_amd.Q4_K, tier_amd.Q5_K, tier_amd.Q6_K,
                                tier_amd.Q2_K, tier_amd.Q3_K, tier_amd.IQ4_NL, tier_amd.IQ4_XS, tier_amd.TQ1_0,
-                               tier_amd.TQ2_0, tier_amd.MXFP4, tier_amd.NF4, tier_amd.FP4])
+                               tier_amd.TQ2_0, tier_amd.MXFP4, tier_amd.NF4, tier_amd.FP4, tier_amd.IQ2_XXS,
+                               tier_amd.IQ2_XS, tier_amd.IQ2_S, tier_amd.IQ3_XXS, tier_amd.IQ3_S, tier_amd.IQ1_S,
+                               tier_amd.IQ1_M])
 def test_host_dequant_matches_oracle_on_random_blocks(t):
     import oracle
     rng = np.random.default_rng(100 + t)

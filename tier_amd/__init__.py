@@ -35,9 +35,10 @@ LIB_PATH = os.path.join(HERE, "libtiermm.so")
 OK, UNSUPPORTED, EINVAL = 0, 1, 2
 F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K, Q6_K, BF16 = 0, 1, 2, 3, 6, 7, 8, 12, 13, 14, 30
 Q2_K, Q3_K, IQ4_NL, IQ4_XS, TQ1_0, TQ2_0, MXFP4, NF4, FP4 = 10, 11, 20, 23, 34, 35, 39, 200, 201
-# the types the GPU kernels decode (dq_k / gemv_q over q_val; not the IQ2/IQ3/IQ1 lattice grids)
+IQ2_XXS, IQ2_XS, IQ3_XXS, IQ1_S, IQ3_S, IQ2_S, IQ1_M = 16, 17, 18, 19, 21, 22, 29
+# the types the GPU kernels decode (dq_k / gemv_q over q_val): every type of quant.h:21-24
 GPU_TYPES = (F32, F16, BF16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS, TQ1_0,
-             TQ2_0, MXFP4, NF4, FP4)
+             TQ2_0, MXFP4, NF4, FP4, IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M)
 OUT_F32, OUT_F16, OUT_BF16 = 0, 1, 2
 HML, LMH = 0, 1
 OP_N, OP_T = 111, 112
@@ -45,7 +46,8 @@ MODE_X3REF, MODE_F32 = 0, 1
 TYPE_NAMES = {F32: "f32", F16: "f16", BF16: "bf16", Q4_0: "q4_0", Q4_1: "q4_1", Q5_0: "q5_0", Q5_1: "q5_1",
               Q8_0: "q8_0", Q2_K: "q2_K", Q3_K: "q3_K", Q4_K: "q4_K", Q5_K: "q5_K", Q6_K: "q6_K",
               IQ4_NL: "iq4_nl", IQ4_XS: "iq4_xs", TQ1_0: "tq1_0", TQ2_0: "tq2_0", MXFP4: "mxfp4", NF4: "nf4",
-              FP4: "fp4"}
+              FP4: "fp4", IQ2_XXS: "iq2_xxs", IQ2_XS: "iq2_xs", IQ2_S: "iq2_s", IQ3_XXS: "iq3_xxs",
+              IQ3_S: "iq3_s", IQ1_S: "iq1_s", IQ1_M: "iq1_m"}
 
 # every symbol include/tiermm.h declares
 EXPORTS = (

@@ -141,7 +141,9 @@ bool gpu_type(int qtype) {
   switch (qtype) {
     case QT_F32: case QT_F16: case QT_BF16: case QT_Q4_0: case QT_Q4_1: case QT_Q5_0: case QT_Q5_1:
     case QT_Q8_0: case QT_Q2_K: case QT_Q3_K: case QT_Q4_K: case QT_Q5_K: case QT_Q6_K: case QT_IQ4_NL:
-    case QT_IQ4_XS: case QT_TQ1_0: case QT_TQ2_0: case QT_MXFP4: case QT_NF4: case QT_FP4: return true;
+    case QT_IQ4_XS: case QT_TQ1_0: case QT_TQ2_0: case QT_MXFP4: case QT_NF4: case QT_FP4:
+    case QT_IQ2_XXS: case QT_IQ2_XS: case QT_IQ2_S: case QT_IQ3_XXS: case QT_IQ3_S: case QT_IQ1_S:
+    case QT_IQ1_M: return true;
     default: return false;
   }
 }

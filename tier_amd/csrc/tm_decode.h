@@ -15,6 +15,7 @@
 #include <cstdint>
 #include <type_traits>
 
+#include "iq_grids.h"
 #include "tm_host.h"
 
 #define TM_HD __host__ __device__ __forceinline__
@@ -389,6 +390,125 @@ struct Dec<QT_TQ1_0> {  // quant.h:117-119 -- 54-byte super-blocks: base-3 packe
   }
 };
 
+// ---- lattice-grid types (quant.h:95-115).  A grid point holds 8 (IQ2, IQ1) or 4
+// (IQ3) element magnitudes, packed as codes in iq_grids.h; signs come from a
+// 7-bit index whose parity gives the eighth bit (ksigns) or from a byte.  Every
+// product is exact in fp32 (fp16 scale times at most 5 + 6 bits), so the values
+// do not depend on the order of the multiplications.
+TM_HD float iq2_level(uint32_t c) { return c == 0 ? 8.f : c == 1 ? 25.f : 43.f; }
+TM_HD float iq3xxs_level(uint32_t c) { return c == 7 ? 62.f : (float)(8 * c + 4); }
+TM_HD uint32_t iq_ksign(uint32_t i) { return i | ((uint32_t)(__builtin_popcount(i) & 1) << 7); }
+TM_HD float iq_sign(uint32_t s, int e) { return (s >> e) & 1u ? -1.f : 1.f; }
+
+template <>
+struct Dec<QT_IQ2_XXS> {  // quant.h:95-97 -- 66 bytes: d, 8 x (4 grid bytes, 4 sign/scale bytes)
+  static constexpr int BLK = 256, BYTES = 66;
+  TM_HD static void run(const uint8_t* row, int c, float v[8]) {
+    const uint8_t* b = row + (size_t)(c >> 8) * 66;
+    const int i0 = c & 255, g = i0 >> 5, k = (i0 & 31) >> 3;
+    const uint32_t a0 = ld_u32_a2(b + 2 + 8 * g), a1 = ld_u32_a2(b + 6 + 8 * g);
+    const float db = h2f(ld_u16(b)) * (0.5f + (float)(a1 >> 28)) * 0.25f;
+    const uint32_t w = tm_iq2xxs_grid[(a0 >> (8 * k)) & 255u], sg = iq_ksign((a1 >> (7 * k)) & 127u);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = db * iq2_level((w >> (2 * e)) & 3u) * iq_sign(sg, e);
+  }
+};
+
+template <>
+struct Dec<QT_IQ2_XS> {  // quant.h:98-100 -- 74 bytes: d, 32 x u16 (9-bit point, 7-bit sign index), 8 scale bytes
+  static constexpr int BLK = 256, BYTES = 74;
+  TM_HD static void run(const uint8_t* row, int c, float v[8]) {
+    const uint8_t* b = row + (size_t)(c >> 8) * 74;
+    const int i0 = c & 255, k = i0 >> 3, s = i0 >> 4;
+    const uint32_t q = ld_u16(b + 2 + 2 * k);
+    const float db = h2f(ld_u16(b)) * (0.5f + (float)((b[66 + (s >> 1)] >> (4 * (s & 1))) & 15)) * 0.25f;
+    const uint32_t w = tm_iq2xs_grid[q & 511u], sg = iq_ksign(q >> 9);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = db * iq2_level((w >> (2 * e)) & 3u) * iq_sign(sg, e);
+  }
+};
+
+template <>
+struct Dec<QT_IQ2_S> {  // quant.h:101-103 -- 82 bytes: d, 32 point bytes, 32 sign bytes, 8 high-bit bytes, 8 scales
+  static constexpr int BLK = 256, BYTES = 82;
+  TM_HD static void run(const uint8_t* row, int c, float v[8]) {
+    const uint8_t* b = row + (size_t)(c >> 8) * 82;
+    const int i0 = c & 255, k = i0 >> 3, s = i0 >> 4;
+    const float db = h2f(ld_u16(b)) * (0.5f + (float)((b[74 + (s >> 1)] >> (4 * (s & 1))) & 15)) * 0.25f;
+    const uint32_t gi = b[2 + k] | (((uint32_t)(b[66 + (k >> 2)] >> (2 * (k & 3))) & 3u) << 8);
+    const uint32_t w = tm_iq2s_grid[gi], sg = b[34 + k];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = db * iq2_level((w >> (2 * e)) & 3u) * iq_sign(sg, e);
+  }
+};
+
+template <>
+struct Dec<QT_IQ3_XXS> {  // quant.h:104-106 -- 98 bytes: d, 64 point bytes, 8 x u32 (4 sign indices, scale)
+  static constexpr int BLK = 256, BYTES = 98;
+  TM_HD static void run(const uint8_t* row, int c, float v[8]) {
+    const uint8_t* b = row + (size_t)(c >> 8) * 98;
+    const int i0 = c & 255, g = i0 >> 5, k = (i0 & 31) >> 3;
+    const uint32_t sw = ld_u32_a2(b + 66 + 4 * g);
+    const float db = h2f(ld_u16(b)) * (0.5f + (float)(sw >> 28)) * 0.5f;
+    const uint32_t sg = iq_ksign((sw >> (7 * k)) & 127u);
+    const uint32_t w0 = tm_iq3xxs_grid[b[2 + (i0 >> 2)]], w1 = tm_iq3xxs_grid[b[3 + (i0 >> 2)]];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = db * iq3xxs_level(((e < 4 ? w0 : w1) >> (3 * (e & 3))) & 7u) * iq_sign(sg, e);
+  }
+};
+
+template <>
+struct Dec<QT_IQ3_S> {  // quant.h:107-109 -- 110 bytes: d, 64 point bytes, 8 high-bit bytes, 32 sign bytes, 4 scales
+  static constexpr int BLK = 256, BYTES = 110;
+  TM_HD static void run(const uint8_t* row, int c, float v[8]) {
+    const uint8_t* b = row + (size_t)(c >> 8) * 110;
+    const int i0 = c & 255, g = i0 >> 5, k0 = i0 >> 2;
+    const float db = h2f(ld_u16(b)) * (float)(1 + 2 * ((b[106 + (g >> 1)] >> (4 * (g & 1))) & 15));
+    uint32_t w[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int k = k0 + j;
+      w[j] = tm_iq3s_grid[b[2 + k] | (((uint32_t)(b[66 + (k >> 3)] >> (k & 7)) & 1u) << 8)];
+    }
+    const uint32_t sg = b[74 + (i0 >> 3)];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = db * (float)(2 * ((w[e >> 2] >> (3 * (e & 3))) & 7u) + 1) * iq_sign(sg, e);
+  }
+};
+
+template <>
+struct Dec<QT_IQ1_S> {  // quant.h:110-112 -- 50 bytes: d, 32 point bytes, 8 x u16 (high bits, scale, delta sign)
+  static constexpr int BLK = 256, BYTES = 50;
+  TM_HD static void run(const uint8_t* row, int c, float v[8]) {
+    const uint8_t* b = row + (size_t)(c >> 8) * 50;
+    const int i0 = c & 255, g = i0 >> 5, k = i0 >> 3;
+    const uint32_t qh = ld_u16(b + 34 + 2 * g);
+    const float dl = h2f(ld_u16(b)) * (float)(2 * ((qh >> 12) & 7) + 1);
+    const float dt = (qh & 0x8000u) ? -0.125f : 0.125f;
+    const uint32_t w = tm_iq1s_grid[b[2 + k] | (((qh >> (3 * (k & 3))) & 7u) << 8)];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = dl * ((float)((int)((w >> (2 * e)) & 3u) - 1) + dt);
+  }
+};
+
+template <>
+struct Dec<QT_IQ1_M> {  // quant.h:113-115 -- 56 bytes: 32 point bytes, 16 high-bit nibbles, 4 x u16 scales (+ fp16 d in their top nibbles)
+  static constexpr int BLK = 256, BYTES = 56;
+  TM_HD static void run(const uint8_t* row, int c, float v[8]) {
+    const uint8_t* b = row + (size_t)(c >> 8) * 56;
+    const uint8_t* sc = b + 48;
+    const int i0 = c & 255, k = i0 >> 3, s = i0 >> 4;
+    const uint32_t s0 = ld_u16(sc), s1 = ld_u16(sc + 2), s2 = ld_u16(sc + 4), s3 = ld_u16(sc + 6);
+    const uint32_t dh = (s0 >> 12) | ((s1 & 0xf000u) >> 8) | ((s2 & 0xf000u) >> 4) | (s3 & 0xf000u);
+    const float dl = h2f(dh) * (float)(2 * ((ld_u16(sc + 2 * (s >> 2)) >> (3 * (s & 3))) & 7) + 1);
+    const uint32_t qh = (b[32 + (k >> 1)] >> (4 * (k & 1))) & 15u;
+    const float dt = (qh & 8u) ? -0.125f : 0.125f;
+    const uint32_t w = tm_iq1s_grid[b[k] | ((qh & 7u) << 8)];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = dl * ((float)((int)((w >> (2 * e)) & 3u) - 1) + dt);
+  }
+};
+
 // One element of a dense row (q_val's F32 / F16 / BF16 cases, quant.h:61-63), for
 // rows whose length is not a whole number of 8-element chunks.
 template <int QT>
@@ -423,6 +543,13 @@ inline auto with_qtype(int qtype, F&& f) {
     case QT_MXFP4: return f(std::integral_constant<int, QT_MXFP4>{});
     case QT_NF4: return f(std::integral_constant<int, QT_NF4>{});
     case QT_FP4: return f(std::integral_constant<int, QT_FP4>{});
+    case QT_IQ2_XXS: return f(std::integral_constant<int, QT_IQ2_XXS>{});
+    case QT_IQ2_XS: return f(std::integral_constant<int, QT_IQ2_XS>{});
+    case QT_IQ2_S: return f(std::integral_constant<int, QT_IQ2_S>{});
+    case QT_IQ3_XXS: return f(std::integral_constant<int, QT_IQ3_XXS>{});
+    case QT_IQ3_S: return f(std::integral_constant<int, QT_IQ3_S>{});
+    case QT_IQ1_S: return f(std::integral_constant<int, QT_IQ1_S>{});
+    case QT_IQ1_M: return f(std::integral_constant<int, QT_IQ1_M>{});
     default: return f(std::integral_constant<int, QT_Q6_K>{});
   }
 }

@@ -12,7 +12,8 @@ namespace tiermm {
 enum : int {
   QT_F32 = 0, QT_F16 = 1, QT_Q4_0 = 2, QT_Q4_1 = 3, QT_Q5_0 = 6, QT_Q5_1 = 7, QT_Q8_0 = 8,
   QT_Q2_K = 10, QT_Q3_K = 11, QT_Q4_K = 12, QT_Q5_K = 13, QT_Q6_K = 14, QT_IQ4_NL = 20, QT_IQ4_XS = 23,
-  QT_BF16 = 30, QT_TQ1_0 = 34, QT_TQ2_0 = 35, QT_MXFP4 = 39, QT_NF4 = 200, QT_FP4 = 201
+  QT_BF16 = 30, QT_TQ1_0 = 34, QT_TQ2_0 = 35, QT_MXFP4 = 39, QT_NF4 = 200, QT_FP4 = 201,
+  QT_IQ2_XXS = 16, QT_IQ2_XS = 17, QT_IQ3_XXS = 18, QT_IQ1_S = 19, QT_IQ3_S = 21, QT_IQ2_S = 22, QT_IQ1_M = 29
 };
 
 struct BlockInfo {
