@@ -9,18 +9,25 @@
 // consecutive tiles, and it streams them one after another.  A tile is cut
 // into stages of GS super-blocks: each of the 4 producer waves (one per SIMD)
 // brings 4 of the 16 rows (4 row segments of GS*144 bytes) into a ring of NS
-// slots of its own with global_load_lds_dwordx4, D stages ahead.  Long row
-// segments and few concurrent tiles measured faster than 16 short segments
-// per wave from 864 tiles at once (13824x5120: 8.9 against 9.2 us; 10240x8192:
-// 10.4 against 11.8 us).  The loads carry the non-temporal hint: every weight
-// byte is read once (13824x5120: 8.9-9.2 against 9.3-9.5 us; 10240x8192: 10.2
-// against 10.7 us).
+// slots of its own with global_load_lds_dwordx4; while it waits for stage q - D
+// to land, stages q - D .. q are in flight.  Long row segments and few
+// concurrent tiles measured faster than 16 short segments per wave from 864
+// tiles at once (13824x5120: 8.9 against 9.2 us; 10240x8192: 10.4 against
+// 11.8 us).  Up to K = 5120 a stage is the whole tile (a contiguous 16-row
+// span) with one more tile in flight: 13824x5120 8.55-8.57 against 8.86-9.02 us
+// for 12-super-block stages two deep, 14336x4096 7.71 against 8.34 us.  Deeper
+// rings measured slower in every geometry tried (whole tiles two ahead: 9.74 us).
+// The loads carry the non-temporal hint: every weight byte is read once
+// (13824x5120: 8.9-9.2 against 9.3-9.5 us; 10240x8192: 10.2 against 10.7 us).
 //
-// Consumers.  GS == NC: consumer c owns super-block column c of every stage,
-// i.e. columns c, c + NC, ... of every row, so the x digits and the x metadata
-// it needs sit in its registers from the start (MS columns) and its LDS reads
-// are the weight bytes alone.  Its partial sum of each tile goes to LDS; after
-// the last tile the workgroup adds the NC partials of each row in a fixed order.
+// Consumers.  Consumer c owns super-block columns c, c + NC, ... < GS of every
+// stage (CPS of them), so the x digits and the x metadata it needs sit in its
+// registers from the start (MS columns) and its LDS reads are the weight bytes
+// alone.  8 consumers with 4 producers (3 waves per SIMD) measured faster than
+// 4-12 consumers in other counts (13824x5120, whole-tile stages: 8.54 against
+// 8.63-9.11 us).  Its partial sum of each tile stays in a register until the
+// last stage is consumed; then the ring holds the partials and the workgroup
+// adds the NC partials of each row in a fixed order.
 //
 // Hand-off through LDS flags holding stage numbers, which only grow:
 //   full[slot][p] = q  -- producer p's rows of stage q have landed (its own
@@ -70,28 +77,32 @@ __device__ __forceinline__ void poll_ge(const int* f, int v) {
   asm volatile("" ::: "memory");
 }
 
-template <int QT, int NC, int NS, int R>
+template <int QT, int GS_, int NC, int NS, int R>
 struct WsLayout {
-  static constexpr int GS = NC;                                 // super-blocks per stage
+  static constexpr int GS = GS_;                                // super-blocks per stage
+  static constexpr int CPS = (GS + NC - 1) / NC;                // columns per consumer per stage
   static constexpr int GRP = GS * MfmaFmt<QT>::SBB;             // one row's segment
   static constexpr int SLOT = PROWS * GRP;                      // one producer's part of a stage
   static constexpr int NLD = (SLOT + 1023) / 1024;              // 1 KiB loads per part
   static constexpr int LAST = (SLOT - (NLD - 1) * 1024) / 16;   // lanes of the last load
   static constexpr int NCP = pad4(NC);
   static constexpr size_t RING = (size_t)NP * NS * SLOT;
-  static constexpr size_t LDS = RING + NS * NP * 4 + NS * NCP * 4 + (size_t)R * NC * 16 * 4;
+  static constexpr size_t LDS = RING + NS * NP * 4 + NS * NCP * 4;
+  // the per-tile partial sums reuse the ring once every stage has been consumed
+  static_assert((size_t)R * NC * 16 * 4 <= RING, "partial sums fit in the ring");
 };
 
-template <int QT, int R, int NC, int NS, int D, int XP, int XK>
+template <int QT, int R, int GS_, int NC, int NS, int D, int XP, int XK>
 __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __restrict__ W, size_t rb,
                                                             const float* __restrict__ x, float* __restrict__ y,
                                                             int N, int K) {
-  using L = WsLayout<QT, NC, NS, R>;
+  using L = WsLayout<QT, GS_, NC, NS, R>;
   constexpr int SBB = MfmaFmt<QT>::SBB;
-  constexpr int GS = L::GS, GRP = L::GRP, SLOT = L::SLOT, NLD = L::NLD, NCP = L::NCP;
-  constexpr int MS = (XK / 256 + GS - 1) / GS;  // super-block columns per consumer
+  constexpr int GS = L::GS, CPS = L::CPS, GRP = L::GRP, SLOT = L::SLOT, NLD = L::NLD, NCP = L::NCP;
+  constexpr int MG = (XK / 256 + GS - 1) / GS;  // stages per tile, at most
+  constexpr int MS = MG * CPS;                  // super-block columns per consumer
   static_assert(NLD * D <= 63, "vmcnt counts at most 63 loads");
-  static_assert(D >= 1 && NS > D, "ring deeper than the stages in flight");
+  static_assert(D >= 0 && NS > D, "ring deeper than the stages in flight");
   static_assert(NC + NP <= 16, "at most 1024 threads per workgroup");
   static_assert(SLOT % 16 == 0, "16-byte aligned slots");
   extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // L::LDS bytes
@@ -99,7 +110,7 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
   __shared__ int nf[NC];               // per consumer: x held a non-finite value
   int* full = (int*)(ring + L::RING);  // [NS][NP]
   int* done = full + NS * NP;          // [NS][NCP]
-  float* red = (float*)(done + NS * NCP);  // [R][NC][16]
+  float* red = (float*)ring;           // [R][NC][16], after the last stage
   const int nsb = K >> 8, ngrp = (nsb + GS - 1) / GS, total = R * ngrp;
   const int tiles = (N + 15) >> 4;
   uint8_t* xq = xlds;
@@ -150,6 +161,7 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
     vm_wait<0>();
     for (; marked < total; ++marked)
       if (lane == 0) lds_rel(&full[NP * (marked % NS) + p], marked);
+    __syncthreads();  // every stage consumed: the ring is free
     __syncthreads();  // partial sums are in red[]
   } else {
     // -------------------------------------------------------------- consumers
@@ -180,12 +192,13 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
     }
     publish_nonfinite(bad, nf, c, lane);
     __syncthreads();
-    // this lane's A operands of its columns c + GS*m (zeros where it carries no digit)
+    // this lane's A operands of its columns GS*gi + c + NC*i, m = gi*CPS + i
+    // (zeros where it carries no digit)
     i32x4 A[MS][4];
     float4 mt[MS];
 #pragma unroll
     for (int m = 0; m < MS; ++m) {
-      const int sb = min(GS * m + c, nsb - 1);
+      const int sb = min(GS * (m / CPS) + c + NC * (m % CPS), nsb - 1);
       uint32_t off[2];
 #pragma unroll
       for (int pp = 0; pp < 2; ++pp)
@@ -199,23 +212,33 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
     }
     // row n of a stage: producer n / 4's slot, row n % 4 of it; column c
     const uint8_t* rowbase = ring + (n / PROWS) * NS * SLOT + (n % PROWS) * GRP + c * SBB;
+    float part[R];  // this consumer's sum of row n of each tile (lanes g == 0)
+#pragma unroll
     for (int r = 0; r < R; ++r) {
       float acc = 0.f;
 #pragma unroll
-      for (int gi = 0; gi < MS; ++gi) {
+      for (int gi = 0; gi < MG; ++gi) {
         if (gi < ngrp) {
           const int q = r * ngrp + gi, slot = q % NS;
           if (GS * gi + c < nsb) {
             poll_ge<NP>(full + NP * slot, q);
-            acc = MfmaFmt<QT>::step_reg(rowbase + slot * SLOT, g, A[gi], mt[gi], acc);
+#pragma unroll
+            for (int i = 0; i < CPS; ++i)
+              if (c + NC * i < GS && GS * gi + c + NC * i < nsb)
+                acc = MfmaFmt<QT>::step_reg(rowbase + slot * SLOT + NC * i * SBB, g, A[gi * CPS + i],
+                                            mt[gi * CPS + i], acc);
           }
           if (lane == 0) lds_rel(&done[slot * NCP + c], q);
         }
       }
       acc += __shfl_xor(acc, 16, 64);
       acc += __shfl_xor(acc, 32, 64);
-      if (g == 0) red[(r * NC + c) * 16 + n] = acc;
+      part[r] = acc;
     }
+    __syncthreads();  // every stage consumed: the ring is free
+    if (g == 0)
+#pragma unroll
+      for (int r = 0; r < R; ++r) red[(r * NC + c) * 16 + n] = part[r];
     __syncthreads();
   }
   if (flags_any(nf, NC)) {  // NaN or +-Inf in x: the rows take gemv_q's non-finite sums
@@ -241,41 +264,44 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
   }
 }
 
-template <int QT, int R, int NC, int NS, int D, int XP, int XK>
+template <int QT, int R, int GS, int NC, int NS, int D, int XP, int XK>
 int launch_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
-  using L = WsLayout<QT, NC, NS, R>;
+  using L = WsLayout<QT, GS, NC, NS, R>;
   static_assert(xq_bytes(XK) + 4 * NC + L::LDS <= 160 * 1024, "LDS budget (x digits, flags, ring)");
   static_assert(XK / 16 <= 64 * NC * XP, "x preparation: one thread per 16 elements");
   const int tiles = (N + 15) / 16;
   const unsigned grid = (unsigned)((tiles + R - 1) / R);
   static std::atomic<uint64_t> attr{0};
-  int st = lds_attr_once(attr, (const void*)qgemv_q4k_ws<QT, R, NC, NS, D, XP, XK>, (int)L::LDS,
+  int st = lds_attr_once(attr, (const void*)qgemv_q4k_ws<QT, R, GS, NC, NS, D, XP, XK>, (int)L::LDS,
                          "tiermm_qgemv: q4_K LDS attribute");
   if (st) return st;
-  qgemv_q4k_ws<QT, R, NC, NS, D, XP, XK><<<grid, 64 * (NC + NP), L::LDS, s>>>((const uint8_t*)W, rb, x, y, N, K);
+  qgemv_q4k_ws<QT, R, GS, NC, NS, D, XP, XK><<<grid, 64 * (NC + NP), L::LDS, s>>>((const uint8_t*)W, rb, x, y, N, K);
   TM_LAUNCH_CHECK("tiermm_qgemv: q4_K launch");
   return TIERMM_OK;
 }
 
-template <int QT, int NC, int NS, int D, int XP, int XK>
+template <int QT, int GS, int NC, int NS, int D, int XP, int XK>
 int launch_ws_r(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
   const int tiles = (N + 15) / 16, r = (tiles + GTILE - 1) / GTILE;
-  if (r <= 3) return launch_ws<QT, 3, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
-  if (r == 4) return launch_ws<QT, 4, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
-  if (r == 5) return launch_ws<QT, 5, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
-  if (r == 6) return launch_ws<QT, 6, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
-  return launch_ws<QT, 8, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
+  if (r <= 3) return launch_ws<QT, 3, GS, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
+  if (r == 4) return launch_ws<QT, 4, GS, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
+  if (r == 5) return launch_ws<QT, 5, GS, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
+  if (r == 6) return launch_ws<QT, 6, GS, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
+  return launch_ws<QT, 8, GS, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
 }
 
 }  // namespace
 
 // Tall matrices (at least 640 row tiles).  Tiles per workgroup: the grid lands
 // near 224 workgroups (a uniform count per workgroup measured faster than a
-// ragged one).  Stages of 12 super-blocks up to K = 5120 (x digits of two
-// columns per consumer), of 8 up to 8192 (four columns).
+// ragged one).  Up to K = 5120 whole-tile stages of 20 super-blocks (shorter
+// rows re-read their last 16 bytes to fill the fixed load count; still the
+// fastest at K = 4096), 8 consumers with up to 3 columns each; up to 8192
+// stages of 8 super-blocks (whole-tile and 16-super-block stages measured
+// slower there: 10240x8192 10.8 against 10.1 us).
 int qgemv_q4k_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
-  if (K <= 5120) return launch_ws_r<QT_Q4_K, 12, 4, 2, 1, 5120>(W, rb, x, y, N, K, s);
-  if (K <= 8192) return launch_ws_r<QT_Q4_K, 8, 4, 2, 1, 8192>(W, rb, x, y, N, K, s);
+  if (K <= 5120) return launch_ws_r<QT_Q4_K, 20, 8, 3, 1, 1, 5120>(W, rb, x, y, N, K, s);
+  if (K <= 8192) return launch_ws_r<QT_Q4_K, 8, 8, 4, 2, 1, 8192>(W, rb, x, y, N, K, s);
   return set_error(TIERMM_UNSUPPORTED, "tiermm_qgemv: q4_K K=%d above %d", K, 8192);
 }
 
@@ -285,8 +311,8 @@ int qgemv_q4k_ws(const void* W, size_t rb, const float* x, float* y, int N, int 
 // groups) gained nothing this way (a 3-slot ring: 17.5 against 17.1 us at
 // 13824x5120, 36.6 against 22.2 us at 10240x8192) and keeps the per-wave kernel.
 int qgemv_q5k_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
-  if (K <= 5120) return launch_ws_r<QT_Q5_K, 10, 4, 2, 1, 5120>(W, rb, x, y, N, K, s);
-  if (K <= 8192) return launch_ws_r<QT_Q5_K, 8, 4, 2, 1, 8192>(W, rb, x, y, N, K, s);
+  if (K <= 5120) return launch_ws_r<QT_Q5_K, 10, 10, 4, 2, 1, 5120>(W, rb, x, y, N, K, s);
+  if (K <= 8192) return launch_ws_r<QT_Q5_K, 8, 8, 4, 2, 1, 8192>(W, rb, x, y, N, K, s);
   return set_error(TIERMM_UNSUPPORTED, "tiermm_qgemv: q5_K K=%d above %d", K, 8192);
 }
 
