@@ -199,6 +199,51 @@ def test_qgemm_q4k_fused_shapes(gpu, M, N, K, beta):
     assert oracle.rel_fro(got, ref) <= BAR
 
 
+@pytest.mark.parametrize("bn", [160, 128, 64])
+@pytest.mark.parametrize("sigma", [0.02, 60.0, 2e-6])
+def test_qgemm_q4k_fused_decode_bit_exact(gpu, monkeypatch, bn, sigma):
+    """One-hot rows of x read the fused kernel's fp16 weights back: row m of x is e_m, so
+    Y[m][n] = W16[n][m] exactly (one non-zero product per sum).  This pins the in-kernel
+    decode -- q_val with one rounding, then fp16 round-to-nearest-even -- bit for bit
+    against the oracle, for each decode layout (one lane per row at BN = 160, two at
+    BN <= 128), with weights from fp16 subnormals up to values in the thousands."""
+    monkeypatch.setenv("TIERMM_QGEMM_TILE", f"{bn},1")
+    t, N, K = tier_amd.Q4_K, 352, 512
+    blocks = quantized_weight(t, N, K, seed=46, sigma=sigma)
+    x = np.eye(K, dtype=np.float32)
+    W, X, Y = hip.to_device(blocks), hip.to_device(x), hip.DeviceBuffer(K * N * 4)
+    tier_amd.qgemm(W.ptr, t, tier_amd.q_row_bytes(t, K), X.ptr, Y.ptr, K, N, K)
+    hip.synchronize()
+    got = Y.download(np.float32, K * N).reshape(K, N)
+    w16 = oracle.h2f(oracle.dequant(blocks, t, K, oracle.OUT_F16)).reshape(N, K)
+    assert np.all(np.isfinite(w16)) and np.count_nonzero(w16) > 0
+    assert np.array_equal(got, w16.T)  # +0 and -0 compare equal: a zero weight sums to +0
+
+
+@pytest.mark.parametrize("M,N,K", [(130, 100, 768), (512, 1000, 2048)])
+def test_qgemm_q4k_fused_x_layouts(gpu, M, N, K):
+    """x at a 16-byte aligned address is split into K-tiled planes, x 4 bytes past one
+    into row-major planes: the fused q4_K kernel gives bit-identical results from both,
+    within the fp64 bar."""
+    t = tier_amd.Q4_K
+    rng = np.random.default_rng(3 * M + N)
+    blocks = oracle.random_blocks(rng, t, N * (K // 256)).reshape(N, -1)
+    x = activations(M, K, seed=24)
+    W, X = hip.to_device(blocks), hip.to_device(x)
+    Xu = hip.DeviceBuffer(M * K * 4 + 16)
+    Xu.upload(x, offset=4)
+    Y, Yu = hip.DeviceBuffer(M * N * 4), hip.DeviceBuffer(M * N * 4)
+    rb = tier_amd.q_row_bytes(t, K)
+    tier_amd.qgemm(W.ptr, t, rb, X.ptr, Y.ptr, M, N, K)
+    tier_amd.qgemm(W.ptr, t, rb, Xu.ptr + 4, Yu.ptr, M, N, K)
+    hip.synchronize()
+    got = Y.download(np.float32, M * N).reshape(M, N)
+    got_u = Yu.download(np.float32, M * N).reshape(M, N)
+    assert np.array_equal(got.view(np.uint32), got_u.view(np.uint32))
+    w16 = oracle.h2f(oracle.dequant(blocks, t, K, oracle.OUT_F16)).reshape(N, K)
+    assert oracle.rel_fro(got, x.astype(np.float64) @ w16.astype(np.float64).T) <= BAR
+
+
 @pytest.mark.parametrize("bn,ks", [(160, 1), (160, 2), (160, 4), (128, 2), (112, 4), (96, 2), (80, 4), (64, 2),
                                    (64, 1)])
 @pytest.mark.parametrize("M,N,K,beta", [(300, 1000, 1024, 1.0), (512, 352, 2048, 0.0)])

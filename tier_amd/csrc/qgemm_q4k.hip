@@ -20,20 +20,27 @@
 //     the pre-split x planes straight into a ring of registers, three stages
 //     ahead -- each consumer reads only its rows, so staging x in LDS would buy
 //     no reuse;
-//   * producer p streams the raw bytes (super-block header and the qs chunk of
-//     the sub-block) of W rows [p*BN/4, (p+1)*BN/4) through a ring of LDS slots
-//     with global_load_lds_dwordx4, six stages ahead, and decodes each row's 32
-//     elements exactly as q_val (d*sc*q - dmin*m, one rounding), rounded to fp16
-//     (v_cvt, RNE), into the B ring.
+//   * producer p decodes W rows [p*BN/4, (p+1)*BN/4) into a ring of four B
+//     stages in LDS.  It works a sub-block pair at a time (two K steps share
+//     their 32 qs bytes: low nibbles, then high nibbles), loading each row's
+//     super-block header and qs bytes into registers four pairs ahead, and
+//     decodes each element exactly as q_val (d*sc*q - dmin*m, one rounding),
+//     rounded to fp16 (RNE, two elements per v_cvt_pk_f16_f32).  Bytes widen
+//     with one mask and convert with v_cvt_f32_ubyte<n>: 2.75 VALU ops per
+//     element.
 // LDS rows hold 32 halfs as four 16-byte chunks, chunk c at slot
 // c ^ ((row >> 2) & 3), so the fragment reads (16 rows x 4 chunks) hit
-// distinct bank groups.
+// distinct bank groups.  x comes in K-tiled planes (ktile_index) where the
+// caller's x allows it, so a fragment load is one contiguous kilobyte.
 //
-// Measured (512x5120x5120 .. 512x5120x14336, bit-identical to the barrier form
-// this replaced): 8-18 % faster.  Timing copies with parts switched off show
-// the consumers' x loads as the largest single cost (consumers alone: 125 us
-// with them, 57 us without, 122 us with every load hitting one cached address),
-// i.e. the vector-memory instructions themselves, not their latency.
+// Measured, M = 512 (bench.py lines; x split and split-K reduce included):
+// 5120x5120 81 us, 14336x5120 195 us, 5120x14336 204 us, against 97-100,
+// 224-234 and 246-254 us when the producers streamed raw bytes through an LDS
+// ring by DMA and decoded a stage at a time (one lane per half row, two passes
+// at BN = 160).  Cycle counters in a timing copy showed that decoder at ~1450
+// cycles per K step, 70 % of the producer's time, with the consumers waiting
+// on it for 26 % of theirs; with the register-fed pair decoder the consumers
+// wait 9 % and the MFMA issue is the larger part of their K step.
 #include <cstdio>
 #include <cstdlib>
 
@@ -46,9 +53,11 @@ int device_cus(int* cus);
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 
 constexpr int QBM = 128, QBK = 32;
+constexpr int QNBR = 4;  // decoded B stages in the LDS ring
 
 // A launch covers up to QG groups (one plain GEMM, or the experts of a routed
 // batch): group g multiplies rows [row0[g], row0[g] + rows[g]) of X and Y with
@@ -57,6 +66,7 @@ constexpr int QG = 64;
 struct QArgs {
   const uint16_t* X;  // parts at X, X + xs, X + 2 xs (hi, mid, lo), rows of K halfs
   size_t xs;
+  size_t xt;          // > 0: the planes are K-tiled (ktile_index) over xt rows
   float* Y;
   size_t rb;
   int ldy, N, K;
@@ -94,27 +104,25 @@ __device__ __forceinline__ void poll4(const int* f, int v) {
 // Flags (stage numbers, slot-major so that one poll reads all four):
 //   ready[q % FL][p] = q -- producer p's B rows of stage q are stored;
 //   done[q % FL][c] = q  -- consumer c has read stage q's B tile.
-// Stage q's B tile is slot q % NBR; producer p's raw bytes of stage q are its
-// slot q % RR.  Producer p loads stage q + DR in its iteration q (that slot held
-// stage q + DR - RR, which it has decoded) and decodes stage q once every
-// consumer has read stage q - NBR (the slot's previous user).  That is a stage
-// below q, whose ready every producer has published, so each wait ends; a
-// consumer waits only for its own loads and for ready.
+// Stage q's B tile is slot q % NBR.  Producer p decodes the pair of stages q,
+// q + 1 once every consumer has read stage q + 1 - NBR (the later slot's
+// previous user, and so the earlier's too).  That stage is below q, its ready
+// published by every producer, so each wait ends; a consumer waits only for
+// its own loads and for ready.
 template <int BN, int KS>
 __global__ __launch_bounds__(512) void qgemm_q4k_x3ref(const QArgs p) {
   constexpr int NB = BN / 16;
-  constexpr int NBR = 3, FL = 4, XR = 4, RR = 8, DR = 6;
+  constexpr int NBR = QNBR, FL = 4, XR = 4, DP = 4;
   constexpr int PR = BN / 4;
-  constexpr int RAWP = PR * 48;
-  constexpr int RAWI = (RAWP + 1023) / 1024, RSLOT = RAWI * 1024;
+  constexpr int LPR = 2 * PR <= 64 ? 2 : 1, HPL = 2 / LPR;  // decode: lanes per row, halves per lane
+  constexpr int NL = 1 + HPL;                                // producer loads per sub-block pair
   constexpr int BPART = BN * 64;
-  constexpr int RAWOFF = NBR * BPART;
-  constexpr int FLAGOFF = RAWOFF + 4 * RR * RSLOT;
+  constexpr int FLAGOFF = NBR * BPART;
   static_assert(BN % 16 == 0 && BN <= 160, "tile width");
-  static_assert(NBR <= FL && DR < RR && RAWI * DR <= 63, "ring depths");
+  static_assert(LPR * PR <= 64, "one decode pass per producer");
+  static_assert(NBR <= FL && NBR >= 3 && NL * DP <= 63, "ring depths");
   extern __shared__ __attribute__((aligned(16))) uint16_t lds_h[];
   uint8_t* lds = (uint8_t*)lds_h;
-  const uint32_t lds0 = lds_addr(lds);
   int* ready = (int*)(lds + FLAGOFF);  // [FL][4]: slot-major, one 16-byte read per poll
   int* done = ready + 4 * FL;          // [FL][4]
   const int tid = threadIdx.x, lane = tid & 63;
@@ -141,59 +149,76 @@ __global__ __launch_bounds__(512) void qgemm_q4k_x3ref(const QArgs p) {
 
   if (wave >= 4) {
     // ------------------------------------------------------------ producer
+    // LPR lanes per row of the producer's PR, each decoding HPL halves of 16
+    // elements.  A sub-block pair (K steps q, q + 1 with q even) shares its 32 qs
+    // bytes: low nibbles for q, high nibbles for q + 1.  Per pair a lane loads the
+    // super-block header and its qs half (or halves) into registers, DP pairs ahead.
     const int pw = wave - 4;
-    const uint8_t* rsrc[RAWI];
-    int rkind[RAWI];
+    const bool act = lane < LPR * PR;
+    const int dr = min(lane / LPR, PR - 1), h0 = (lane % LPR) * HPL;
+    const int r = pw * PR + dr;
+    const uint8_t* rowp = Wg + (size_t)min(n0 + r, p.N - 1) * p.rb;
+    const int np = nk / 2;  // pairs of this split (a multiple of 4)
+    u32x4 Hr[DP], Qr[DP][HPL];
+    // pair j into register slot u (j >= np: pair np - 1 again, so every pair issues NL loads)
+    auto issue = [&](int j, u32x4& h, u32x4 (&qv)[HPL]) __attribute__((always_inline)) {
+      const int qq = kq0 + 2 * min(j, np - 1);
+      const uint8_t* b = rowp + (size_t)(qq >> 3) * 144;
+      h = gload16(b);
 #pragma unroll
-    for (int j = 0; j < RAWI; ++j) {
-      const int f = min(j * 1024 + lane * 16, RAWP - 16);
-      rsrc[j] = Wg + (size_t)min(n0 + pw * PR + f / 48, p.N - 1) * p.rb;
-      rkind[j] = (f % 48) >> 4;
-    }
-    const uint32_t raw0 = lds0 + RAWOFF + pw * RR * RSLOT;
-    // raw bytes of stage q (q >= nk: stage nk - 1 again, into its own slot)
-    auto issue = [&](int q) __attribute__((always_inline)) {
-      const int qq = kq0 + min(q, nk - 1), sb = qq >> 3, s = qq & 7;
-#pragma unroll
-      for (int j = 0; j < RAWI; ++j) {
-        const int c = rkind[j];
-        dma16(rsrc[j] + (size_t)sb * 144 + (c == 0 ? 0 : 16 + 32 * (s >> 1) + 16 * (c - 1)),
-              raw0 + (min(q, nk - 1) % RR) * RSLOT + j * 1024);
-      }
+      for (int i = 0; i < HPL; ++i) qv[i] = gload16(b + 16 + 32 * ((qq & 7) >> 1) + 16 * (h0 + i));
     };
-    for (int q = 0; q < DR; ++q) issue(q);
-    for (int q = 0; q < nk; ++q) {
-      issue(q + DR);          // its slot held stage q + DR - RR < q, decoded already
-      vm_wait<RAWI * DR>();   // stage q's raw bytes have landed
-      if (q >= NBR) poll4(done + 4 * ((q - NBR) % FL), q - NBR);  // B slot: stage q - NBR read by all
-      for (int li = lane; li < 2 * PR; li += 64) {  // row li / 2, half li % 2 (two passes for BN = 160)
-        const int dr = li >> 1, dh = li & 1;
-        const int s = q & 7;
-        const uint8_t* raw = lds + RAWOFF + (pw * RR + q % RR) * RSLOT + dr * 48;
-        const u32x4 H = *(const u32x4*)raw;
-        const u32x4 Q = *(const u32x4*)(raw + 16 + 16 * dh);
-        int sc, mn;
-        kq_scale_min(s, H[1], H[2], H[3], sc, mn);
-        const float dsc = h2f(H[0] & 0xffffu) * (float)sc, dm = h2f(H[0] >> 16) * (float)mn;
-        const int sh = 4 * (s & 1);
-        uint32_t o[8];
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const uint32_t v = Q[w] >> sh;
+    for (int u = 0; u < DP; ++u) issue(u, Hr[u], Qr[u]);
+    for (int j0 = 0; j0 < np; j0 += DP) {
 #pragma unroll
-          for (int e = 0; e < 2; ++e) {
-            // q_val (quant.h:83-84): both products exact, one rounding; then fp16 RNE
-            const float lo = fmaf(dsc, (float)((v >> (16 * e)) & 15u), -dm);
-            const float hi = fmaf(dsc, (float)((v >> (16 * e + 8)) & 15u), -dm);
-            o[2 * w + e] = (uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16);
+      for (int u = 0; u < DP; ++u) {
+        const int j = j0 + u, q = 2 * j;
+        vm_wait<NL * (DP - 1)>();  // pair j is in registers
+        asm volatile("" : "+v"(Hr[u]));
+#pragma unroll
+        for (int i = 0; i < HPL; ++i) asm volatile("" : "+v"(Qr[u][i]));
+        // B slots of stages q, q + 1: their previous users, q + 1 - NBR and before, read by all
+        if (q + 1 >= NBR) poll4(done + 4 * ((q + 1 - NBR) % FL), q + 1 - NBR);
+        if (act) {
+          const u32x4 H = Hr[u];
+          const float d = h2f(H[0] & 0xffffu), dmin = h2f(H[0] >> 16);
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            int sc, mn;
+            kq_scale_min(((kq0 + q) & 7) + t, H[1], H[2], H[3], sc, mn);
+            const float dsc = d * (float)sc, dm = dmin * (float)mn;
+            uint8_t* bt = lds + ((q + t) % NBR) * BPART;
+#pragma unroll
+            for (int i = 0; i < HPL; ++i) {
+              uint32_t o[8];
+#pragma unroll
+              for (int w = 0; w < 4; ++w) {
+                // elements 4w..4w+3 of the half, one per byte (the empty asm keeps the
+                // masked word, so each byte converts with v_cvt_f32_ubyte<n>)
+                uint32_t v = (Qr[u][i][w] >> (4 * t)) & 0x0f0f0f0fu;
+                asm volatile("" : "+v"(v));
+                // q_val (quant.h:83-84): both products exact, one rounding; then fp16 RNE
+                // (the empty asm keeps the fp32 results, so fma and conversion stay two roundings)
+                float f[4];
+#pragma unroll
+                for (int b = 0; b < 4; ++b) f[b] = fmaf(dsc, (float)((v >> (8 * b)) & 0xffu), -dm);
+                asm volatile("" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]));
+                const h2v p0 = {(_Float16)f[0], (_Float16)f[1]}, p1 = {(_Float16)f[2], (_Float16)f[3]};
+                o[2 * w] = __builtin_bit_cast(uint32_t, p0);
+                o[2 * w + 1] = __builtin_bit_cast(uint32_t, p1);
+              }
+              *(u32x4*)(bt + swz(r, 2 * (h0 + i))) = u32x4{o[0], o[1], o[2], o[3]};
+              *(u32x4*)(bt + swz(r, 2 * (h0 + i) + 1)) = u32x4{o[4], o[5], o[6], o[7]};
+            }
           }
         }
-        uint8_t* bt = lds + (q % NBR) * BPART;
-        const int r = pw * PR + dr;
-        *(u32x4*)(bt + swz(r, 2 * dh)) = u32x4{o[0], o[1], o[2], o[3]};
-        *(u32x4*)(bt + swz(r, 2 * dh + 1)) = u32x4{o[4], o[5], o[6], o[7]};
+        if (lane == 0) {
+          lds_rel(&ready[4 * (q % FL) + pw], q);
+          lds_rel(&ready[4 * ((q + 1) % FL) + pw], q + 1);
+        }
+        issue(j + DP, Hr[u], Qr[u]);  // the slot of pair j is free again
       }
-      if (lane == 0) lds_rel(&ready[4 * (q % FL) + pw], q);
     }
     vm_wait<0>();  // drain the re-loads past the end
     return;
@@ -204,19 +229,25 @@ __global__ __launch_bounds__(512) void qgemm_q4k_x3ref(const QArgs p) {
   const int fr = lane & 15, fc = lane >> 4;
   const uint32_t fo = swz(fr, fc);
   // A fragment (part, i): row c*32 + 16i + fr of the tile, halfs 8fc.. of stage q
+  // K-tiled planes: K step qq of row r at (qq * xt + r) * 32, so a fragment's 16
+  // rows are one contiguous kilobyte; row-major: row r at r * K + qq * 32
   const uint16_t* xa[3][2];
+  const size_t kstep = p.xt ? p.xt * QBK : (size_t)QBK;
 #pragma unroll
   for (int part = 0; part < 3; ++part)
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-      xa[part][i] = Xg + part * p.xs + (size_t)min(m0 + c * 32 + i * 16 + fr, M - 1) * p.K + 8 * fc;
+    for (int i = 0; i < 2; ++i) {
+      const size_t r = (size_t)min(m0 + c * 32 + i * 16 + fr, M - 1);
+      xa[part][i] = p.xt ? p.X + part * p.xs + ((size_t)p.row0[grp] + r) * QBK + 8 * fc
+                         : Xg + part * p.xs + r * p.K + 8 * fc;
+    }
   u32x4 A[XR][3][2];
   auto loadA = [&](int q, u32x4 (&dst)[3][2]) __attribute__((always_inline)) {
     const int qq = kq0 + min(q, nk - 1);  // past the end: a re-read, so every stage issues 6 loads
 #pragma unroll
     for (int part = 0; part < 3; ++part)
 #pragma unroll
-      for (int i = 0; i < 2; ++i) dst[part][i] = gload16(xa[part][i] + qq * QBK);
+      for (int i = 0; i < 2; ++i) dst[part][i] = gload16(xa[part][i] + (size_t)qq * kstep);
   };
   float4v acc[2][NB];
 #pragma unroll
@@ -292,8 +323,7 @@ __global__ __launch_bounds__(256) void qgemm_splitk_reduce(const float* __restri
 
 template <int BN, int KS>
 int launch_q(const QArgs& a, hipStream_t s, const char* who) {
-  constexpr int PR = BN / 4, RSLOT = (PR * 48 + 1023) / 1024 * 1024;
-  constexpr size_t lds = 3 * (size_t)BN * 64 + 4 * 8 * (size_t)RSLOT + 2 * 4 * 4 * 4;
+  constexpr size_t lds = QNBR * (size_t)BN * 64 + 2 * 4 * 4 * 4;
   static_assert(lds <= 160 * 1024, "LDS budget");
   static std::atomic<uint64_t> attr{0};
   int st = lds_attr_once(attr, (const void*)qgemm_q4k_x3ref<BN, KS>, (int)lds, who);
@@ -395,13 +425,13 @@ bool qgemm_q4k_fusable(const int* rows, int n, int N, int K, bool split) {
 // the x planes hold every group's rows (plane stride xs).  A single group may split K,
 // with `partials` (qgemm_q4k_partials_bytes) holding the partial sums.
 int qgemm_q4k_fused_groups(const void* const* W, const int* row0, const int* rows, int n, size_t rb,
-                           const uint16_t* xparts, size_t xs, float* Y, int ldy, int N, int K, float beta, int cus,
-                           hipStream_t s, const char* who, float* partials) {
+                           const uint16_t* xparts, size_t xs, size_t xt, float* Y, int ldy, int N, int K, float beta,
+                           int cus, hipStream_t s, const char* who, float* partials) {
   const QPlan pl = q_plan(rows, n, N, K, cus, n == 1 && partials != nullptr);
   if (pl.bn == 0) return set_error(TIERMM_UNSUPPORTED, "%s: no fused q4_K plan for N=%d K=%d", who, N, K);
   for (int g0 = 0; g0 < n; g0 += QG) {
     QArgs a{};
-    a.X = xparts; a.xs = xs; a.Y = Y; a.rb = rb; a.ldy = ldy; a.N = N; a.K = K; a.beta = beta;
+    a.X = xparts; a.xs = xs; a.xt = xt; a.Y = Y; a.rb = rb; a.ldy = ldy; a.N = N; a.K = K; a.beta = beta;
     a.P = partials; a.ps = n == 1 ? (size_t)rows[0] * N : 0;
     a.ngroups = 0;
     a.tile0[0] = 0;
@@ -432,10 +462,10 @@ int qgemm_q4k_fused_groups(const void* const* W, const int* row0, const int* row
   return TIERMM_OK;
 }
 
-int qgemm_q4k_fused(const void* W, size_t rb, const uint16_t* xparts, size_t xs, float* Y, int ldy, int M, int N, int K,
-                    float beta, int cus, hipStream_t s, const char* who, float* partials) {
+int qgemm_q4k_fused(const void* W, size_t rb, const uint16_t* xparts, size_t xs, size_t xt, float* Y, int ldy, int M,
+                    int N, int K, float beta, int cus, hipStream_t s, const char* who, float* partials) {
   const int row0 = 0;
-  return qgemm_q4k_fused_groups(&W, &row0, &M, 1, rb, xparts, xs, Y, ldy, N, K, beta, cus, s, who, partials);
+  return qgemm_q4k_fused_groups(&W, &row0, &M, 1, rb, xparts, xs, xt, Y, ldy, N, K, beta, cus, s, who, partials);
 }
 
 }  // namespace tiermm

@@ -29,11 +29,12 @@ int dequant_f16_rows(const void* W, int qtype, size_t rb, int cols, size_t nrows
                      bool tiled = false);
 int dequant_f16_group(const void* const* W, uint16_t* const* out, int n, int qtype, size_t rb, int cols,
                       size_t nrows, hipStream_t s, bool tiled = false);
-int qgemm_q4k_fused(const void* W, size_t rb, const uint16_t* xparts, size_t xs, float* Y, int ldy, int M, int N, int K,
-                    float beta, int cus, hipStream_t s, const char* who, float* partials);
+// xparts: three fp16 planes (stride xs), row-major (xt = 0) or K-tiled over xt rows.
+int qgemm_q4k_fused(const void* W, size_t rb, const uint16_t* xparts, size_t xs, size_t xt, float* Y, int ldy, int M,
+                    int N, int K, float beta, int cus, hipStream_t s, const char* who, float* partials);
 int qgemm_q4k_fused_groups(const void* const* W, const int* row0, const int* rows, int n, size_t rb,
-                           const uint16_t* xparts, size_t xs, float* Y, int ldy, int N, int K, float beta, int cus,
-                           hipStream_t s, const char* who, float* partials);
+                           const uint16_t* xparts, size_t xs, size_t xt, float* Y, int ldy, int N, int K, float beta,
+                           int cus, hipStream_t s, const char* who, float* partials);
 size_t qgemm_q4k_partials_bytes(int M, int N, int K);
 bool qgemm_q4k_fusable(const int* rows, int n, int N, int K, bool split);
 int device_cus(int* cus);
@@ -1238,12 +1239,14 @@ int tiermm_qgemm(const void* W, int qtype, size_t rb, const float* X, float* Y, 
   if (qtype == TIERMM_Q4_K && big_tiles(M, N) < 192 && qgemm_q4k_fusable(&M, 1, N, K, true)) {  // small M: decode W inside the GEMM
     uint16_t* parts = (uint16_t*)w;
     float* partials = (float*)((uint8_t*)w + al256(3 * mk * sizeof(uint16_t)));
-    st = split3_launch(X, parts, mk, mk, TIERMM_HML, s);
+    // K-tiled planes where x allows (a fragment load is then one contiguous kilobyte)
+    const size_t xt = ((uintptr_t)X & 15) == 0 ? (size_t)M : 0;
+    st = split3_launch(X, parts, mk, mk, TIERMM_HML, s, false, xt, K);
     if (st) return st;
     int cus = 0;
     st = device_cus(&cus);
     if (st) return st;
-    return qgemm_q4k_fused(W, rb, parts, mk, Y, ldy, M, N, K, beta, cus, s, who, partials);
+    return qgemm_q4k_fused(W, rb, parts, mk, xt, Y, ldy, M, N, K, beta, cus, s, who, partials);
   }
   uint16_t* w16 = (uint16_t*)w;
   uint16_t* parts = w16 + (size_t)N * K;
@@ -1394,7 +1397,7 @@ int tiermm_qgemm_grouped(const void* const* W_e, const int* qtype_e, const size_
     gr.push_back(Me);
   }
   if (!gw.empty()) {
-    st = qgemm_q4k_fused_groups(gw.data(), g0.data(), gr.data(), (int)gw.size(), grb, parts, pk, Y_sorted, N, N, K,
+    st = qgemm_q4k_fused_groups(gw.data(), g0.data(), gr.data(), (int)gw.size(), grb, parts, pk, 0, Y_sorted, N, N, K,
                                 0.f, cus, s, who, nullptr);
     if (st) return st;
   }
