@@ -146,13 +146,13 @@ def test_gemv_q4k_tall_ragged(gpu, N, K):
 
 
 @pytest.mark.parametrize("t", [tier_amd.Q4_K, tier_amd.Q5_K])
-@pytest.mark.parametrize("N,K", [(10256, 2048), (13824, 5120), (16390, 2048), (20000, 768), (28700, 1024),
-                                 (40000, 512), (14000, 8192)])
+@pytest.mark.parametrize("N,K", [(2000, 5120), (5000, 3072), (10256, 2048), (13824, 5120), (16390, 2048),
+                                 (20000, 768), (28700, 1024), (40000, 512), (14000, 8192)])
 def test_gemv_tall_tiles_per_workgroup(gpu, t, N, K):
-    """The tall whole-tile kernel (q4_K, q5_K) at each count of row tiles per workgroup it
-    is built for (3, 4, 5, 6 and 8; 40000 rows need more workgroups than CUs), with
-    workgroups that hold fewer tiles than the others and partial last row tiles (16390,
-    28700)."""
+    """The whole-tile kernel (q4_K, q5_K) at each count of row tiles per workgroup it is
+    built for (1, 2, 3, 4, 6 and 8; 40000 rows need more workgroups than CUs), with
+    workgroups whose last tiles lie past the matrix and partial last row tiles (5000,
+    16390, 28700)."""
     rng = np.random.default_rng(7 * N + K + t)
     blocks = oracle.random_blocks(rng, t, N * (K // 256)).reshape(N, -1)
     x = rng.standard_normal(K).astype(np.float32)
@@ -164,9 +164,11 @@ def test_gemv_tall_tiles_per_workgroup(gpu, t, N, K):
 
 
 @pytest.mark.parametrize("t", [tier_amd.Q4_K, tier_amd.Q5_K, tier_amd.Q8_0])
-@pytest.mark.parametrize("N", [1000, 4096, 4100])
+@pytest.mark.parametrize("N", [1000, 1024, 4096, 4100])
 def test_gemv_long_k_launch_shapes(gpu, t, N):
-    """K = 14336 around the 256-tile boundary between one tile x eight K parts and two
+    """K = 14336 around the launch-shape boundaries: q4_K takes the whole-tile kernel from
+    64 to 256 row tiles (1024 and 4096 rows) and the per-wave kernel outside them (1000,
+    4100); q5_K and q8_0 switch at 256 tiles between one tile x eight K parts and two
     tiles x four K parts per workgroup."""
     K = 14336
     rng = np.random.default_rng(N + t)

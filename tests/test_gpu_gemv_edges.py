@@ -42,11 +42,16 @@ def _classes(y):
 
 # (type, N, K): the kernel that serves each shape is named in the id
 KERNELS = [
-    (tier_amd.Q4_K, 13824, 5120, "q4K-whole-tile"),
-    (tier_amd.Q4_K, 5120, 5120, "q4K-per-wave-2x4"),
-    (tier_amd.Q4_K, 1024, 14336, "q4K-per-wave-1x8"),
+    (tier_amd.Q4_K, 13824, 5120, "q4K-whole-tile-4-tiles"),
+    (tier_amd.Q4_K, 5120, 5120, "q4K-whole-tile-2-tiles"),
+    (tier_amd.Q4_K, 1024, 14336, "q4K-whole-tile-k14336"),
+    (tier_amd.Q4_K, 10240, 8192, "q4K-whole-tile-k8192"),
+    (tier_amd.Q4_K, 512, 5120, "q4K-per-wave-1x4"),
+    (tier_amd.Q4_K, 5120, 14336, "q4K-per-wave-2x4"),
+    (tier_amd.Q4_K, 512, 14336, "q4K-per-wave-1x8"),
     (tier_amd.Q5_K, 13824, 5120, "q5K-whole-tile"),
-    (tier_amd.Q5_K, 1024, 5120, "q5K-per-wave"),
+    (tier_amd.Q5_K, 1024, 5120, "q5K-whole-tile-1-tile"),
+    (tier_amd.Q5_K, 512, 5120, "q5K-per-wave"),
     (tier_amd.Q8_0, 4096, 4096, "q8_0-per-wave"),
     (tier_amd.Q8_0, 10240, 8192, "q8_0-per-wave-tall"),
     (tier_amd.Q6_K, 1024, 5120, "q6K"),

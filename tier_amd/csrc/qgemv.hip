@@ -376,6 +376,7 @@ int launch_dense(const void* W, const float* x, float* y, int N, int K, hipStrea
 int qgemv_q4k(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s);
 int qgemv_q4k_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s);
 int qgemv_q5k_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s);
+bool qgemv_ws_takes(int qtype, int N, int K);
 bool qgemv_mfma_fits(const void* W, int qtype, size_t rb, int K);
 bool qgemv_q6k_fits(const void* W, size_t rb, int N, int K);
 int qgemv_q6k(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s);
@@ -389,14 +390,14 @@ int qgemv_dispatch(const void* W, int qtype, size_t rb, const float* x, float* y
     case QT_F16: return launch_dense<TIERMM_F16>(W, x, y, N, K, s);
     case QT_BF16: return launch_dense<TIERMM_BF16>(W, x, y, N, K, s);
     case QT_Q4_K:  // MFMA kernels up to kQ4kMaxK (x digits in LDS); beyond, the generic kernel
-      if (K <= 8192 && (N + 15) / 16 >= 640) return qgemv_q4k_ws(W, rb, x, y, N, K, s);
+      if (qgemv_ws_takes(QT_Q4_K, N, K)) return qgemv_q4k_ws(W, rb, x, y, N, K, s);
       return K <= kQ4kMaxK ? qgemv_q4k(W, rb, x, y, N, K, s) : launch_generic<QT_Q4_K>(W, rb, x, y, N, K, s);
     case QT_Q8_0:  // int8 MFMA kernel; rows that do not fit it staged whole in LDS
       if (qgemv_mfma_fits(W, qtype, rb, K)) return qgemv_mfma(W, qtype, rb, x, y, N, K, s);
       if (staged_fits(W, rb, K)) return launch_staged<QT_Q8_0>(W, rb, x, y, N, K, s);
       return launch_generic<QT_Q8_0>(W, rb, x, y, N, K, s);
-    case QT_Q5_K:  // tall matrices on the whole-tile kernel, the rest on the per-wave one
-      if (qgemv_mfma_fits(W, qtype, rb, K) && K <= 8192 && (N + 15) / 16 >= 640) return qgemv_q5k_ws(W, rb, x, y, N, K, s);
+    case QT_Q5_K:  // the whole-tile kernel where qgemv_ws_takes, the rest on the per-wave one
+      if (qgemv_mfma_fits(W, qtype, rb, K) && qgemv_ws_takes(QT_Q5_K, N, K)) return qgemv_q5k_ws(W, rb, x, y, N, K, s);
       if (qgemv_mfma_fits(W, qtype, rb, K)) return qgemv_mfma(W, qtype, rb, x, y, N, K, s);
       return launch_generic<QT_Q5_K>(W, rb, x, y, N, K, s);
     case QT_Q6_K:

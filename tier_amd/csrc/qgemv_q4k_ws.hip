@@ -1,5 +1,5 @@
-// qgemv_q4k_ws.hip -- Q4_K (and Q5_K) decode GEMV for tall matrices: a workgroup
-// streams one 16-row tile at a time through producer waves.
+// qgemv_q4k_ws.hip -- Q4_K (and Q5_K) decode GEMV from 1024 rows up (qgemv_ws_takes):
+// a workgroup streams one 16-row tile at a time through producer waves.
 //
 // Same arithmetic and x digit layout as qgemv_q4k.hip (gemv_q, tier.cpp:299-306;
 // q_val Q4_K, quant.h:83-84); q4k_mfma.h holds the shared pieces.
@@ -48,7 +48,7 @@ namespace {
 
 constexpr int NP = 4;      // producer waves
 constexpr int PROWS = 4;   // rows of a tile per producer
-constexpr int GTILE = 224; // target grid: tiles per workgroup R = ceil(tiles / GTILE)
+constexpr int GTILE = 256; // target grid: tiles per workgroup R = ceil(tiles / GTILE)
 
 constexpr int pad4(int n) { return (n + 3) / 4 * 4; }
 
@@ -266,11 +266,10 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
 
 template <int QT, int R, int GS, int NC, int NS, int D, int XP, int XK>
 int launch_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
+  const unsigned grid = (unsigned)((N + 15) / 16 + R - 1) / R;
   using L = WsLayout<QT, GS, NC, NS, R>;
   static_assert(xq_bytes(XK) + 4 * NC + L::LDS <= 160 * 1024, "LDS budget (x digits, flags, ring)");
   static_assert(XK / 16 <= 64 * NC * XP, "x preparation: one thread per 16 elements");
-  const int tiles = (N + 15) / 16;
-  const unsigned grid = (unsigned)((tiles + R - 1) / R);
   static std::atomic<uint64_t> attr{0};
   int st = lds_attr_once(attr, (const void*)qgemv_q4k_ws<QT, R, GS, NC, NS, D, XP, XK>, (int)L::LDS,
                          "tiermm_qgemv: q4_K LDS attribute");
@@ -280,36 +279,56 @@ int launch_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, 
   return TIERMM_OK;
 }
 
+// R = ceil(tiles / GTILE) tiles per workgroup (instantiated for 1-4, 6 and 8), so
+// the grid, ceil(tiles / R), stays at or below 256 workgroups up to 2048 tiles.
 template <int QT, int GS, int NC, int NS, int D, int XP, int XK>
 int launch_ws_r(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
   const int tiles = (N + 15) / 16, r = (tiles + GTILE - 1) / GTILE;
-  if (r <= 3) return launch_ws<QT, 3, GS, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
-  if (r == 4) return launch_ws<QT, 4, GS, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
-  if (r == 5) return launch_ws<QT, 5, GS, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
-  if (r == 6) return launch_ws<QT, 6, GS, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
-  return launch_ws<QT, 8, GS, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
+  switch (r <= 4 ? r : r <= 6 ? 6 : 8) {
+    case 1: return launch_ws<QT, 1, GS, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
+    case 2: return launch_ws<QT, 2, GS, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
+    case 3: return launch_ws<QT, 3, GS, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
+    case 4: return launch_ws<QT, 4, GS, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
+    case 6: return launch_ws<QT, 6, GS, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
+    default: return launch_ws<QT, 8, GS, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
+  }
 }
 
 }  // namespace
 
-// Tall matrices (at least 640 row tiles).  Tiles per workgroup: the grid lands
-// near 224 workgroups (a uniform count per workgroup measured faster than a
-// ragged one).  Up to K = 5120 whole-tile stages of 20 super-blocks (shorter
-// rows re-read their last 16 bytes to fill the fixed load count; still the
-// fastest at K = 4096), 8 consumers with up to 3 columns each; up to 8192
-// stages of 8 super-blocks (whole-tile and 16-super-block stages measured
-// slower there: 10240x8192 10.8 against 10.1 us).
+// Which GEMVs take this kernel.  q4_K: from 64 row tiles up to K = 5120, from 640
+// up to 8192, and 64..256 tiles up to 14336 (one tile per workgroup; at 320 tiles
+// 160 workgroups of two lose to the per-wave kernel: 5120x14336 14.7 against
+// 12.9 us).  q5_K: from 64 row tiles up to K = 5120, from 640 up to 8192 (at
+// 5120x14336 the per-wave kernel is faster: 14.9 against 15.5 us).
+bool qgemv_ws_takes(int qtype, int N, int K) {
+  const int tiles = (N + 15) / 16;
+  if (qtype == QT_Q4_K)
+    return (K <= 5120 && tiles >= 64) || (K <= 8192 && tiles >= 640) || (K <= 14336 && tiles >= 64 && tiles <= 256);
+  if (qtype == QT_Q5_K) return (K <= 5120 && tiles >= 64) || (K <= 8192 && tiles >= 640);
+  return false;
+}
+
+// Tiles per workgroup: the grid lands at or below 256 workgroups (a uniform count
+// per workgroup measured faster than a ragged one: 13824x5120 8.90 against 9.16 us,
+// 5120x5120 5.89 against 6.26 us).  Up to K = 5120 whole-tile stages of 20
+// super-blocks (shorter rows re-read their last 16 bytes to fill the fixed load
+// count; still the fastest at K = 4096), 8 consumers with up to 3 columns each; up
+// to 8192 and up to 14336 stages of 8 super-blocks (whole-tile and 16-super-block
+// stages measured slower at 10240x8192: 10.8 against 10.1 us).
 int qgemv_q4k_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
   if (K <= 5120) return launch_ws_r<QT_Q4_K, 20, 8, 3, 1, 1, 5120>(W, rb, x, y, N, K, s);
   if (K <= 8192) return launch_ws_r<QT_Q4_K, 8, 8, 4, 2, 1, 8192>(W, rb, x, y, N, K, s);
-  return set_error(TIERMM_UNSUPPORTED, "tiermm_qgemv: q4_K K=%d above %d", K, 8192);
+  if (K <= 14336) return launch_ws_r<QT_Q4_K, 8, 8, 4, 2, 2, 14336>(W, rb, x, y, N, K, s);
+  return set_error(TIERMM_UNSUPPORTED, "tiermm_qgemv: q4_K K=%d above %d", K, 14336);
 }
 
 // The same kernel on Q5_K (176-byte super-blocks; stages of 10 super-blocks up
 // to K = 5120 keep the ring within the LDS).  Against the per-wave kernel:
-// 13824x5120 10.8 against 12.5 us, 10240x8192 12.0 against 15.4 us.  Q8_0 (272-byte
-// groups) gained nothing this way (a 3-slot ring: 17.5 against 17.1 us at
-// 13824x5120, 36.6 against 22.2 us at 10240x8192) and keeps the per-wave kernel.
+// 13824x5120 10.8 against 12.5 us, 10240x8192 12.0 against 15.4 us, 5120x5120
+// 7.2 against 7.8 us.  Q8_0 (272-byte groups) gained nothing this way (a 3-slot
+// ring: 17.5 against 17.1 us at 13824x5120, 36.6 against 22.2 us at 10240x8192;
+// 4096x4096 whole-tile stages: 8.4 against 5.9 us) and keeps the per-wave kernel.
 int qgemv_q5k_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
   if (K <= 5120) return launch_ws_r<QT_Q5_K, 10, 10, 4, 2, 1, 5120>(W, rb, x, y, N, K, s);
   if (K <= 8192) return launch_ws_r<QT_Q5_K, 8, 8, 4, 2, 1, 8192>(W, rb, x, y, N, K, s);
