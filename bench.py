@@ -163,7 +163,8 @@ def bench_chat_stream(tier_amd, hip, stream, layers=4):
     """chat_lin with weight streaming (tier.cpp:2283-2285, 2351-2378): the 28 linears of
     `layers` config-4 decoder layers (q4_K_S, 155.6 MiB each) with every matrix streamed from
     pinned host memory through 2 device slots, against the same set resident, at M=1 (decode)
-    and M=4096 (prefill, MODE_X3REF).  The roof of the streamed decode pass is the
+    and M=4096 (prefill, MODE_F32: chat_lin's fp32 dequant and fp32-accurate product,
+    tier.cpp:2358-2359).  The roof of the streamed decode pass is the
     host-to-device copy rate, measured here as the same 28 copies back to back without
     compute.  Every figure is taken after warm-up passes (the first DMA reads of fresh
     pinned pages and a new copy queue run up to 35 % slower) and is the median over
@@ -219,7 +220,7 @@ def bench_chat_stream(tier_amd, hip, stream, layers=4):
             def one_pass():
                 for i, idx in enumerate(ids):
                     qt, N, K = shapes[i % 7]
-                    c.lin(idx, X[K].ptr, Y.ptr, M, tier_amd.MODE_X3REF)
+                    c.lin(idx, X[K].ptr, Y.ptr, M, tier_amd.MODE_F32)
             for _ in range(3):  # the first passes over fresh host rows and a new copy queue run slower
                 one_pass()
             stream.synchronize()
