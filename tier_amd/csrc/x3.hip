@@ -1329,9 +1329,23 @@ int tiermm_qgemm_grouped(const void* const* W_e, const int* qtype_e, const size_
   const size_t P = (size_t)expert_offsets[n_experts], pk = P * K;
   uint16_t* parts = (uint16_t*)w;
   uint16_t* w16 = (uint16_t*)((uint8_t*)w + al256(3 * pk * sizeof(uint16_t)));
-  const int chunk = big_group_chunk(expert_offsets, n_experts, N, K);
-  // the grouped big-tile launch reads K-tiled planes; the other paths row-major ones
-  const bool tiled = chunk && K % 32 == 0 && ((uintptr_t)X_sorted & 15) == 0;
+  int chunk = big_group_chunk(expert_offsets, n_experts, N, K);
+  // Every routed expert q4_K, at most 2048 rows each on average: the fused grouped kernel
+  // (no fp16 decode pass) beats decode + the big-tile launch.  Config 5's gate/up (64
+  // experts, ~512 rows each, N = 1408, K = 2048): the MoE line 2.72 ms against 2.86 ms.
+  bool all_q4k = true;
+  int nz = 0;
+  for (int e = 0; e < n_experts; ++e)
+    if (expert_offsets[e + 1] > expert_offsets[e]) {
+      ++nz;
+      all_q4k = all_q4k && qtype_e[e] == TIERMM_Q4_K;
+    }
+  const bool fused_all = all_q4k && nz > 0 && P <= (size_t)nz * 2048 &&
+                         grouped_q4k_fused(qtype_e, expert_offsets, n_experts, N, K);
+  if (fused_all) chunk = 0;
+  // the grouped big-tile launch and the all-q4_K fused launch read K-tiled planes; the
+  // per-expert paths row-major ones
+  const bool tiled = (chunk || fused_all) && K % 32 == 0 && ((uintptr_t)X_sorted & 15) == 0;
   st = split3_launch(X_sorted, parts, pk, pk, TIERMM_HML, s, false, tiled ? P : 0, K);
   if (st) return st;
   if (chunk) {  // fp16 weights of up to `chunk` experts, then one grouped launch over their tiles
@@ -1397,8 +1411,8 @@ int tiermm_qgemm_grouped(const void* const* W_e, const int* qtype_e, const size_
     gr.push_back(Me);
   }
   if (!gw.empty()) {
-    st = qgemm_q4k_fused_groups(gw.data(), g0.data(), gr.data(), (int)gw.size(), grb, parts, pk, 0, Y_sorted, N, N, K,
-                                0.f, cus, s, who, nullptr);
+    st = qgemm_q4k_fused_groups(gw.data(), g0.data(), gr.data(), (int)gw.size(), grb, parts, pk, tiled ? P : 0,
+                                Y_sorted, N, N, K, 0.f, cus, s, who, nullptr);
     if (st) return st;
   }
   // other types: fp16 W staged per expert, then the x3-ref GEMM on the expert's rows
