@@ -89,6 +89,15 @@ __device__ __forceinline__ void ktile_unit(size_t u, size_t rows, size_t& row, i
 }
 
 // 16 bytes per lane from p into LDS at lds_addr + 16*lane (lds_addr wave-uniform, through M0).
+//
+// M0 is written here without the compiler's knowledge (it treats M0 as reserved, and an
+// "m0" clobber is not honoured).  This holds because nothing else in the kernels that
+// call these helpers uses M0: no LDS-DMA builtins, s_sendmsg, indexed register access or
+// LDS-direct reads; a kernel that adds such a use must not keep M0 live across a call
+// here.  Either form leaves the ordering of DMA and LDS reads to the program (the
+// compiler adds no vmcnt wait before an LDS read of a slot that
+// __builtin_amdgcn_global_load_lds writes), so the stage pipelines wait with explicit
+// vm_wait counts; every one of them was measured with this asm form.
 __device__ __forceinline__ void dma16(const void* p, uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(p),
                "s"(__builtin_amdgcn_readfirstlane(lds_addr))
