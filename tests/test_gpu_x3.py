@@ -199,25 +199,85 @@ def test_qgemm_q4k_fused_shapes(gpu, M, N, K, beta):
     assert oracle.rel_fro(got, ref) <= BAR
 
 
+# Types the fused kernel decodes, with a K whose rows are only 2-byte aligned where the
+# block size allows it (q6_K 768: 630-byte rows; q8_0 / q5_0 480: 510 / 330-byte rows).
+FUSED = [("q4_K", tier_amd.Q4_K, 512), ("q5_K", tier_amd.Q5_K, 512), ("q6_K", tier_amd.Q6_K, 768),
+         ("q8_0", tier_amd.Q8_0, 480), ("q5_0", tier_amd.Q5_0, 480)]
+
+
+@pytest.mark.parametrize("name,t,K", FUSED, ids=[f[0] for f in FUSED])
 @pytest.mark.parametrize("bn", [160, 128, 64])
-@pytest.mark.parametrize("sigma", [0.02, 60.0, 2e-6])
-def test_qgemm_q4k_fused_decode_bit_exact(gpu, monkeypatch, bn, sigma):
+@pytest.mark.parametrize("scale", ["0.02", "60", "tiny"])
+def test_qgemm_fused_decode_bit_exact(gpu, monkeypatch, name, t, K, bn, scale):
     """One-hot rows of x read the fused kernel's fp16 weights back: row m of x is e_m, so
     Y[m][n] = W16[n][m] exactly (one non-zero product per sum).  This pins the in-kernel
-    decode -- q_val with one rounding, then fp16 round-to-nearest-even -- bit for bit
-    against the oracle, for each decode layout (one lane per row at BN = 160, two at
-    BN <= 128), with weights from fp16 subnormals up to values in the thousands."""
+    decode -- q_val, then fp16 round-to-nearest-even -- bit for bit against the oracle,
+    for each type and decode layout (one lane per row at BN = 160, two at BN <= 128),
+    with weights from fp16 subnormals up to values in the thousands (q5_0, which has no
+    quantizer: random blocks with d ~N(0, 0.02))."""
     monkeypatch.setenv("TIERMM_QGEMM_TILE", f"{bn},1")
-    t, N, K = tier_amd.Q4_K, 352, 512
+    N = 352
+    # tiny: mostly fp16 subnormal weights (q6_K's fp16 d would itself underflow at 2e-6)
+    sigma = {"0.02": 0.02, "60": 60.0, "tiny": 5e-5 if t == tier_amd.Q6_K else 2e-6}[scale]
     blocks = quantized_weight(t, N, K, seed=46, sigma=sigma)
     x = np.eye(K, dtype=np.float32)
     W, X, Y = hip.to_device(blocks), hip.to_device(x), hip.DeviceBuffer(K * N * 4)
-    tier_amd.qgemm(W.ptr, t, tier_amd.q_row_bytes(t, K), X.ptr, Y.ptr, K, N, K)
+    rb = tier_amd.q_row_bytes(t, K)
+    assert tier_amd.qgemm_ws_bytes(t, K, N, K) == 3 * K * K * 2  # the fused plan: no fp16 W in the workspace
+    tier_amd.qgemm(W.ptr, t, rb, X.ptr, Y.ptr, K, N, K)
     hip.synchronize()
     got = Y.download(np.float32, K * N).reshape(K, N)
     w16 = oracle.h2f(oracle.dequant(blocks, t, K, oracle.OUT_F16)).reshape(N, K)
     assert np.all(np.isfinite(w16)) and np.count_nonzero(w16) > 0
     assert np.array_equal(got, w16.T)  # +0 and -0 compare equal: a zero weight sums to +0
+
+
+TYPE_PLANS = [(160, 1), (160, 2), (128, 4), (96, 2), (64, 1), (64, 4)]
+
+
+@pytest.mark.parametrize("name,t", [(f[0], f[1]) for f in FUSED[1:]], ids=[f[0] for f in FUSED[1:]])
+@pytest.mark.parametrize("bn,ks", TYPE_PLANS)
+def test_qgemm_fused_type_plans(gpu, monkeypatch, name, t, bn, ks):
+    """The fused kernel on q5_K, q6_K, q8_0 and q5_0 weights at every tile width and
+    split-K factor it takes: partial M and N tiles, beta = 1, K split into units of
+    each type's producer (q6_K: quarter super-blocks)."""
+    monkeypatch.setenv("TIERMM_QGEMM_TILE", f"{bn},{ks}")
+    M, N, K, beta = 300, 1000, 1024, 1.0
+    assert tier_amd.qgemm_ws_bytes(t, M, N, K) == 3 * M * K * 2 + (ks * M * N * 4 if ks > 1 else 0)
+    rng = np.random.default_rng(M + N + K + bn + ks + t)
+    be, _ = oracle.block(t)
+    blocks = oracle.random_blocks(rng, t, N * (K // be)).reshape(N, -1)
+    x = activations(M, K, seed=25)
+    y0 = rng.standard_normal((M, N)).astype(np.float32)
+    W, X, Y = hip.to_device(blocks), hip.to_device(x), hip.to_device(y0)
+    tier_amd.qgemm(W.ptr, t, tier_amd.q_row_bytes(t, K), X.ptr, Y.ptr, M, N, K, beta=beta)
+    hip.synchronize()
+    got = Y.download(np.float32, M * N).reshape(M, N)
+    w16 = oracle.h2f(oracle.dequant(blocks, t, K, oracle.OUT_F16)).reshape(N, K)
+    ref = x.astype(np.float64) @ w16.astype(np.float64).T + beta * y0.astype(np.float64)
+    assert np.all(np.isfinite(got))
+    assert oracle.rel_fro(got, ref) <= BAR
+
+
+@pytest.mark.parametrize("name,t,K", [("q8_0", tier_amd.Q8_0, 1408), ("q5_0", tier_amd.Q5_0, 1408),
+                                      ("q8_0_k96", tier_amd.Q8_0, 96), ("q6_K_k256", tier_amd.Q6_K, 256)],
+                         ids=lambda v: v if isinstance(v, str) else None)
+@pytest.mark.parametrize("M", [1, 257])
+def test_qgemm_fused_odd_k(gpu, name, t, K, M):
+    """K that is not a multiple of 256 (the MoE down projection's 1408; three q8_0
+    blocks) or a single q6_K super-block with 2-byte aligned rows, through the default
+    plan: every row of x, every partial tile."""
+    N = 200
+    rng = np.random.default_rng(K + M + t)
+    be, _ = oracle.block(t)
+    blocks = oracle.random_blocks(rng, t, N * (K // be)).reshape(N, -1)
+    x = activations(M, K, seed=26)
+    W, X, Y = hip.to_device(blocks), hip.to_device(x), hip.DeviceBuffer(M * N * 4)
+    tier_amd.qgemm(W.ptr, t, tier_amd.q_row_bytes(t, K), X.ptr, Y.ptr, M, N, K)
+    hip.synchronize()
+    got = Y.download(np.float32, M * N).reshape(M, N)
+    w16 = oracle.h2f(oracle.dequant(blocks, t, K, oracle.OUT_F16)).reshape(N, K)
+    assert oracle.rel_fro(got, x.astype(np.float64) @ w16.astype(np.float64).T) <= BAR
 
 
 @pytest.mark.parametrize("M,N,K", [(130, 100, 768), (512, 1000, 2048)])

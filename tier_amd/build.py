@@ -17,7 +17,7 @@ LIB = os.path.join(HERE, "libtiermm.so")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 
-HIP_SOURCES = ["dequant.hip", "qgemv.hip", "qgemv_q4k.hip", "qgemv_q4k_ws.hip", "qgemv_q6k.hip", "qgemm_q4k.hip", "x3.hip",
+HIP_SOURCES = ["dequant.hip", "qgemv.hip", "qgemv_q4k.hip", "qgemv_q4k_ws.hip", "qgemv_q6k.hip", "qgemm_fused.hip", "x3.hip",
                "noalloc.hip", "host_dequant.hip", "chat_ops.hip"]
 CXX_SOURCES = ["api.cpp", "quantize.cpp", "tq.cpp", "chat.cpp"]
 

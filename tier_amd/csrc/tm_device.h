@@ -66,8 +66,13 @@ __device__ float nonfinite_terms(const uint8_t* row, const float* x, int k0, int
 // waiting for everything before LDS reads), which would serialise the stream.
 // Every vector load below is one instruction per wave regardless of the lane
 // mask, and loads retire in order, so "s_waitcnt vmcnt(N)" means all but the N
-// most recent ones have landed.
+// most recent ones have landed.  gload16's destination looks ready to the
+// compiler at once: use it only where nothing touches that register before the
+// explicit wait (straight-line code); a register ring carried around a loop can
+// be copied by the compiler while its load is in flight, so loops load with
+// plain loads and let the compiler place the waits.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ u32x4 gload16(const void* p) {
   u32x4 r;
   asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p) : "memory");
@@ -121,7 +126,7 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // Longest K one fp32 accumulator sums in the MFMA GEMMs: its rounding error grows
 // like sqrt(K), and above kAccChunkFrom the x3 products run as chunks of at most
 // kAccChunkMax columns whose sums are added in fp32 (x3.hip run_k_chunks; the
-// fused q4_K GEMM splits K at least as finely).
+// fused dequant GEMM splits K at least as finely).
 constexpr int kAccChunkFrom = 6144, kAccChunkMax = 4096;
 inline int acc_chunks(int K) { return K > kAccChunkFrom ? (K + kAccChunkMax - 1) / kAccChunkMax : 1; }
 

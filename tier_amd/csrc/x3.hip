@@ -29,14 +29,15 @@ int dequant_f16_rows(const void* W, int qtype, size_t rb, int cols, size_t nrows
                      bool tiled = false);
 int dequant_f16_group(const void* const* W, uint16_t* const* out, int n, int qtype, size_t rb, int cols,
                       size_t nrows, hipStream_t s, bool tiled = false);
-// xparts: three fp16 planes (stride xs), row-major (xt = 0) or K-tiled over xt rows.
-int qgemm_q4k_fused(const void* W, size_t rb, const uint16_t* xparts, size_t xs, size_t xt, float* Y, int ldy, int M,
-                    int N, int K, float beta, int cus, hipStream_t s, const char* who, float* partials);
-int qgemm_q4k_fused_groups(const void* const* W, const int* row0, const int* rows, int n, size_t rb,
-                           const uint16_t* xparts, size_t xs, size_t xt, float* Y, int ldy, int N, int K, float beta,
-                           int cus, hipStream_t s, const char* who, float* partials);
-size_t qgemm_q4k_partials_bytes(int M, int N, int K);
-bool qgemm_q4k_fusable(const int* rows, int n, int N, int K, bool split);
+// Fused dequant + x3-ref GEMM (q4_K, q5_K, q6_K, q8_0, q5_0 weights).  xparts: three
+// fp16 planes (stride xs), row-major (xt = 0) or K-tiled over xt rows.
+int qgemm_fused(const void* W, int qtype, size_t rb, const uint16_t* xparts, size_t xs, size_t xt, float* Y, int ldy,
+                int M, int N, int K, float beta, int cus, hipStream_t s, const char* who, float* partials);
+int qgemm_fused_groups(const void* const* W, int qtype, const int* row0, const int* rows, int n, size_t rb,
+                       const uint16_t* xparts, size_t xs, size_t xt, float* Y, int ldy, int N, int K, float beta,
+                       int cus, hipStream_t s, const char* who, float* partials);
+size_t qgemm_fused_partials_bytes(int qtype, int M, int N, int K);
+bool qgemm_fusable(int qtype, const int* rows, int n, int N, int K, bool split);
 int device_cus(int* cus);
 
 namespace {
@@ -838,14 +839,31 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
 
-// Whether the routed q4_K experts take the fused kernel in one launch (one group
-// per expert, no split-K: K <= kAccChunkFrom); otherwise they are staged in fp16
-// like the other types.
-bool grouped_q4k_fused(const int* qt, const int* offs, int n_experts, int N, int K) {
+// Whether the routed experts of type qt take the fused kernel in one launch (one group
+// per expert, no split-K); experts of the types it does not take are staged in fp16.
+bool grouped_fused(int qt, const int* qts, const int* offs, int n_experts, int N, int K) {
   std::vector<int> rows;
   for (int e = 0; e < n_experts; ++e)
-    if (offs[e + 1] > offs[e] && qt[e] == TIERMM_Q4_K) rows.push_back(offs[e + 1] - offs[e]);
-  return rows.empty() || qgemm_q4k_fusable(rows.data(), (int)rows.size(), N, K, false);
+    if (offs[e + 1] > offs[e] && qts[e] == qt) rows.push_back(offs[e + 1] - offs[e]);
+  return !rows.empty() && qgemm_fusable(qt, rows.data(), (int)rows.size(), N, K, false);
+}
+
+// The distinct weight types of the routed experts, each with whether grouped_fused takes it.
+std::vector<std::pair<int, bool>> routed_types(const int* qts, const int* offs, int n_experts, int N, int K) {
+  std::vector<std::pair<int, bool>> t;
+  for (int e = 0; e < n_experts; ++e) {
+    if (offs[e + 1] == offs[e]) continue;
+    bool seen = false;
+    for (auto& x : t) seen = seen || x.first == qts[e];
+    if (!seen) t.push_back({qts[e], grouped_fused(qts[e], qts, offs, n_experts, N, K)});
+  }
+  return t;
+}
+
+bool type_fused(const std::vector<std::pair<int, bool>>& t, int qt) {
+  for (auto& x : t)
+    if (x.first == qt) return x.second;
+  return false;
 }
 
 // Routed experts through the grouped 256x320 launch: the number of experts whose
@@ -1190,8 +1208,8 @@ size_t tiermm_qgemm_ws_bytes(int qtype, int M, int N, int K, int mode) {
     return al256((size_t)N * K * 4) + 2 * al256((size_t)N * K * 2) + al256((size_t)N * 4) +
            2 * al256((size_t)M * K * 2) + al256((size_t)M * 4);
   const size_t parts = (size_t)3 * M * K * sizeof(uint16_t);  // x split in three fp16 planes
-  if (qtype == TIERMM_Q4_K && big_tiles(M, N) < 192 && qgemm_q4k_fusable(&M, 1, N, K, true))
-    return al256(parts) + qgemm_q4k_partials_bytes(M, N, K);  // W decoded inside the GEMM; split-K partial sums
+  if (big_tiles(M, N) < 192 && qgemm_fusable(qtype, &M, 1, N, K, true))
+    return al256(parts) + qgemm_fused_partials_bytes(qtype, M, N, K);  // W decoded inside the GEMM; split-K partials
   return (size_t)N * K * sizeof(uint16_t) + parts;                   // W16 staged in the workspace
 }
 
@@ -1236,7 +1254,7 @@ int tiermm_qgemm(const void* W, int qtype, size_t rb, const float* X, float* Y, 
     if (big_tiles(M, N) >= 192) return launch_x3_big<X3_2X2>(a, s, who);
     return launch_x3<128, 128, X3_2X2>(a, s, who);
   }
-  if (qtype == TIERMM_Q4_K && big_tiles(M, N) < 192 && qgemm_q4k_fusable(&M, 1, N, K, true)) {  // small M: decode W inside the GEMM
+  if (big_tiles(M, N) < 192 && qgemm_fusable(qtype, &M, 1, N, K, true)) {  // small M: decode W inside the GEMM
     uint16_t* parts = (uint16_t*)w;
     float* partials = (float*)((uint8_t*)w + al256(3 * mk * sizeof(uint16_t)));
     // K-tiled planes where x allows (a fragment load is then one contiguous kilobyte)
@@ -1246,7 +1264,7 @@ int tiermm_qgemm(const void* W, int qtype, size_t rb, const float* X, float* Y, 
     int cus = 0;
     st = device_cus(&cus);
     if (st) return st;
-    return qgemm_q4k_fused(W, rb, parts, mk, xt, Y, ldy, M, N, K, beta, cus, s, who, partials);
+    return qgemm_fused(W, qtype, rb, parts, mk, xt, Y, ldy, M, N, K, beta, cus, s, who, partials);
   }
   uint16_t* w16 = (uint16_t*)w;
   uint16_t* parts = w16 + (size_t)N * K;
@@ -1282,12 +1300,9 @@ size_t tiermm_qgemm_grouped_ws_bytes(const int* qtype_e, const int* expert_offse
   const size_t P = n_experts > 0 ? (size_t)expert_offsets[n_experts] : 0;
   const int chunk = n_experts > 0 ? big_group_chunk(expert_offsets, n_experts, N, K) : 0;
   if (chunk) return al256(3 * P * K * sizeof(uint16_t)) + chunk * al256((size_t)N * K * sizeof(uint16_t));
-  const bool fused = grouped_q4k_fused(qtype_e, expert_offsets, n_experts, N, K);
+  const auto types = routed_types(qtype_e, expert_offsets, n_experts, N, K);
   bool staged = false;
-  for (int e = 0; e < n_experts; ++e) {
-    const int Me = expert_offsets[e + 1] - expert_offsets[e];
-    if (Me > 0 && (qtype_e[e] != TIERMM_Q4_K || !fused)) staged = true;
-  }
+  for (auto& t : types) staged = staged || !t.second;
   return al256(3 * P * K * sizeof(uint16_t)) + (staged ? (size_t)N * K * sizeof(uint16_t) : 0);
 }
 
@@ -1330,20 +1345,16 @@ int tiermm_qgemm_grouped(const void* const* W_e, const int* qtype_e, const size_
   uint16_t* parts = (uint16_t*)w;
   uint16_t* w16 = (uint16_t*)((uint8_t*)w + al256(3 * pk * sizeof(uint16_t)));
   int chunk = big_group_chunk(expert_offsets, n_experts, N, K);
-  // Every routed expert q4_K, at most 2048 rows each on average: the fused grouped kernel
-  // (no fp16 decode pass) beats decode + the big-tile launch.  Config 5's gate/up (64
-  // experts, ~512 rows each, N = 1408, K = 2048): the MoE line 2.72 ms against 2.86 ms.
-  bool all_q4k = true;
+  // Every routed expert of one type the fused kernel decodes, at most 2048 rows each on
+  // average: the fused grouped kernel (no fp16 decode pass) beats decode + the big-tile
+  // launch.  Config 5's gate/up (64 q4_K experts, ~512 rows each, N = 1408, K = 2048):
+  // the MoE line 2.72 ms against 2.86 ms.
+  const auto types = routed_types(qtype_e, expert_offsets, n_experts, N, K);
   int nz = 0;
-  for (int e = 0; e < n_experts; ++e)
-    if (expert_offsets[e + 1] > expert_offsets[e]) {
-      ++nz;
-      all_q4k = all_q4k && qtype_e[e] == TIERMM_Q4_K;
-    }
-  const bool fused_all = all_q4k && nz > 0 && P <= (size_t)nz * 2048 &&
-                         grouped_q4k_fused(qtype_e, expert_offsets, n_experts, N, K);
+  for (int e = 0; e < n_experts; ++e) nz += expert_offsets[e + 1] > expert_offsets[e];
+  const bool fused_all = types.size() == 1 && types[0].second && P <= (size_t)nz * 2048;
   if (fused_all) chunk = 0;
-  // the grouped big-tile launch and the all-q4_K fused launch read K-tiled planes; the
+  // the grouped big-tile launch and the all-fused launch read K-tiled planes; the
   // per-expert paths row-major ones
   const bool tiled = (chunk || fused_all) && K % 32 == 0 && ((uintptr_t)X_sorted & 15) == 0;
   st = split3_launch(X_sorted, parts, pk, pk, TIERMM_HML, s, false, tiled ? P : 0, K);
@@ -1396,29 +1407,30 @@ int tiermm_qgemm_grouped(const void* const* W_e, const int* qtype_e, const size_
   int cus = 0;
   st = device_cus(&cus);
   if (st) return st;
-  // q4_K experts: one launch (per 64 experts) whose workgroups cover every expert's tiles
-  const bool fused = grouped_q4k_fused(qtype_e, expert_offsets, n_experts, N, K);
-  std::vector<const void*> gw;
-  std::vector<int> g0, gr;
-  size_t grb = 0;
-  for (int e = 0; e < n_experts; ++e) {
-    const int o = expert_offsets[e], Me = expert_offsets[e + 1] - o;
-    if (Me == 0 || qtype_e[e] != TIERMM_Q4_K || !fused) continue;
-    if (grb && rb_e[e] != grb) return set_error(TIERMM_EINVAL, "%s: q4_K experts with different row bytes", who);
-    grb = rb_e[e];
-    gw.push_back(W_e[e]);
-    g0.push_back(o);
-    gr.push_back(Me);
-  }
-  if (!gw.empty()) {
-    st = qgemm_q4k_fused_groups(gw.data(), g0.data(), gr.data(), (int)gw.size(), grb, parts, pk, tiled ? P : 0,
-                                Y_sorted, N, N, K, 0.f, cus, s, who, nullptr);
+  // experts of each fused type: one launch (per 64 experts) whose workgroups cover every
+  // expert's tiles
+  for (auto& t : types) {
+    if (!t.second) continue;
+    std::vector<const void*> gw;
+    std::vector<int> g0, gr;
+    size_t grb = 0;
+    for (int e = 0; e < n_experts; ++e) {
+      const int o = expert_offsets[e], Me = expert_offsets[e + 1] - o;
+      if (Me == 0 || qtype_e[e] != t.first) continue;
+      if (grb && rb_e[e] != grb) return set_error(TIERMM_EINVAL, "%s: experts of one type with different row bytes", who);
+      grb = rb_e[e];
+      gw.push_back(W_e[e]);
+      g0.push_back(o);
+      gr.push_back(Me);
+    }
+    st = qgemm_fused_groups(gw.data(), t.first, g0.data(), gr.data(), (int)gw.size(), grb, parts, pk,
+                            tiled ? P : 0, Y_sorted, N, N, K, 0.f, cus, s, who, nullptr);
     if (st) return st;
   }
   // other types: fp16 W staged per expert, then the x3-ref GEMM on the expert's rows
   for (int e = 0; e < n_experts; ++e) {
     const int o = expert_offsets[e], Me = expert_offsets[e + 1] - o;
-    if (Me == 0 || (qtype_e[e] == TIERMM_Q4_K && fused)) continue;
+    if (Me == 0 || type_fused(types, qtype_e[e])) continue;
     st = dequant_f16_rows(W_e[e], qtype_e[e], rb_e[e], K, (size_t)N, w16, s);
     if (!st) st = x3ref_nt(parts + (size_t)o * K, pk, w16, K, Y_sorted + (size_t)o * N, N, Me, N, K, 0.f, s, who);
     if (st) return st;
