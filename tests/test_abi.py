@@ -132,22 +132,27 @@ def test_workspace_sizes():
     # three planes of B, plus the transposed weight for TIERMM_OP_N
     assert tier_amd.x3_gemm_ws_bytes(5120, 4096, 5120) == 3 * 4096 * 5120 * 2 + 5120 * 5120 * 2
     assert tier_amd.x3_rows_ws_bytes(256, 5120, 14336) == 3 * 256 * 5120 * 2
-    # the fused types decode W inside the GEMM: the three fp16 planes of x, then split-K
-    # partial sums (2 splits at this shape on 256 CUs)
+    # the fused types decode W inside the GEMM at every M: the three fp16 planes of x, then
+    # split-K partial sums (2 splits at this shape on 256 CUs)
     for t in (tier_amd.Q4_K, tier_amd.Q5_K, tier_amd.Q6_K, tier_amd.Q8_0):
         assert tier_amd.qgemm_ws_bytes(t, 512, 5120, 5120) == 3 * 512 * 5120 * 2 + 2 * 512 * 5120 * 4
+        assert tier_amd.qgemm_ws_bytes(t, 4096, 5120, 5120) == 3 * 4096 * 5120 * 2
     assert tier_amd.qgemm_ws_bytes(tier_amd.Q4_K, 512, 14336, 5120) == 3 * 512 * 5120 * 2
-    # other types, and the large-M path of every type, stage fp16 W in the workspace as well
+    # K = 14336 at M = 4096: four K chunks added into Y in turn, no partial sums
+    assert tier_amd.qgemm_ws_bytes(tier_amd.Q5_K, 4096, 5120, 14336) == 3 * 4096 * 14336 * 2
+    # other types stage fp16 W in the workspace as well
     assert tier_amd.qgemm_ws_bytes(tier_amd.Q4_0, 512, 5120, 5120) == 5120 * 5120 * 2 + 3 * 512 * 5120 * 2
-    assert tier_amd.qgemm_ws_bytes(tier_amd.Q6_K, 4096, 5120, 5120) == 5120 * 5120 * 2 + 3 * 4096 * 5120 * 2
     # routed experts: 256-row tiles that fill the chip stage the fp16 weights of
     # up to 64 experts (1 GiB at most); few or mostly empty tiles keep one expert's
     E, N, K = 64, 1408, 2048
     full = [512 * e for e in range(E + 1)]
     planes = 3 * full[-1] * K * 2
-    assert tier_amd.qgemm_grouped_ws_bytes([tier_amd.Q5_0] * E, full, N, K) == planes + 64 * N * K * 2
-    assert tier_amd.qgemm_grouped_ws_bytes([tier_amd.Q5_0] * E, full, 14336, 5120) == \
+    assert tier_amd.qgemm_grouped_ws_bytes([tier_amd.Q4_0] * E, full, N, K) == planes + 64 * N * K * 2
+    assert tier_amd.qgemm_grouped_ws_bytes([tier_amd.Q4_0] * E, full, 14336, 5120) == \
         planes // K * 5120 + (1 << 30) // (14336 * 5120 * 2) * 14336 * 5120 * 2
+    # every routed type decoded inside the GEMM: the planes only
+    assert tier_amd.qgemm_grouped_ws_bytes([tier_amd.Q5_0] * E, full, N, K) == planes
+    assert tier_amd.qgemm_grouped_ws_bytes([tier_amd.Q4_K, tier_amd.Q6_K] * (E // 2), full, N, K) == planes
     sparse = [100 * e for e in range(E + 1)]  # 100 rows per 256-row tile
     assert tier_amd.qgemm_grouped_ws_bytes([tier_amd.Q4_0] * E, sparse, N, K) == \
         3 * sparse[-1] * K * 2 + N * K * 2

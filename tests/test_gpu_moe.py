@@ -84,14 +84,21 @@ def test_grouped_gemm_and_combine(gpu, t, N, K):
     assert oracle.rel_fro(out, ref) <= BAR
 
 
+MIXED = {"fused": [tier_amd.Q4_K, tier_amd.Q5_0, tier_amd.Q8_0, tier_amd.Q6_K],
+         "staged": [tier_amd.Q4_K, tier_amd.Q4_0, tier_amd.Q8_0, tier_amd.Q3_K]}
+
+
 @pytest.mark.parametrize("with_ws", [False, True])
-def test_grouped_big_tiles_mixed_types(gpu, with_ws):
-    """Routed rows that fill the chip with 256-row tiles (the grouped 256x320 path):
-    70 experts (two chunks of at most 64), four weight types in one call, an empty
-    expert, a one-row expert and ragged row counts."""
+@pytest.mark.parametrize("kind", ["fused", "staged"])
+def test_grouped_big_tiles_mixed_types(gpu, with_ws, kind):
+    """Routed rows that fill the chip with 256-row tiles: 70 experts (two groups of at
+    most 64 per launch), four weight types in one call, an empty expert, a one-row
+    expert and ragged row counts.  "fused": every type is decoded inside the GEMM, one
+    fused launch per type; "staged": one type (q4_0, q3_K) is not, so every expert goes
+    through fp16 staging and the grouped 256x320 launch."""
     rng = np.random.default_rng(70)
     E, N, K = 70, 640, 256
-    types = [tier_amd.Q4_K, tier_amd.Q5_0, tier_amd.Q8_0, tier_amd.Q6_K]
+    types = MIXED[kind]
     counts = rng.integers(260, 330, E)
     counts[3], counts[11], counts[40] = 0, 1, 257
     offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
@@ -105,7 +112,8 @@ def test_grouped_big_tiles_mixed_types(gpu, with_ws):
     ws = wsb = None
     if with_ws:
         wsb = tier_amd.qgemm_grouped_ws_bytes(qt, offsets.tolist(), N, K)
-        assert wsb >= 3 * P * K * 2 + 64 * N * K * 2  # planes + one chunk of fp16 experts
+        # planes, plus one chunk of fp16 experts when staged
+        assert wsb == 3 * P * K * 2 if kind == "fused" else wsb >= 3 * P * K * 2 + 64 * N * K * 2
         ws = hip.DeviceBuffer(wsb)
     tier_amd.qgemm_grouped([w.ptr for w in dW], qt, rbs, X.ptr, offsets.tolist(), Y.ptr, N, K,
                            ws=ws.ptr if ws else None, ws_bytes=wsb or 0)

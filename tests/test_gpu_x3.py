@@ -153,14 +153,17 @@ def test_qgemm_x3ref(gpu, name, t, M, N, K):
     assert oracle.rel_fro(got, ref) <= BAR
 
 
-@pytest.mark.parametrize("t,beta,M", [(tier_amd.Q4_K, 0.0, 4096), (tier_amd.Q5_K, 1.0, 4000), (tier_amd.Q6_K, 0.0, 4096)])
+@pytest.mark.parametrize("t,beta,M", [(tier_amd.Q4_0, 0.0, 4096), (tier_amd.Q3_K, 1.0, 4000),
+                                      (tier_amd.IQ4_XS, 0.0, 4096), (tier_amd.Q4_K, 0.0, 4096),
+                                      (tier_amd.Q5_K, 1.0, 4000), (tier_amd.Q6_K, 0.0, 4096)])
 def test_qgemm_big_tiles_k_tiled_planes(gpu, t, beta, M):
-    """Large M (the fp16 staging + big-tile x3-ref path, whose planes are K-tiled): a
-    partial last column tile, beta = 1; an x that is only 4-byte aligned takes the
-    row-major planes instead, and both give the same bits (M = 4000: a partial last row
-    tile too)."""
+    """Large M: a partial last column tile, beta = 1; an x that is only 4-byte aligned
+    takes row-major planes instead of K-tiled ones, and both give the same bits (M = 4000:
+    a partial last row tile too).  q4_0, q3_K and IQ4_XS go through fp16 staging and the
+    big-tile x3-ref GEMM; q4_K, q5_K and q6_K through the fused kernel's wide tiles."""
     N, K = 4000, 512
-    blocks = quantized_weight(t, N, K, seed=40 + t)
+    be, _ = oracle.block(t)
+    blocks = oracle.random_blocks(np.random.default_rng(40 + t), t, N * (K // be)).reshape(N, -1)
     x = activations(M, K, seed=41)
     y0 = np.random.default_rng(42).standard_normal((M, N)).astype(np.float32)
     W = hip.to_device(blocks)
@@ -232,7 +235,7 @@ def test_qgemm_fused_decode_bit_exact(gpu, monkeypatch, name, t, K, bn, scale):
     assert np.array_equal(got, w16.T)  # +0 and -0 compare equal: a zero weight sums to +0
 
 
-TYPE_PLANS = [(160, 1), (160, 2), (128, 4), (96, 2), (64, 1), (64, 4)]
+TYPE_PLANS = [(256, 1), (224, 2), (160, 1), (160, 2), (128, 4), (64, 1), (64, 4)]
 
 
 @pytest.mark.parametrize("name,t", [(f[0], f[1]) for f in FUSED[1:]], ids=[f[0] for f in FUSED[1:]])
@@ -256,6 +259,31 @@ def test_qgemm_fused_type_plans(gpu, monkeypatch, name, t, bn, ks):
     w16 = oracle.h2f(oracle.dequant(blocks, t, K, oracle.OUT_F16)).reshape(N, K)
     ref = x.astype(np.float64) @ w16.astype(np.float64).T + beta * y0.astype(np.float64)
     assert np.all(np.isfinite(got))
+    assert oracle.rel_fro(got, ref) <= BAR
+
+
+@pytest.mark.parametrize("plan", ["128,1,2", "256,2", "160,1,2", "default"])
+@pytest.mark.parametrize("t", [tier_amd.Q4_K, tier_amd.Q6_K])
+def test_qgemm_fused_k_chunks(gpu, monkeypatch, t, plan):
+    """K = 8192, beyond one accumulator's 6144: two K chunks, either launched in turn with
+    the second adding into Y (BN,1,2) or as two splits with partial sums (BN,2); beta = 1
+    on top of both."""
+    if plan != "default":
+        monkeypatch.setenv("TIERMM_QGEMM_TILE", plan)
+    M, N, K, beta = 300, 1000, 8192, 1.0
+    ks = int(plan.split(",")[1]) if plan != "default" else None
+    if ks is not None:
+        assert tier_amd.qgemm_ws_bytes(t, M, N, K) == 3 * M * K * 2 + (ks * M * N * 4 if ks > 1 else 0)
+    rng = np.random.default_rng(K + t + len(plan))
+    blocks = oracle.random_blocks(rng, t, N * (K // 256)).reshape(N, -1)
+    x = activations(M, K, seed=27)
+    y0 = rng.standard_normal((M, N)).astype(np.float32)
+    W, X, Y = hip.to_device(blocks), hip.to_device(x), hip.to_device(y0)
+    tier_amd.qgemm(W.ptr, t, tier_amd.q_row_bytes(t, K), X.ptr, Y.ptr, M, N, K, beta=beta)
+    hip.synchronize()
+    got = Y.download(np.float32, M * N).reshape(M, N)
+    w16 = oracle.h2f(oracle.dequant(blocks, t, K, oracle.OUT_F16)).reshape(N, K)
+    ref = x.astype(np.float64) @ w16.astype(np.float64).T + beta * y0.astype(np.float64)
     assert oracle.rel_fro(got, ref) <= BAR
 
 
@@ -304,8 +332,8 @@ def test_qgemm_q4k_fused_x_layouts(gpu, M, N, K):
     assert oracle.rel_fro(got, x.astype(np.float64) @ w16.astype(np.float64).T) <= BAR
 
 
-@pytest.mark.parametrize("bn,ks", [(160, 1), (160, 2), (160, 4), (128, 2), (112, 4), (96, 2), (80, 4), (64, 2),
-                                   (64, 1)])
+@pytest.mark.parametrize("bn,ks", [(256, 1), (256, 4), (224, 2), (192, 1), (160, 1), (160, 2), (160, 4), (128, 2),
+                                   (112, 4), (96, 2), (80, 4), (64, 2), (64, 1)])
 @pytest.mark.parametrize("M,N,K,beta", [(300, 1000, 1024, 1.0), (512, 352, 2048, 0.0)])
 def test_qgemm_q4k_tile_plans(gpu, monkeypatch, bn, ks, M, N, K, beta):
     """Every tile width and split-K factor of the fused q4_K kernel, forced through

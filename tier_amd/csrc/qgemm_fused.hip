@@ -79,6 +79,7 @@ struct QArgs {
   float* Y;
   size_t rb;
   int ldy, N, K;
+  int kcs;      // accumulation chunks (KS == 1): K steps per chunk, each chunk's sum added into Y
   float beta;
   float* P;   // split K: partial sums of split kz at P + kz * ps, rows of N floats
   size_t ps;
@@ -95,20 +96,23 @@ __device__ __forceinline__ void lds_rel(int* p, int v) {
   __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// Waits until the four flags at f (16-byte aligned, LDS) are all >= v: one
-// 16-byte read per try.  The flags only grow, and the data they publish is read
-// after this returns (the empty asm keeps those reads below the loop).
-__device__ __forceinline__ void poll4(const int* f, int v) {
-  typedef int i4 __attribute__((ext_vector_type(4)));
-  const volatile __attribute__((address_space(3))) i4* fl =
-      (const volatile __attribute__((address_space(3))) i4*)(size_t)lds_addr(f);
-  for (;;) {
-    const i4 t = *fl;
-    if (min(min(t[0], t[1]), min(t[2], t[3])) >= v) break;
+// The four flags at f (16-byte aligned, LDS), one 16-byte read.
+typedef int i4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i4 flags_read(const int* f) {
+  return *(const volatile __attribute__((address_space(3))) i4*)(size_t)lds_addr(f);
+}
+// Waits until the four flags at f are all >= v, starting from the values t read
+// earlier (flags_read), so the first read can be issued well before the check.  The
+// flags only grow, and the data they publish is read after this returns (the empty
+// asm keeps those reads below the loop).
+__device__ __forceinline__ void flags_wait(const int* f, i4 t, int v) {
+  while (min(min(t[0], t[1]), min(t[2], t[3])) < v) {
     __builtin_amdgcn_s_sleep(1);
+    t = flags_read(f);
   }
   asm volatile("" ::: "memory");
 }
+__device__ __forceinline__ void poll4(const int* f, int v) { flags_wait(f, flags_read(f), v); }
 
 // ------------------------------------------------------------ decode units
 // The producers of the types other than q4_K work a unit of U K steps at a time (the
@@ -343,16 +347,18 @@ struct Unit<QT_Q6_K> {
 // writes the pair q, q + 1 once stage q + 1 - NBR is read).  That stage is
 // below q, its ready published by every producer, so each wait ends; a consumer
 // waits only for its own loads and for ready.
-template <int QT, int BN, int KS>
+template <int QT, int BN, int KS, bool CH>
 __global__ __launch_bounds__(512) void qgemm_fused_x3ref(const QArgs p) {
   constexpr int NB = BN / 16;
-  constexpr int NBR = QNBR, FL = 4, XR = 4, DP = 4;
+  // x fragments XR stages ahead: the depth is not what limits (2 and 4 time alike), so the
+  // wide tiles, whose accumulators need the registers, and the chunked variant keep two
+  constexpr int NBR = QNBR, FL = 4, XR = BN > 160 || CH ? 2 : 4, DP = 4;
   constexpr int PR = BN / 4;
   constexpr int LPR = 2 * PR <= 64 ? 2 : 1, HPL = 2 / LPR;  // decode: lanes per row, halves per lane
   constexpr int NL = 1 + HPL;                                // producer loads per sub-block pair
   constexpr int BPART = BN * 64;
   constexpr int FLAGOFF = NBR * BPART;
-  static_assert(BN % 16 == 0 && BN <= 160, "tile width");
+  static_assert(BN % 16 == 0 && BN <= 256, "tile width");
   static_assert(LPR * PR <= 64, "one decode pass per producer");
   static_assert(NBR <= FL && NBR >= 3 && NL * DP <= 63, "ring depths");
   extern __shared__ __attribute__((aligned(16))) uint16_t lds_h[];
@@ -536,6 +542,52 @@ __global__ __launch_bounds__(512) void qgemm_fused_x3ref(const QArgs p) {
     for (int j = 0; j < NB; ++j) acc[i][j] = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int d = 0; d < XR - 1; ++d) loadA(d, A[d]);
+  // Stores the accumulators (register i of lane l holds row 4*(l/16) + i, column l%16
+  // of a 16x16 block): into Y, Y = acc + beta Y, or split kz's partial sums.  With
+  // accumulation chunks (kcs) it runs at the end of each chunk, which adds the
+  // chunk's sum into Y (beta = 1 after the first) and starts the next from zero.
+  auto store = [&](float beta) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int col = n0 + j * 16 + (lane & 15);
+      if (col >= p.N) continue;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = m0 + c * 32 + i * 16 + 4 * (lane >> 4) + r;
+          if (row >= M) continue;
+          if constexpr (KS == 1) {
+            float* cp = Yg + (size_t)row * p.ldy + col;
+            float v = acc[i][j][r];
+            if (beta != 0.f) v = fmaf(beta, *cp, v);
+            *cp = v;
+          } else {
+            p.P[(size_t)kz * p.ps + (size_t)row * p.N + col] = acc[i][j][r];  // split K: one group
+          }
+        }
+    }
+  };
+  float chunk_beta = p.beta;
+  // B fragments one stage ahead, in two register sets (stage q in set q & 1; XR is
+  // even, so the set follows u): stage q + 1's flags are read when stage q starts,
+  // checked and its fragments loaded after the first part's MFMAs, so neither the
+  // flag read nor the fragment reads stall the MFMA issue.  Stage q's slot is
+  // released once its fragments are in registers, before its last MFMAs.
+  // (At BN = 160, and with accumulation chunks, the second set does not fit in
+  // registers: fragments are read when the stage starts.)
+  constexpr bool PIPE = NB <= 8 && !CH;
+  static_assert(XR % 2 == 0, "B register sets follow u");
+  half8 bf[PIPE ? 2 : 1][NB];
+  auto readB = [&](int q, half8 (&dst)[NB]) __attribute__((always_inline)) {
+    const uint8_t* bs = lds + (q % NBR) * BPART;
+#pragma unroll
+    for (int j = 0; j < NB; ++j) dst[j] = *(const half8*)(bs + j * 1024 + fo);
+  };
+  if constexpr (PIPE) {
+    poll4(ready, 0);
+    readB(0, bf[0]);
+  }
   for (int q0 = 0; q0 < nk; q0 += XR) {
 #pragma unroll
     for (int u = 0; u < XR; ++u) {
@@ -543,47 +595,47 @@ __global__ __launch_bounds__(512) void qgemm_fused_x3ref(const QArgs p) {
       loadA(q + XR - 1, A[(u + XR - 1) % XR]);
       __builtin_amdgcn_s_waitcnt(WAITVM(6 * (XR - 1)));  // stage q's fragments are in registers
       if (q < nk) {
-        const int sl = q % FL;
-        poll4(ready + 4 * sl, q);
-        const uint8_t* bs = lds + (q % NBR) * BPART;
-        half8 bf[NB];
-#pragma unroll
-        for (int j = 0; j < NB; ++j) bf[j] = *(const half8*)(bs + j * 1024 + fo);
+        const bool more = PIPE && q + 1 < nk;
+        const int* fn = ready + 4 * ((q + 1) % FL);
+        i4 t{};
+        if (more) t = flags_read(fn);
+        if constexpr (!PIPE) {
+          poll4(ready + 4 * (q % FL), q);
+          readB(q, bf[0]);
+        }
+        const int cur = PIPE ? (u & 1) : 0;  // u is a constant after unrolling
         // parts lo, mid, hi (tier.cpp:940) into one fp32 accumulator
 #pragma unroll
-        for (int part = 2; part >= 0; --part)
+        for (int part = 2; part >= 0; --part) {
 #pragma unroll
           for (int j = 0; j < NB; ++j)
 #pragma unroll
             for (int i = 0; i < 2; ++i)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, A[u][part][i]), bf[j],
-                                                                 acc[i][j], 0, 0, 0);
-        if (lane == 0) lds_rel(&done[4 * sl + c], q);
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, A[u][part][i]),
+                                                                 bf[cur][j], acc[i][j], 0, 0, 0);
+          if (part == 2) {
+            if (lane == 0) lds_rel(&done[4 * (q % FL) + c], q);  // stage q's B tile is in registers
+            if (more) {
+              flags_wait(fn, t, q + 1);
+              readB(q + 1, bf[PIPE ? (u + 1) & 1 : 0]);
+            }
+          }
+        }
+      }
+    }
+    if constexpr (CH) {
+      if ((q0 + XR) % p.kcs == 0 && q0 + XR < nk) {  // end of an accumulation chunk
+        store(chunk_beta);
+        chunk_beta = 1.f;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < NB; ++j) acc[i][j] = float4v{0.f, 0.f, 0.f, 0.f};
       }
     }
   }
 
-  // epilogue: register i of lane l holds row 4*(l/16) + i, column l%16 of a 16x16 block
-#pragma unroll
-  for (int j = 0; j < NB; ++j) {
-    const int col = n0 + j * 16 + (lane & 15);
-    if (col >= p.N) continue;
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = m0 + c * 32 + i * 16 + 4 * (lane >> 4) + r;
-        if (row >= M) continue;
-        if constexpr (KS == 1) {
-          float* cp = Yg + (size_t)row * p.ldy + col;
-          float v = acc[i][j][r];
-          if (p.beta != 0.f) v = fmaf(p.beta, *cp, v);
-          *cp = v;
-        } else {
-          p.P[(size_t)kz * p.ps + (size_t)row * p.N + col] = acc[i][j][r];  // split K: one group
-        }
-      }
-  }
+  store(chunk_beta);
 }
 
 // Y (beta)= sum of the KS partial sums, in split order, for rows [0, rows).
@@ -598,23 +650,26 @@ __global__ __launch_bounds__(256) void qgemm_splitk_reduce(const float* __restri
   *y = v;
 }
 
-template <int QT, int BN, int KS>
+template <int QT, int BN, int KS, bool CH = false>
 int launch_q(const QArgs& a, hipStream_t s, const char* who) {
   constexpr size_t lds = QNBR * (size_t)BN * 64 + 2 * 4 * 4 * 4;
   static_assert(lds <= 160 * 1024, "LDS budget");
   static std::atomic<uint64_t> attr{0};
-  int st = lds_attr_once(attr, (const void*)qgemm_fused_x3ref<QT, BN, KS>, (int)lds, who);
+  int st = lds_attr_once(attr, (const void*)qgemm_fused_x3ref<QT, BN, KS, CH>, (int)lds, who);
   if (st) return st;
-  qgemm_fused_x3ref<QT, BN, KS><<<(unsigned)a.tile0[a.ngroups] * KS, 512, lds, s>>>(a);
+  qgemm_fused_x3ref<QT, BN, KS, CH><<<(unsigned)a.tile0[a.ngroups] * KS, 512, lds, s>>>(a);
   TM_LAUNCH_CHECK(who);
   return TIERMM_OK;
 }
 
-// q4_K takes every tile width of kBns; the other types 160, 128, 96 and 64.
+// q4_K takes every tile width of kBns; the other types 256, 224, 160, 128 and 64.
 template <int QT, int KS>
 int launch_q_bn(int bn, const QArgs& a, hipStream_t s, const char* who) {
   if constexpr (QT == QT_Q4_K) {
     switch (bn) {
+      case 256: return launch_q<QT, 256, KS>(a, s, who);
+      case 224: return launch_q<QT, 224, KS>(a, s, who);
+      case 192: return launch_q<QT, 192, KS>(a, s, who);
       case 160: return launch_q<QT, 160, KS>(a, s, who);
       case 128: return launch_q<QT, 128, KS>(a, s, who);
       case 112: return launch_q<QT, 112, KS>(a, s, who);
@@ -624,9 +679,10 @@ int launch_q_bn(int bn, const QArgs& a, hipStream_t s, const char* who) {
     }
   } else {
     switch (bn) {
+      case 256: return launch_q<QT, 256, KS>(a, s, who);
+      case 224: return launch_q<QT, 224, KS>(a, s, who);
       case 160: return launch_q<QT, 160, KS>(a, s, who);
       case 128: return launch_q<QT, 128, KS>(a, s, who);
-      case 96: return launch_q<QT, 96, KS>(a, s, who);
       default: return launch_q<QT, 64, KS>(a, s, who);
     }
   }
@@ -634,6 +690,10 @@ int launch_q_bn(int bn, const QArgs& a, hipStream_t s, const char* who) {
 
 template <int QT>
 int launch_q_plan(int bn, int ks, const QArgs& a, hipStream_t s, const char* who) {
+  if (a.kcs) {  // accumulation chunks: KS = 1, BN = 160 or 128 (wider ones spill with the chunk store)
+    if (bn == 160) return launch_q<QT, 160, 1, true>(a, s, who);
+    return launch_q<QT, 128, 1, true>(a, s, who);
+  }
   switch (ks) {
     case 4: return launch_q_bn<QT, 4>(bn, a, s, who);
     case 2: return launch_q_bn<QT, 2>(bn, a, s, who);
@@ -648,17 +708,23 @@ long q_tiles(const int* rows, int n, int N, int bn) {
   return t;
 }
 
-constexpr int kBns[6] = {160, 128, 112, 96, 80, 64};
-// Per-workgroup time model, us: kRound + kUnit[BN] * BN * (K steps of the split), fitted to
-// 512x{5120,14336,4096,1024,2048,1408}x{5120,14336,4096,2048} and {256,1024,2048}x5120x5120
-// on MI355X with q4_K weights (every (BN, KS) of the sweep; the model picks the measured
-// best in each).  The other types use the same model.
-constexpr double kRound = 12.0;
-constexpr double kUnit[6] = {6.25e-3, 6.8e-3, 7.0e-3, 8.0e-3, 8.7e-3, 10.5e-3};
+constexpr int kNbn = 9;
+constexpr int kBns[kNbn] = {256, 224, 192, 160, 128, 112, 96, 80, 64};
+// Per-workgroup time model, us: kRound + kUnit[BN] * BN * (K steps of the split), fitted
+// (log least squares, rms error 6 %) to every (BN, KS) of q4_K at M in {256, 512, 1024,
+// 2048, 4096} x (N, K) in {5120, 14336, 4096, 1024} x 5120, 5120 x {14336, 4096} on
+// MI355X.  Its pick is the measured best in 26 of those 29 shapes and within 2.2 % of
+// it in 28.  The other types use the same model.
+constexpr double kRound = 4.26;
+constexpr double kUnit[kNbn] = {3.83e-3, 3.915e-3, 4.013e-3, 4.277e-3, 4.442e-3, 4.553e-3, 4.723e-3, 5.247e-3, 6.031e-3};
+constexpr double kReduceBpus = 2.93e6;  // bytes per us of the split-K reduce
 constexpr size_t kMaxPartials = (size_t)256 << 20;  // bytes of split-K partial sums
 
+// KS > 1: the K steps split KS ways, partial sums added by a second kernel; KC > 1:
+// each workgroup sums KC consecutive K ranges in turn, adding each range's sum into its
+// Y tile (for K beyond one accumulator's chunk when the partial sums would not fit).
 struct QPlan {
-  int bn, ks;
+  int bn, ks, kc;
 };
 
 // Weight types the fused kernel decodes, and the K steps of one producer unit: a split
@@ -674,43 +740,48 @@ int fused_unit(int qt) {
   }
 }
 
-bool plan_ok(int qt, int bn, int ks, int K, size_t rows_total, int N, bool split) {
+bool plan_ok(int qt, int bn, int ks, int kc, int K, size_t rows_total, int N, bool split) {
   const int unit = fused_unit(qt);
-  if (!unit || K % QBK || (K / QBK) % (unit * ks)) return false;
-  if (ks > 1 && (!split || (size_t)ks * rows_total * N * 4 > kMaxPartials)) return false;
-  if (ks < acc_chunks(K)) return false;  // each split's accumulator sums at most the chunk of the x3 GEMMs
-  if (ks != 1 && ks != 2 && ks != 4) return false;
+  if (!unit || K % QBK || (K / QBK) % (unit * ks * kc)) return false;
+  if (ks > 1 && (!split || kc > 1 || (size_t)ks * rows_total * N * 4 > kMaxPartials)) return false;
+  if (ks * kc < acc_chunks(K)) return false;  // each accumulator sums at most the chunk of the x3 GEMMs
+  if ((ks != 1 && ks != 2 && ks != 4) || kc < 1 || kc > 8) return false;
+  if (kc > 1 && ((K / QBK / kc) % 4 || ks > 1 || (bn != 160 && bn != 128)))
+    return false;  // chunks end where the consumer's unrolled steps do; the chunked widths
   if (qt == QT_Q4_K) {
     for (int b : kBns)
       if (b == bn) return true;
     return false;
   }
-  return bn == 160 || bn == 128 || bn == 96 || bn == 64;
+  return bn == 256 || bn == 224 || bn == 160 || bn == 128 || bn == 64;
 }
 
-// (BN, KS) for the fused kernel.  TIERMM_QGEMM_TILE="BN,KS" overrides the model when
-// the pair is valid for the shape (tests and tuning).
+// (BN, KS, KC) for the fused kernel.  TIERMM_QGEMM_TILE="BN,KS[,KC]" overrides the model
+// when the plan is valid for the shape (tests and tuning).
 QPlan q_plan(int qt, const int* rows, int n, int N, int K, int cus, bool split) {
   size_t rows_total = 0;
   for (int g = 0; g < n; ++g) rows_total += (size_t)rows[g];
   if (const char* e = getenv("TIERMM_QGEMM_TILE")) {
-    int bn = 0, ks = 0;
-    if (sscanf(e, "%d,%d", &bn, &ks) == 2 && plan_ok(qt, bn, ks, K, rows_total, N, split)) return {bn, ks};
+    int bn = 0, ks = 0, kc = 1;
+    if (sscanf(e, "%d,%d,%d", &bn, &ks, &kc) >= 2 && plan_ok(qt, bn, ks, kc, K, rows_total, N, split))
+      return {bn, ks, kc};
   }
   const int nk = K / QBK;
-  QPlan best{0, 0};  // none: the shape does not take the fused kernel
+  QPlan best{0, 0, 0};  // none: the shape does not take the fused kernel
   double best_t = -1;
-  for (int i = 0; i < 6; ++i)
-    for (int ks = 1; ks <= 4; ks *= 2) {
-      if (!plan_ok(qt, kBns[i], ks, K, rows_total, N, split)) continue;
-      const long wg = q_tiles(rows, n, N, kBns[i]) * ks;
-      double t = (double)((wg + cus - 1) / cus) * (kRound + kUnit[i] * kBns[i] * nk / ks);
-      if (ks > 1) t += (double)rows_total * N * 4 * (ks + 1) / 4e6;  // the reduce, ~4 TB/s
-      if (best_t < 0 || t < best_t) {
-        best_t = t;
-        best = {kBns[i], ks};
+  const int need = acc_chunks(K);
+  for (int i = 0; i < kNbn; ++i)
+    for (int ks = 1; ks <= 4; ks *= 2)
+      for (int kc : {1, need}) {
+        if (!plan_ok(qt, kBns[i], ks, kc, K, rows_total, N, split)) continue;
+        const long wg = q_tiles(rows, n, N, kBns[i]) * ks;
+        double t = (double)((wg + cus - 1) / cus) * (kRound + kUnit[i] * kBns[i] * nk / ks);
+        if (ks > 1) t += (double)rows_total * N * 4 * (ks + 1) / kReduceBpus;  // the reduce
+        if (best_t < 0 || t < best_t) {
+          best_t = t;
+          best = {kBns[i], ks, kc};
+        }
       }
-    }
   return best;
 }
 
@@ -749,6 +820,7 @@ int qgemm_fused_groups(const void* const* W, int qtype, const int* row0, const i
   for (int g0 = 0; g0 < n; g0 += QG) {
     QArgs a{};
     a.X = xparts; a.xs = xs; a.xt = xt; a.Y = Y; a.rb = rb; a.ldy = ldy; a.N = N; a.K = K; a.beta = beta;
+    a.kcs = pl.kc > 1 ? K / QBK / pl.kc : 0;
     a.P = partials; a.ps = n == 1 ? (size_t)rows[0] * N : 0;
     a.ngroups = 0;
     a.tile0[0] = 0;
@@ -770,7 +842,7 @@ int qgemm_fused_groups(const void* const* W, int qtype, const int* row0, const i
       default: st = launch_q_plan<QT_Q5_0>(pl.bn, pl.ks, a, s, who); break;
     }
     if (st) return st;
-    if (pl.ks > 1) {  // n == 1: rows row0[0].. of Y
+    if (pl.ks > 1) {  // n == 1, kc == 1: rows row0[0].. of Y
       const size_t cnt = (size_t)rows[0] * N;
       qgemm_splitk_reduce<<<(unsigned)((cnt + 255) / 256), 256, 0, s>>>(partials, a.ps, pl.ks,
                                                                        Y + (size_t)row0[0] * ldy, ldy, rows[0], N,

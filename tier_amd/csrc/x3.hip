@@ -1208,7 +1208,7 @@ size_t tiermm_qgemm_ws_bytes(int qtype, int M, int N, int K, int mode) {
     return al256((size_t)N * K * 4) + 2 * al256((size_t)N * K * 2) + al256((size_t)N * 4) +
            2 * al256((size_t)M * K * 2) + al256((size_t)M * 4);
   const size_t parts = (size_t)3 * M * K * sizeof(uint16_t);  // x split in three fp16 planes
-  if (big_tiles(M, N) < 192 && qgemm_fusable(qtype, &M, 1, N, K, true))
+  if (qgemm_fusable(qtype, &M, 1, N, K, true))
     return al256(parts) + qgemm_fused_partials_bytes(qtype, M, N, K);  // W decoded inside the GEMM; split-K partials
   return (size_t)N * K * sizeof(uint16_t) + parts;                   // W16 staged in the workspace
 }
@@ -1254,7 +1254,9 @@ int tiermm_qgemm(const void* W, int qtype, size_t rb, const float* X, float* Y, 
     if (big_tiles(M, N) >= 192) return launch_x3_big<X3_2X2>(a, s, who);
     return launch_x3<128, 128, X3_2X2>(a, s, who);
   }
-  if (big_tiles(M, N) < 192 && qgemm_fusable(qtype, &M, 1, N, K, true)) {  // small M: decode W inside the GEMM
+  // The types the fused kernel decodes, at every M: W is decoded inside the GEMM (at
+  // M = 4096 the wide-tile plans beat fp16 staging + the big-tile GEMM by 5-25 %).
+  if (qgemm_fusable(qtype, &M, 1, N, K, true)) {
     uint16_t* parts = (uint16_t*)w;
     float* partials = (float*)((uint8_t*)w + al256(3 * mk * sizeof(uint16_t)));
     // K-tiled planes where x allows (a fragment load is then one contiguous kilobyte)
@@ -1298,11 +1300,11 @@ size_t tiermm_qgemm_grouped_ws_bytes(const int* qtype_e, const int* expert_offse
   // chunk of experts (grouped 256x320 launch) or of one expert at a time (the
   // experts that are not decoded inside the GEMM)
   const size_t P = n_experts > 0 ? (size_t)expert_offsets[n_experts] : 0;
-  const int chunk = n_experts > 0 ? big_group_chunk(expert_offsets, n_experts, N, K) : 0;
-  if (chunk) return al256(3 * P * K * sizeof(uint16_t)) + chunk * al256((size_t)N * K * sizeof(uint16_t));
   const auto types = routed_types(qtype_e, expert_offsets, n_experts, N, K);
   bool staged = false;
   for (auto& t : types) staged = staged || !t.second;
+  const int chunk = staged && n_experts > 0 ? big_group_chunk(expert_offsets, n_experts, N, K) : 0;
+  if (chunk) return al256(3 * P * K * sizeof(uint16_t)) + chunk * al256((size_t)N * K * sizeof(uint16_t));
   return al256(3 * P * K * sizeof(uint16_t)) + (staged ? (size_t)N * K * sizeof(uint16_t) : 0);
 }
 
@@ -1344,19 +1346,18 @@ int tiermm_qgemm_grouped(const void* const* W_e, const int* qtype_e, const size_
   const size_t P = (size_t)expert_offsets[n_experts], pk = P * K;
   uint16_t* parts = (uint16_t*)w;
   uint16_t* w16 = (uint16_t*)((uint8_t*)w + al256(3 * pk * sizeof(uint16_t)));
-  int chunk = big_group_chunk(expert_offsets, n_experts, N, K);
-  // Every routed expert of one type the fused kernel decodes, at most 2048 rows each on
-  // average: the fused grouped kernel (no fp16 decode pass) beats decode + the big-tile
-  // launch.  Config 5's gate/up (64 q4_K experts, ~512 rows each, N = 1408, K = 2048):
-  // the MoE line 2.72 ms against 2.86 ms.
+  // Every routed type one the fused kernel decodes: one fused launch per type (no fp16
+  // decode pass), which beats decode + the grouped big-tile launch (config 5's gate/up,
+  // 64 q4_K experts of ~512 rows, N = 1408, K = 2048: the MoE line 2.72 ms against
+  // 2.86 ms).  Otherwise, where the experts' 256-row tiles fill the chip, every expert
+  // goes through fp16 staging and the grouped big-tile launch.
   const auto types = routed_types(qtype_e, expert_offsets, n_experts, N, K);
-  int nz = 0;
-  for (int e = 0; e < n_experts; ++e) nz += expert_offsets[e + 1] > expert_offsets[e];
-  const bool fused_all = types.size() == 1 && types[0].second && P <= (size_t)nz * 2048;
-  if (fused_all) chunk = 0;
-  // the grouped big-tile launch and the all-fused launch read K-tiled planes; the
+  bool all_fused = !types.empty();
+  for (auto& t : types) all_fused = all_fused && t.second;
+  const int chunk = all_fused ? 0 : big_group_chunk(expert_offsets, n_experts, N, K);
+  // the grouped big-tile launch and the all-fused launches read K-tiled planes; the
   // per-expert paths row-major ones
-  const bool tiled = (chunk || fused_all) && K % 32 == 0 && ((uintptr_t)X_sorted & 15) == 0;
+  const bool tiled = (chunk || all_fused) && K % 32 == 0 && ((uintptr_t)X_sorted & 15) == 0;
   st = split3_launch(X_sorted, parts, pk, pk, TIERMM_HML, s, false, tiled ? P : 0, K);
   if (st) return st;
   if (chunk) {  // fp16 weights of up to `chunk` experts, then one grouped launch over their tiles
