@@ -224,9 +224,11 @@ int tiermm_x3s_gemm(const uint16_t* Xhi, const uint16_t* Xlo, const int32_t* xex
  * semantics (fp32 dequant, then an fp32 GEMM, tier.cpp:2358-2359): rel.
  * Frobenius error <= 2^-20 against fp64(deq(W) * X).  qtype: the GPU types of
  * tiermm_dequant.  The workspace (tiermm_qgemm_ws_bytes) holds the x parts and,
- * for q4_K at small M, the split-K partial sums; the environment variable
- * TIERMM_QGEMM_TILE="BN,KS" overrides that kernel's tile width and split count
- * (read at each call, and by the size query; ignored when invalid for the shape). */
+ * for q8_0 / q4_K / q5_K / q6_K / q5_0 (decoded inside the GEMM), the split-K partial
+ * sums, or for the other types the fp16 weight; the environment variable
+ * TIERMM_QGEMM_TILE="BN,KS[,KC]" overrides the fused kernel's tile width, split count
+ * and accumulation chunks (read at each call, and by the size query; ignored when
+ * invalid for the shape). */
 int tiermm_qgemm(const void* W, int qtype, size_t rb, const float* X, float* Y, int M, int N,
                  int K, int ldy, int mode, float beta, void* ws, size_t ws_bytes,
                  tiermm_stream_t stream);
