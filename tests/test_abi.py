@@ -138,8 +138,11 @@ def test_workspace_sizes():
         assert tier_amd.qgemm_ws_bytes(t, 512, 5120, 5120) == 3 * 512 * 5120 * 2 + 2 * 512 * 5120 * 4
         assert tier_amd.qgemm_ws_bytes(t, 4096, 5120, 5120) == 3 * 4096 * 5120 * 2
     assert tier_amd.qgemm_ws_bytes(tier_amd.Q4_K, 512, 14336, 5120) == 3 * 512 * 5120 * 2
-    # K = 14336 at M = 4096: four K chunks added into Y in turn, no partial sums
-    assert tier_amd.qgemm_ws_bytes(tier_amd.Q5_K, 4096, 5120, 14336) == 3 * 4096 * 14336 * 2
+    # K = 14336 at M = 4096: four K splits with partial sums (up to 1 GiB of them); at
+    # M = 16384 those would not fit, and four K chunks are added into Y in turn instead
+    assert tier_amd.qgemm_ws_bytes(tier_amd.Q5_K, 4096, 5120, 14336) == \
+        3 * 4096 * 14336 * 2 + 4 * 4096 * 5120 * 4
+    assert tier_amd.qgemm_ws_bytes(tier_amd.Q5_K, 16384, 5120, 14336) == 3 * 16384 * 14336 * 2
     # other types stage fp16 W in the workspace as well
     assert tier_amd.qgemm_ws_bytes(tier_amd.Q4_0, 512, 5120, 5120) == 5120 * 5120 * 2 + 3 * 512 * 5120 * 2
     # routed experts: 256-row tiles that fill the chip stage the fp16 weights of

@@ -718,7 +718,12 @@ constexpr int kBns[kNbn] = {256, 224, 192, 160, 128, 112, 96, 80, 64};
 constexpr double kRound = 4.26;
 constexpr double kUnit[kNbn] = {3.83e-3, 3.915e-3, 4.013e-3, 4.277e-3, 4.442e-3, 4.553e-3, 4.723e-3, 5.247e-3, 6.031e-3};
 constexpr double kReduceBpus = 2.93e6;  // bytes per us of the split-K reduce
-constexpr size_t kMaxPartials = (size_t)256 << 20;  // bytes of split-K partial sums
+constexpr size_t kMaxPartials = (size_t)1 << 30;  // bytes of split-K partial sums
+// KC > 1 plans run 1.12-1.27x their modelled time where the KS plans run 1.03-1.14x
+// (q4_K and q5_K at M in {1024, 2048, 4096} x (N, K) in {5120 x 14336, 5120 x 8192,
+// 14336 x 8192}): their kernel keeps a shallower x ring, does not pipeline B and
+// flushes Y once per chunk.
+constexpr double kChunkCost = 1.12;
 
 // KS > 1: the K steps split KS ways, partial sums added by a second kernel; KC > 1:
 // each workgroup sums KC consecutive K ranges in turn, adding each range's sum into its
@@ -776,6 +781,7 @@ QPlan q_plan(int qt, const int* rows, int n, int N, int K, int cus, bool split) 
         if (!plan_ok(qt, kBns[i], ks, kc, K, rows_total, N, split)) continue;
         const long wg = q_tiles(rows, n, N, kBns[i]) * ks;
         double t = (double)((wg + cus - 1) / cus) * (kRound + kUnit[i] * kBns[i] * nk / ks);
+        if (kc > 1) t *= kChunkCost;
         if (ks > 1) t += (double)rows_total * N * 4 * (ks + 1) / kReduceBpus;  // the reduce
         if (best_t < 0 || t < best_t) {
           best_t = t;
