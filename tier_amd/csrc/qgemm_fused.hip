@@ -50,6 +50,7 @@
 // cycles per K step, 70 % of the producer's time, with the consumers waiting
 // on it for 26 % of theirs; with the register-fed pair decoder the consumers
 // wait 9 % and the MFMA issue is the larger part of their K step.
+#include <climits>
 #include <cstdio>
 #include <cstdlib>
 
@@ -512,6 +513,13 @@ __global__ __launch_bounds__(512) void qgemm_fused_x3ref(const QArgs p) {
 
   // -------------------------------------------------------------- consumer
   const int c = wave;
+  if (m0 + c * 32 >= M) {
+    // Every row of this consumer is past the group's (the last tile of a group that is
+    // not a multiple of 128 rows): it stores nothing, so it skips the K loop, and its
+    // done flags never hold a producer back.
+    if (lane < FL) __hip_atomic_store(&done[4 * lane + c], INT_MAX, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    return;
+  }
   const int fr = lane & 15, fc = lane >> 4;
   const uint32_t fo = swz(fr, fc);
   // A fragment (part, i): row c*32 + 16i + fr of the tile, halfs 8fc.. of stage q
