@@ -247,7 +247,9 @@ def bench_chat_stream(tier_amd, hip, stream, layers=4):
 def bench_moe(tier_amd, hip, stream):
     """Config 5: 64 experts, top-8 of softmax(router logits ~N(0,1)), hidden 2048, expert ffn
     1408; 4096 tokens sorted by expert; gate/up q4_K, down q5_0 (K = 1408 is not a whole
-    number of 256-element super-blocks); grouped GEMMs + per-token weighted combine."""
+    number of 256-element super-blocks); grouped GEMMs + per-token weighted combine.  Each
+    expert's gate and up rows are stored stacked (one 2816-row weight, as MoE engines keep
+    w1/w3), so one grouped GEMM gives both from one split of the routed rows."""
     T, E, topk, H, F = 4096, 64, 8, 2048, 1408
     rng = np.random.default_rng(18)
     logits = rng.standard_normal((T, E))
@@ -263,20 +265,22 @@ def bench_moe(tier_amd, hip, stream):
     P = T * topk
     # 8 distinct quantized experts per matrix, copied to 64 device buffers
     log("bench: moe weights")
-    ws_ = {}
+    base = {}
     for name, qt, N, K in (("gate", tier_amd.Q4_K, F, H), ("up", tier_amd.Q4_K, F, H), ("down", tier_amd.Q5_0, H, F)):
-        base = [_quantized(tier_amd, qt, N, K, 19 + 31 * j + len(ws_)) for j in range(8)]
-        ws_[name] = (qt, N, K, [hip.to_device(base[e % 8]) for e in range(E)])
+        base[name] = [_quantized(tier_amd, qt, N, K, 19 + 31 * j + len(base)) for j in range(8)]
+    gu = [np.concatenate([base["gate"][j], base["up"][j]]) for j in range(8)]
+    ws_ = {"gate_up": (tier_amd.Q4_K, 2 * F, H, [hip.to_device(gu[e % 8]) for e in range(E)]),
+           "down": (tier_amd.Q5_0, H, F, [hip.to_device(base["down"][e % 8]) for e in range(E)])}
     Xs = hip.to_device(rng.standard_normal((P, H), dtype=np.float32))
     A = hip.to_device(rng.standard_normal((P, F), dtype=np.float32))
-    G, U, D = hip.DeviceBuffer(P * F * 4), hip.DeviceBuffer(P * F * 4), hip.DeviceBuffer(P * H * 4)
+    GU, D = hip.DeviceBuffer(P * 2 * F * 4), hip.DeviceBuffer(P * H * 4)
     TP, PW, OUT = hip.to_device(inv.reshape(T, topk).astype(np.int32)), hip.to_device(pair_w[order]), \
         hip.DeviceBuffer(T * H * 4)
     wsb = max(tier_amd.qgemm_grouped_ws_bytes([q] * E, offsets, N, K) for q, N, K, _ in ws_.values())
     WS = hip.DeviceBuffer(wsb)
 
     def step(_i):
-        for name, dst, src in (("gate", G, Xs), ("up", U, Xs), ("down", D, A)):
+        for name, dst, src in (("gate_up", GU, Xs), ("down", D, A)):
             qt, N, K, bufs = ws_[name]
             tier_amd.qgemm_grouped([b.ptr for b in bufs], [qt] * E, [tier_amd.q_row_bytes(qt, K)] * E, src.ptr,
                                    offsets, dst.ptr, N, K, tier_amd.MODE_X3REF, WS.ptr, wsb, stream)
@@ -288,7 +292,8 @@ def bench_moe(tier_amd, hip, stream):
     tf = flop / (km * 1e-3) / 1e12
     return {"experts": E, "topk": topk, "tokens": T, "us": round(km * 1e3, 1), "TFLOPS": round(tf, 1),
             "frac_x3_peak": round(tf / X3_PEAK_TFLOPS, 4), "types": "gate/up q4_K, down q5_0",
-            "includes": "3 grouped GEMMs (64 experts each) + combine; no activation between"}
+            "includes": "gate+up as one grouped GEMM of the stacked 2816-row expert weights, down, combine "
+                        "(64 experts each); no activation between"}
 
 
 def measured_traffic():

@@ -128,3 +128,33 @@ def test_grouped_big_tiles_mixed_types(gpu, with_ws, kind):
         a, b = offsets[e], offsets[e + 1]
         assert oracle.rel_fro(ys[a:b], ref[a:b]) <= BAR, e
     assert oracle.rel_fro(ys, ref) <= BAR
+
+
+def test_grouped_stacked_gate_up_bit_identical(gpu):
+    """Each expert's gate and up rows stored stacked (one 2N-row weight, as MoE engines keep
+    w1 / w3) give, in one grouped call, exactly the two separate grouped products: every
+    output column is summed over K in the same order whatever the tile width."""
+    rng = np.random.default_rng(2816)
+    E, N, K = 16, 1408, 2048
+    counts = rng.integers(440, 590, E)
+    counts[2], counts[9] = 0, 3
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    P = int(offsets[-1])
+    t = tier_amd.Q4_K
+    gate = [oracle.random_blocks(rng, t, N * (K // 256)).reshape(N, -1) for _ in range(E)]
+    up = [oracle.random_blocks(rng, t, N * (K // 256)).reshape(N, -1) for _ in range(E)]
+    xs = activations(P, K, seed=72)
+    X = hip.to_device(xs)
+    rb = tier_amd.q_row_bytes(t, K)
+    outs = {}
+    for name, ws_, n in (("gate", gate, N), ("up", up, N), ("gu", [np.concatenate([g, u]) for g, u in zip(gate, up)], 2 * N)):
+        dW = [hip.to_device(b) for b in ws_]
+        Y = hip.DeviceBuffer(P * n * 4)
+        tier_amd.qgemm_grouped([w.ptr for w in dW], [t] * E, [rb] * E, X.ptr, offsets.tolist(), Y.ptr, n, K)
+        hip.synchronize()
+        outs[name] = Y.download(np.float32, P * n).reshape(P, n)
+    assert np.array_equal(outs["gu"][:, :N].view(np.uint32), outs["gate"].view(np.uint32))
+    assert np.array_equal(outs["gu"][:, N:].view(np.uint32), outs["up"].view(np.uint32))
+    a, b = offsets[9], offsets[10]
+    w16 = oracle.h2f(oracle.dequant(gate[9], t, K, oracle.OUT_F16)).reshape(N, K).astype(np.float64)
+    assert oracle.rel_fro(outs["gate"][a:b], xs[a:b].astype(np.float64) @ w16.T) <= BAR
