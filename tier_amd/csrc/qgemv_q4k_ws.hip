@@ -25,9 +25,12 @@
 // registers from the start (MS columns) and its LDS reads are the weight bytes
 // alone.  8 consumers with 4 producers (3 waves per SIMD) measured faster than
 // 4-12 consumers in other counts (13824x5120, whole-tile stages: 8.54 against
-// 8.63-9.11 us).  Its partial sum of each tile stays in a register until the
-// last stage is consumed; then the ring holds the partials and the workgroup
-// adds the NC partials of each row in a fixed order.
+// 8.63-9.11 us).  With 3 or 4 tiles per workgroup its partial sum of each tile
+// goes to an LDS area of its own as the tile ends, and after one barrier the
+// workgroup adds the NC partials of each row in a fixed order (13824x5120 8.51
+// against 8.57-8.64 us, 16384x8192 13.74-13.81 against 13.85-13.93); otherwise
+// the sums stay in registers until every stage is consumed and then go to the
+// ring, behind a second barrier.
 //
 // Hand-off through LDS flags holding stage numbers, which only grow:
 //   full[slot][p] = q  -- producer p's rows of stage q have landed (its own
@@ -110,7 +113,11 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
   __shared__ int nf[NC];               // per consumer: x held a non-finite value
   int* full = (int*)(ring + L::RING);  // [NS][NP]
   int* done = full + NS * NP;          // [NS][NCP]
-  float* red = (float*)ring;           // [R][NC][16], after the last stage
+  // [R][NC][16]: for 3 or 4 tiles an area of their own, written as each tile ends;
+  // otherwise the ring, once every stage has been consumed
+  constexpr bool OWN = R == 3 || R == 4;
+  __shared__ float red_own[OWN ? R * NC * 16 : 1];
+  float* red = OWN ? red_own : (float*)ring;
   const int nsb = K >> 8, ngrp = (nsb + GS - 1) / GS, total = R * ngrp;
   const int tiles = (N + 15) >> 4;
   uint8_t* xq = xlds;
@@ -161,8 +168,8 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
     vm_wait<0>();
     for (; marked < total; ++marked)
       if (lane == 0) lds_rel(&full[NP * (marked % NS) + p], marked);
-    __syncthreads();  // every stage consumed: the ring is free
-    __syncthreads();  // partial sums are in red[]
+    if constexpr (!OWN) __syncthreads();  // every stage consumed: the ring is free
+    __syncthreads();                         // partial sums are in red[]
   } else {
     // -------------------------------------------------------------- consumers
     const int c = wave, n = lane & 15, g = lane >> 4;
@@ -212,7 +219,7 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
     }
     // row n of a stage: producer n / 4's slot, row n % 4 of it; column c
     const uint8_t* rowbase = ring + (n / PROWS) * NS * SLOT + (n % PROWS) * GRP + c * SBB;
-    float part[R];  // this consumer's sum of row n of each tile (lanes g == 0)
+    float part[OWN ? 1 : R];  // (!OWN) this consumer's sum of row n of each tile (lanes g == 0)
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       float acc = 0.f;
@@ -233,13 +240,19 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
       }
       acc += __shfl_xor(acc, 16, 64);
       acc += __shfl_xor(acc, 32, 64);
-      part[r] = acc;
+      if constexpr (OWN) {
+        if (g == 0) red[(r * NC + c) * 16 + n] = acc;
+      } else {
+        part[r] = acc;
+      }
     }
-    __syncthreads();  // every stage consumed: the ring is free
-    if (g == 0)
+    if constexpr (!OWN) {
+      __syncthreads();  // every stage consumed: the ring is free
+      if (g == 0)
 #pragma unroll
-      for (int r = 0; r < R; ++r) red[(r * NC + c) * 16 + n] = part[r];
-    __syncthreads();
+        for (int r = 0; r < R; ++r) red[(r * NC + c) * 16 + n] = part[r];
+    }
+    __syncthreads();  // partial sums are in red[]
   }
   if (flags_any(nf, NC)) {  // NaN or +-Inf in x: the rows take gemv_q's non-finite sums
     for (int i = wave; i < R * 16; i += NC + NP) {
@@ -268,7 +281,8 @@ template <int QT, int R, int GS, int NC, int NS, int D, int XP, int XK>
 int launch_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
   const unsigned grid = (unsigned)((N + 15) / 16 + R - 1) / R;
   using L = WsLayout<QT, GS, NC, NS, R>;
-  static_assert(xq_bytes(XK) + 4 * NC + L::LDS <= 160 * 1024, "LDS budget (x digits, flags, ring)");
+  static_assert(xq_bytes(XK) + 4 * NC + (R == 3 || R == 4 ? R * NC * 64 : 0) + L::LDS <= 160 * 1024,
+                "LDS budget (x digits, flags, partial sums, ring)");
   static_assert(XK / 16 <= 64 * NC * XP, "x preparation: one thread per 16 elements");
   static std::atomic<uint64_t> attr{0};
   int st = lds_attr_once(attr, (const void*)qgemv_q4k_ws<QT, R, GS, NC, NS, D, XP, XK>, (int)L::LDS,
