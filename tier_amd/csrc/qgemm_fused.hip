@@ -555,6 +555,27 @@ __global__ __launch_bounds__(512) void qgemm_fused_x3ref(const QArgs p) {
   // accumulation chunks (kcs) it runs at the end of each chunk, which adds the
   // chunk's sum into Y (beta = 1 after the first) and starts the next from zero.
   auto store = [&](float beta) __attribute__((always_inline)) {
+    // A consumer whose 32 rows and the tile's BN columns all exist (every tile but the
+    // last of a row or column of tiles) stores without per-element tests: one row
+    // pointer per register row, the 16-column blocks at immediate offsets from it.
+    if (m0 + c * 32 + 32 <= M && n0 + BN <= p.N) {
+      const int rb0 = m0 + c * 32 + 4 * (lane >> 4), cb = n0 + (lane & 15);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const size_t row = (size_t)(rb0 + i * 16 + r);
+          float* rp = KS == 1 ? Yg + row * p.ldy + cb : p.P + (size_t)kz * p.ps + row * p.N + cb;
+          if (KS == 1 && beta != 0.f) {
+#pragma unroll
+            for (int j = 0; j < NB; ++j) rp[16 * j] = fmaf(beta, rp[16 * j], acc[i][j][r]);
+          } else {
+#pragma unroll
+            for (int j = 0; j < NB; ++j) rp[16 * j] = acc[i][j][r];
+          }
+        }
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       const int col = n0 + j * 16 + (lane & 15);
