@@ -678,6 +678,26 @@ __global__ __launch_bounds__(256) void qgemm_splitk_reduce(const float* __restri
   if (beta != 0.f) v = fmaf(beta, *y, v);
   *y = v;
 }
+// The same, four columns a thread and one row per blockIdx.y (N and ldy multiples of
+// 4, P and Y 16-byte aligned): 16-byte loads and stores, no index division.  Each
+// element is summed in the same split order.
+__global__ __launch_bounds__(256) void qgemm_splitk_reduce4(const float* __restrict__ P, size_t ps, int ks,
+                                                           float* __restrict__ Y, int ldy, int N, float beta) {
+  const int c4 = blockIdx.x * 256 + threadIdx.x;
+  if (4 * c4 >= N) return;
+  const size_t i = (size_t)blockIdx.y * N + 4 * c4;
+  float4 v = *(const float4*)(P + i);
+  for (int z = 1; z < ks; ++z) {
+    const float4 t = *(const float4*)(P + z * ps + i);
+    v.x += t.x; v.y += t.y; v.z += t.z; v.w += t.w;
+  }
+  float4* y = (float4*)(Y + (size_t)blockIdx.y * ldy + 4 * c4);
+  if (beta != 0.f) {
+    const float4 o = *y;
+    v.x = fmaf(beta, o.x, v.x); v.y = fmaf(beta, o.y, v.y); v.z = fmaf(beta, o.z, v.z); v.w = fmaf(beta, o.w, v.w);
+  }
+  *y = v;
+}
 
 template <int QT, int BN, int KS, bool CH = false>
 int launch_q(const QArgs& a, hipStream_t s, const char* who) {
@@ -878,10 +898,16 @@ int qgemm_fused_groups(const void* const* W, int qtype, const int* row0, const i
     }
     if (st) return st;
     if (pl.ks > 1) {  // n == 1, kc == 1: rows row0[0].. of Y
-      const size_t cnt = (size_t)rows[0] * N;
-      qgemm_splitk_reduce<<<(unsigned)((cnt + 255) / 256), 256, 0, s>>>(partials, a.ps, pl.ks,
-                                                                       Y + (size_t)row0[0] * ldy, ldy, rows[0], N,
-                                                                       beta);
+      float* y0 = Y + (size_t)row0[0] * ldy;
+      if (N % 4 == 0 && ldy % 4 == 0 && rows[0] <= 65535 && ((uintptr_t)y0 & 15) == 0 &&
+          ((uintptr_t)partials & 15) == 0 && a.ps % 4 == 0) {
+        const dim3 grid((unsigned)((N / 4 + 255) / 256), (unsigned)rows[0]);
+        qgemm_splitk_reduce4<<<grid, 256, 0, s>>>(partials, a.ps, pl.ks, y0, ldy, N, beta);
+      } else {
+        const size_t cnt = (size_t)rows[0] * N;
+        qgemm_splitk_reduce<<<(unsigned)((cnt + 255) / 256), 256, 0, s>>>(partials, a.ps, pl.ks, y0, ldy, rows[0], N,
+                                                                         beta);
+      }
       TM_LAUNCH_CHECK(who);
     }
   }
