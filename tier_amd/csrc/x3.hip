@@ -353,6 +353,79 @@ struct X3Args {
   float beta;
 };
 
+// Stores a wave's WM x WN blocks of 32x32 accumulators at rows r0 + 32i.., columns
+// c0 + 32j.. (register r of lane l holds row 8*(r/4) + 4*(l/32) + r%4, column l%32 of
+// its block): C = acc * 2^-(aexp[row] + bexp[col]) (+ beta * C).  The exponents and
+// beta are read once, before any store.  A wave whose rows and columns all exist
+// stores without per-element tests: one row pointer per register row, the column
+// blocks at immediate offsets from it.
+template <int WM, int WN>
+__device__ __forceinline__ void x3_store(const X3Args& p, const float16v (&acc)[WM][WN], int r0, int c0, int lane) {
+  const int M = p.M, N = p.N, ldc = p.ldc;
+  const float beta = p.beta;
+  const int32_t* aexp = p.aexp;
+  const int32_t* bexp = p.bexp;
+  float* C = p.C;
+  const int lr = 4 * (lane >> 5), lc = lane & 31;
+  const bool sc = aexp || bexp;
+  int eb[WN], ea[WM][16];
+#pragma unroll
+  for (int j = 0; j < WN; ++j) {
+    const int col = c0 + 32 * j + lc;
+    eb[j] = bexp && col < N ? bexp[col] : 0;
+  }
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = r0 + 32 * i + 8 * (r >> 2) + lr + (r & 3);
+      ea[i][r] = aexp && row < M ? aexp[row] : 0;
+    }
+  if (r0 + 32 * WM <= M && c0 + 32 * WN <= N) {
+    if (!sc && beta == 0.f) {
+#pragma unroll
+      for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float* rp = C + (size_t)(r0 + 32 * i + 8 * (r >> 2) + lr + (r & 3)) * ldc + c0 + lc;
+#pragma unroll
+          for (int j = 0; j < WN; ++j) rp[32 * j] = acc[i][j][r];
+        }
+    } else {
+#pragma unroll
+      for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float* rp = C + (size_t)(r0 + 32 * i + 8 * (r >> 2) + lr + (r & 3)) * ldc + c0 + lc;
+#pragma unroll
+          for (int j = 0; j < WN; ++j) {
+            float v = acc[i][j][r];
+            if (sc) v = ldexpf(v, -(ea[i][r] + eb[j]));
+            if (beta != 0.f) v = fmaf(beta, rp[32 * j], v);
+            rp[32 * j] = v;
+          }
+        }
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = r0 + 32 * i + 8 * (r >> 2) + lr + (r & 3);
+      if (row >= M) continue;
+      float* rp = C + (size_t)row * ldc + c0 + lc;
+#pragma unroll
+      for (int j = 0; j < WN; ++j) {
+        if (c0 + 32 * j + lc >= N) continue;
+        float v = acc[i][j][r];
+        if (sc) v = ldexpf(v, -(ea[i][r] + eb[j]));
+        if (beta != 0.f) v = fmaf(beta, rp[32 * j], v);
+        rp[32 * j] = v;
+      }
+    }
+}
+
 template <int BM, int BN, int MODE>
 __global__ __launch_bounds__(256) void gemm_x3_kernel(const X3Args p) {
   using Md = X3Mode<MODE>;
@@ -458,26 +531,7 @@ __global__ __launch_bounds__(256) void gemm_x3_kernel(const X3Args p) {
     __syncthreads();
   }
 
-  // epilogue: 32x32 accumulator layout -- register r of lane l holds
-  // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
-#pragma unroll
-  for (int i = 0; i < WM; ++i)
-#pragma unroll
-    for (int j = 0; j < WN; ++j) {
-      const int col = n0 + wn * WN * 32 + j * 32 + (lane & 31);
-      if (col >= p.N) continue;
-      const int eb = p.bexp ? p.bexp[col] : 0;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * WM * 32 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (row >= p.M) continue;
-        float v = acc[i][j][r];
-        if (p.aexp || p.bexp) v = ldexpf(v, -((p.aexp ? p.aexp[row] : 0) + eb));
-        float* c = p.C + (size_t)row * p.ldc + col;
-        if (p.beta != 0.f) v = fmaf(p.beta, *c, v);
-        *c = v;
-      }
-    }
+  x3_store<WM, WN>(p, acc, m0 + wm * WM * 32, n0 + wn * WN * 32, lane);
 #undef X3_GLOAD
 #undef X3_SSTORE
 }
@@ -635,26 +689,7 @@ __device__ __forceinline__ void x3_big_tile(const X3Args& p, int t) {
     }
   }
   if (!live) return;
-
-  // epilogue: register r of lane l holds row 8*(r/4) + 4*(l/32) + r%4, column l%32
-#pragma unroll
-  for (int i = 0; i < WM; ++i)
-#pragma unroll
-    for (int j = 0; j < WN; ++j) {
-      const int col = n0 + wn * WN * 32 + j * 32 + (lane & 31);
-      if (col >= p.N) continue;
-      const int eb = p.bexp ? p.bexp[col] : 0;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * WM * 32 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (row >= p.M) continue;
-        float v = acc[i][j][r];
-        if (p.aexp || p.bexp) v = ldexpf(v, -((p.aexp ? p.aexp[row] : 0) + eb));
-        float* c = p.C + (size_t)row * p.ldc + col;
-        if (p.beta != 0.f) v = fmaf(p.beta, *c, v);
-        *c = v;
-      }
-    }
+  x3_store<WM, WN>(p, acc, m0 + wm * WM * 32, n0 + wn * WN * 32, lane);
 }
 
 template <int MODE, int TN>
