@@ -158,3 +158,22 @@ def test_grouped_stacked_gate_up_bit_identical(gpu):
     a, b = offsets[9], offsets[10]
     w16 = oracle.h2f(oracle.dequant(gate[9], t, K, oracle.OUT_F16)).reshape(N, K).astype(np.float64)
     assert oracle.rel_fro(outs["gate"][a:b], xs[a:b].astype(np.float64) @ w16.T) <= BAR
+
+
+@pytest.mark.parametrize("N,topk", [(2048, 8), (8, 1), (6, 8), (1024, 17), (4, 16)])
+def test_moe_combine_shapes(gpu, N, topk):
+    """The combine on both of its kernels (four columns a thread when N % 4 == 0 and
+    topk <= 16, one column otherwise): each token's weighted sum of its top-k rows
+    against fp64."""
+    rng = np.random.default_rng(N * 31 + topk)
+    T = 37
+    P = T * topk
+    ys = rng.standard_normal((P, N)).astype(np.float32)
+    tp = rng.permutation(P).astype(np.int32).reshape(T, topk)
+    pw = rng.random(P).astype(np.float32)
+    Y, TP, PW, OUT = hip.to_device(ys), hip.to_device(tp), hip.to_device(pw), hip.DeviceBuffer(T * N * 4)
+    tier_amd.moe_combine(Y.ptr, TP.ptr, PW.ptr, OUT.ptr, T, topk, N)
+    hip.synchronize()
+    out = OUT.download(np.float32, T * N).reshape(T, N)
+    ref = np.einsum("tj,tjn->tn", pw[tp].astype(np.float64), ys[tp].astype(np.float64))
+    assert oracle.rel_fro(out, ref) <= BAR

@@ -305,6 +305,35 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
     out[(size_t)t * N + n] = acc;
   }
 }
+// The same, four columns a thread (N a multiple of 4, Y and out 16-byte aligned, topk
+// at most 16): the token's pairs and weights are read once, then 16-byte loads of
+// each pair's row; each column is summed in the same j order.
+__global__ __launch_bounds__(256) void moe_combine4_kernel(const float* __restrict__ Y, const int* __restrict__ tp,
+                                                           const float* __restrict__ pw, float* __restrict__ out,
+                                                           int topk, int N) {
+  const int t = blockIdx.x;
+  int pj[16];
+  float wj[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j)
+    if (j < topk) {
+      pj[j] = tp[(size_t)t * topk + j];
+      wj[j] = pw[pj[j]];
+    }
+  for (int n = 4 * threadIdx.x; n < N; n += 1024) {
+    float4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if (j < topk) {
+        const float4 y = *(const float4*)(Y + (size_t)pj[j] * N + n);
+        acc.x = fmaf(wj[j], y.x, acc.x);
+        acc.y = fmaf(wj[j], y.y, acc.y);
+        acc.z = fmaf(wj[j], y.z, acc.z);
+        acc.w = fmaf(wj[j], y.w, acc.w);
+      }
+    *(float4*)(out + (size_t)t * N + n) = acc;
+  }
+}
 
 // ------------------------------------------------------------- GEMM core
 constexpr int BK = 32;            // K per LDS stage (two 32x32x16 MFMA steps)
@@ -1479,7 +1508,10 @@ int tiermm_moe_combine(const float* Y_sorted, const int* token_pairs, const floa
   if (T < 0 || topk < 0 || N < 0) return set_error(TIERMM_EINVAL, "tiermm_moe_combine: negative size");
   if (T == 0 || N == 0) return TIERMM_OK;
   if (!Y_sorted || !token_pairs || !pair_weight || !out) return set_error(TIERMM_EINVAL, "tiermm_moe_combine: null buffer");
-  moe_combine_kernel<<<T, 256, 0, (hipStream_t)stream>>>(Y_sorted, token_pairs, pair_weight, out, topk, N);
+  if (N % 4 == 0 && topk <= 16 && ((uintptr_t)Y_sorted & 15) == 0 && ((uintptr_t)out & 15) == 0)
+    moe_combine4_kernel<<<T, 256, 0, (hipStream_t)stream>>>(Y_sorted, token_pairs, pair_weight, out, topk, N);
+  else
+    moe_combine_kernel<<<T, 256, 0, (hipStream_t)stream>>>(Y_sorted, token_pairs, pair_weight, out, topk, N);
   TM_LAUNCH_CHECK("tiermm_moe_combine: launch");
   return TIERMM_OK;
 }
