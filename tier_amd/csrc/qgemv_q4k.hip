@@ -141,11 +141,19 @@ __global__ __launch_bounds__(64 * RT * KS) void qgemv_q4k_mfma(const uint8_t* __
   };
 
   for (int grp = 0; grp < ngrp; ++grp) {
-    // keep STAGES-1 groups in flight: issue group grp+STAGES-1 (a clamped re-read
-    // past the end keeps the count of outstanding loads fixed), then wait for grp
-    load_group<GS, F::SBB>(base0, rb, roff, coff, lane, grp + STAGES - 1, nsb,
-                   ring_lds + ((grp + STAGES - 1) % STAGES) * SBYTES);
-    vm_wait<NLD * (STAGES - 1)>();  // group grp has landed in its stage
+    // keep STAGES-1 groups in flight: issue group grp+STAGES-1, then wait for grp.
+    // Past the last group nothing is issued, and the wait leaves in flight only the
+    // groups after grp (no re-reads whose latency the wave would wait out at its end).
+    if (grp + STAGES - 1 < ngrp) {
+      load_group<GS, F::SBB>(base0, rb, roff, coff, lane, grp + STAGES - 1, nsb,
+                             ring_lds + ((grp + STAGES - 1) % STAGES) * SBYTES);
+      vm_wait<NLD * (STAGES - 1)>();  // group grp has landed in its stage
+    } else {
+      const int left = ngrp - 1 - grp;  // groups issued after grp, at most STAGES - 2
+      if (STAGES > 2 && left == 1) vm_wait<(STAGES > 2 ? NLD : 0)>();
+      else if (STAGES > 3 && left == 2) vm_wait<(STAGES > 3 ? 2 * NLD : 0)>();
+      else vm_wait<0>();
+    }
     const uint8_t* st = myring + (grp % STAGES) * SBYTES;
     if (GS * grp + GS <= nsb) {
 #pragma unroll
@@ -156,7 +164,7 @@ __global__ __launch_bounds__(64 * RT * KS) void qgemv_q4k_mfma(const uint8_t* __
         if (GS * grp + i < nsb) superblock(st, i, GS * grp + i);
     }
   }
-  vm_wait<0>();  // drain the clamped tail loads before the wave ends
+  vm_wait<0>();  // every load has landed (the prologue's re-reads of short K parts too)
 
   if (xbad) {  // NaN or +-Inf in x: the workgroup's rows take gemv_q's non-finite sums
     for (int r = wave; r < RT * 16; r += RT * KS) {
