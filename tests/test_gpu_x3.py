@@ -334,11 +334,12 @@ def test_qgemm_q4k_fused_x_layouts(gpu, M, N, K):
 
 @pytest.mark.parametrize("bn,ks", [(256, 1), (256, 4), (224, 2), (192, 1), (160, 1), (160, 2), (160, 4), (128, 2),
                                    (112, 4), (96, 2), (80, 4), (64, 2), (64, 1)])
-@pytest.mark.parametrize("M,N,K,beta", [(300, 1000, 1024, 1.0), (512, 352, 2048, 0.0)])
+@pytest.mark.parametrize("M,N,K,beta", [(300, 1000, 1024, 1.0), (512, 352, 2048, 0.0), (130, 998, 1024, 1.0)])
 def test_qgemm_q4k_tile_plans(gpu, monkeypatch, bn, ks, M, N, K, beta):
     """Every tile width and split-K factor of the fused q4_K kernel, forced through
-    TIERMM_QGEMM_TILE: partial M and N tiles, the split-K reduce with beta = 1, and the
-    workspace query sized for the partial sums."""
+    TIERMM_QGEMM_TILE: partial M and N tiles, the split-K reduce with beta = 1 (four
+    columns a thread, and one at N = 998), and the workspace query sized for the partial
+    sums."""
     monkeypatch.setenv("TIERMM_QGEMM_TILE", f"{bn},{ks}")
     t = tier_amd.Q4_K
     assert tier_amd.qgemm_ws_bytes(t, M, N, K) == 3 * M * K * 2 + (ks * M * N * 4 if ks > 1 else 0)
