@@ -42,7 +42,12 @@ __device__ __forceinline__ bool flags_any(const int* flags, int n) {
 
 // Prepare x elements [16h, 16h+16) of sub-block s (h = half, values in v): the
 // partner thread (lane ^ 1) holds the other half; both reach this together.
-__device__ __forceinline__ void prep_half(int s, int h, const float (&v)[16], uint8_t* xq, float* meta) {
+// With DSUM, also dsum[32 sb + 8 a + 2 t + {0, 1}] = 32 (256 T3 + T2) and
+// 32 (256 T1 + T0), T_l = the sum of digit l over these 16 elements: what
+// (q + 32) in place of q adds to the two int32 halves of a digit dot.
+template <bool DSUM = false>
+__device__ __forceinline__ void prep_half(int s, int h, const float (&v)[16], uint8_t* xq, float* meta,
+                                          int* dsum = nullptr) {
   float amax = 0.f, sum = 0.f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
@@ -85,6 +90,16 @@ __device__ __forceinline__ void prep_half(int s, int h, const float (&v)[16], ui
   uint8_t* dst = xq + sb * XQ_SB + t * XQ_T + a * 64;
 #pragma unroll
   for (int l = 0; l < 4; ++l) *(u32x4*)(dst + 16 * l) = L[l];
+  if constexpr (DSUM) {
+    int T[4];
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+      T[l] = 0;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) T[l] = __builtin_amdgcn_sdot4((int)L[l][w], 0x01010101, T[l], false);
+    }
+    *(int2*)(dsum + sb * 32 + a * 8 + t * 2) = make_int2(32 * (256 * T[3] + T[2]), 32 * (256 * T[1] + T[0]));
+  }
 }
 
 // Async loads of group `grp` (GS super-blocks of the wave's 16 rows) into an
