@@ -10,7 +10,12 @@
 // into stages of GS super-blocks: each of the 4 producer waves (one per SIMD)
 // brings 4 of the 16 rows (4 row segments of GS*144 bytes) into a ring of NS
 // slots of its own with global_load_lds_dwordx4; while it waits for stage q - D
-// to land, stages q - D .. q are in flight.  Long row segments and few
+// to land, stages q - D .. q are in flight.  16-byte pads after the row segments
+// and after each producer's slots (ws_pad) put the 16 rows a consumer reads at one
+// column on distinct groups of LDS banks: without them up to four rows met in one
+// group.  That halved the bank-conflict cycles (13824x5120: 0.47 -> 0.25 M;
+// 16384x8192: 1.94 -> 0.59 M) without moving the time: the consumers of this
+// kernel are not LDS-bound.  Long row segments and few
 // concurrent tiles measured faster than 16 short segments per wave from 864
 // tiles at once (13824x5120: 8.9 against 9.2 us; 10240x8192: 10.4 against
 // 11.8 us).  Up to K = 5120 a stage is the whole tile (a contiguous 16-row
@@ -80,16 +85,56 @@ __device__ __forceinline__ void poll_ge(const int* f, int v) {
   asm volatile("" ::: "memory");
 }
 
+// LDS bank conflicts of the consumers' 16-byte reads (8 lanes a pass over 32
+// banks: rows 0-7, then 8-15, at one column) for row segments `pitch` bytes apart
+// in a slot and producer regions `region` bytes apart: the sum over both passes
+// of the most rows that meet in one group of four banks (2 = none).
+constexpr int ws_conflicts(int pitch, int region) {
+  int cost = 0;
+  for (int pass = 0; pass < 2; ++pass) {
+    int cnt[8] = {0, 0, 0, 0, 0, 0, 0, 0}, worst = 0;
+    for (int n = 8 * pass; n < 8 * pass + 8; ++n) {
+      const long dw = ((long)(n / PROWS) * region + (long)(n % PROWS) * pitch) / 4;
+      const int grp = (int)(dw % 32) / 4;
+      worst = ++cnt[grp] > worst ? cnt[grp] : worst;
+    }
+    cost += worst;
+  }
+  return cost;
+}
+// Padding of a ring: 16-byte pads after each row segment (k) and after each
+// producer's region of ns slots (m), the fewest (k + m, up to 7 each) that spread
+// the 16 rows over the banks (13824x5120: one pad per row, 2896-byte rows).
+struct WsPad {
+  int k, m;
+};
+constexpr WsPad ws_pad(int grp, int ns) {
+  WsPad best{0, 0};
+  int bc = ws_conflicts(grp, ns * PROWS * grp);
+  for (int t = 1; t < 15; ++t)
+    for (int k = 0; k <= t && k < 8; ++k) {
+      const int m = t - k, pitch = grp + 16 * k;
+      if (m < 8 && ws_conflicts(pitch, ns * PROWS * pitch + 16 * m) < bc) {
+        bc = ws_conflicts(pitch, ns * PROWS * pitch + 16 * m);
+        best = WsPad{k, m};
+      }
+    }
+  return best;
+}
+
 template <int QT, int GS_, int NC, int NS, int R>
 struct WsLayout {
   static constexpr int GS = GS_;                                // super-blocks per stage
   static constexpr int CPS = (GS + NC - 1) / NC;                // columns per consumer per stage
   static constexpr int GRP = GS * MfmaFmt<QT>::SBB;             // one row's segment
-  static constexpr int SLOT = PROWS * GRP;                      // one producer's part of a stage
+  static constexpr WsPad PAD = ws_pad(GRP, NS);
+  static constexpr int PITCH = GRP + 16 * PAD.k;                // its place in a slot (with the pad)
+  static constexpr int SLOT = PROWS * PITCH;                    // one producer's part of a stage
+  static constexpr int REGION = NS * SLOT + 16 * PAD.m;         // one producer's slots (with the pad)
   static constexpr int NLD = (SLOT + 1023) / 1024;              // 1 KiB loads per part
   static constexpr int LAST = (SLOT - (NLD - 1) * 1024) / 16;   // lanes of the last load
   static constexpr int NCP = pad4(NC);
-  static constexpr size_t RING = (size_t)NP * NS * SLOT;
+  static constexpr size_t RING = (size_t)NP * REGION;
   static constexpr size_t LDS = RING + NS * NP * 4 + NS * NCP * 4;
   // the per-tile partial sums reuse the ring once every stage has been consumed
   static_assert((size_t)R * NC * 16 * 4 <= RING, "partial sums fit in the ring");
@@ -101,7 +146,8 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
                                                             int N, int K) {
   using L = WsLayout<QT, GS_, NC, NS, R>;
   constexpr int SBB = MfmaFmt<QT>::SBB;
-  constexpr int GS = L::GS, CPS = L::CPS, GRP = L::GRP, SLOT = L::SLOT, NLD = L::NLD, NCP = L::NCP;
+  constexpr int GS = L::GS, CPS = L::CPS, GRP = L::GRP, PITCH = L::PITCH, SLOT = L::SLOT, NLD = L::NLD,
+                NCP = L::NCP;
   constexpr int MG = (XK / 256 + GS - 1) / GS;  // stages per tile, at most
   constexpr int MS = MG * CPS;                  // super-block columns per consumer
   static_assert(NLD * D <= 63, "vmcnt counts at most 63 loads");
@@ -109,7 +155,7 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
   static_assert(NC + NP <= 16, "at most 1024 threads per workgroup");
   static_assert(SLOT % 16 == 0, "16-byte aligned slots");
   extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // L::LDS bytes
-  __shared__ __attribute__((aligned(16))) uint8_t xlds[xq_bytes(XK)];
+  __shared__ __attribute__((aligned(16))) uint8_t xlds[xq_bytes(XK) - ZERO_BYTES];  // no zero rows: A is set once
   __shared__ int nf[NC];               // per consumer: x held a non-finite value
   int* full = (int*)(ring + L::RING);  // [NS][NP]
   int* done = full + NS * NP;          // [NS][NCP]
@@ -122,7 +168,6 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
   const int tiles = (N + 15) >> 4;
   uint8_t* xq = xlds;
   float* meta = (float*)(xq + nsb * XQ_SB);
-  uint8_t* zero = xq + nsb * (XQ_SB + META_SB);
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
   if (wave >= NC) {
@@ -131,15 +176,16 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
     if (lane < NS) full[NP * lane + p] = -1;
     if (p == 0)  // consumer flags; padding entries never hold a wait back
       for (int i = lane; i < NS * NCP; i += 64) done[i] = (i % NCP) < NC ? -1 : INT_MAX;
-    // byte f of a slot: row f / GRP of the producer's 4, byte f % GRP of its segment
+    // byte f of a slot: row f / PITCH of the producer's 4, byte f % PITCH of its
+    // segment (the pad past GRP takes a re-read of the segment's last 16 bytes)
     int roff[NLD], coff[NLD];
 #pragma unroll
     for (int j = 0; j < NLD; ++j) {
       const int f = min(j * 1024 + lane * 16, SLOT - 16);
-      roff[j] = f / GRP;
-      coff[j] = f % GRP;
+      roff[j] = f / PITCH;
+      coff[j] = f % PITCH;
     }
-    const uint32_t ring_lds = lds_addr(ring + p * NS * SLOT);
+    const uint32_t ring_lds = lds_addr(ring + p * L::REGION);
     auto issue = [&](int q) __attribute__((always_inline)) {
       const int r = q / ngrp, gi = q - r * ngrp;
       // a tile past the last one (its workgroup has fewer) re-reads the last tile
@@ -182,7 +228,6 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
 #pragma unroll
       for (int i = 0; i < 4; ++i) xr[j][i] = *(const u32x4*)(x + hh * 16 + 4 * i);
     }
-    for (int i = tid; i < ZERO_BYTES / 4; i += NT) ((uint32_t*)zero)[i] = 0u;
     bool bad = false;
 #pragma unroll
     for (int j = 0; j < XP; ++j) {
@@ -206,19 +251,17 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
 #pragma unroll
     for (int m = 0; m < MS; ++m) {
       const int sb = min(GS * (m / CPS) + c + NC * (m % CPS), nsb - 1);
-      uint32_t off[2];
-#pragma unroll
-      for (int pp = 0; pp < 2; ++pp)
-        off[pp] = (n >> 2) == 2 * (g >> 1) + pp ? (uint32_t)(sb * XQ_SB + g * 64 + (n & 3) * 16)
-                                                : (uint32_t)(zero - xlds);
-      A[m][0] = *(const i32x4*)(xlds + off[0]);
-      A[m][1] = *(const i32x4*)(xlds + off[1] + XQ_T);
-      A[m][2] = *(const i32x4*)(xlds + off[0] + 2 * XQ_T);
-      A[m][3] = *(const i32x4*)(xlds + off[1] + 3 * XQ_T);
+      const uint8_t* ap = xlds + sb * XQ_SB + g * 64 + (n & 3) * 16;
+      const bool live0 = (n >> 2) == 2 * (g >> 1), live1 = (n >> 2) == 2 * (g >> 1) + 1;
+      const i32x4 z4 = {0, 0, 0, 0};
+      A[m][0] = live0 ? *(const i32x4*)(ap) : z4;
+      A[m][1] = live1 ? *(const i32x4*)(ap + XQ_T) : z4;
+      A[m][2] = live0 ? *(const i32x4*)(ap + 2 * XQ_T) : z4;
+      A[m][3] = live1 ? *(const i32x4*)(ap + 3 * XQ_T) : z4;
       mt[m] = *(const float4*)(meta + sb * 16 + g * 4);
     }
     // row n of a stage: producer n / 4's slot, row n % 4 of it; column c
-    const uint8_t* rowbase = ring + (n / PROWS) * NS * SLOT + (n % PROWS) * GRP + c * SBB;
+    const uint8_t* rowbase = ring + (n / PROWS) * L::REGION + (n % PROWS) * PITCH + c * SBB;
     float part[OWN ? 1 : R];  // (!OWN) this consumer's sum of row n of each tile (lanes g == 0)
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -281,7 +324,7 @@ template <int QT, int R, int GS, int NC, int NS, int D, int XP, int XK>
 int launch_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
   const unsigned grid = (unsigned)((N + 15) / 16 + R - 1) / R;
   using L = WsLayout<QT, GS, NC, NS, R>;
-  static_assert(xq_bytes(XK) + 4 * NC + (R == 3 || R == 4 ? R * NC * 64 : 0) + L::LDS <= 160 * 1024,
+  static_assert(xq_bytes(XK) - ZERO_BYTES + 4 * NC + (R == 3 || R == 4 ? R * NC * 64 : 0) + L::LDS <= 160 * 1024,
                 "LDS budget (x digits, flags, partial sums, ring)");
   static_assert(XK / 16 <= 64 * NC * XP, "x preparation: one thread per 16 elements");
   static std::atomic<uint64_t> attr{0};
