@@ -91,7 +91,13 @@ struct QArgs {
   const uint8_t* W[QG];
 };
 
-__device__ __forceinline__ uint32_t swz(int row, int chunk) { return (uint32_t)(row * 64 + ((chunk ^ ((row >> 2) & 3)) * 16)); }
+// Byte of 16-byte chunk `chunk` (of 4) of B-tile row `row` (64 bytes, 32 halfs of K):
+// the chunk index is XORed with (row / 2) % 4, so the 8 rows that one pass of a
+// 16-byte LDS access serves (8 lanes, 32 banks) start on 8 distinct bank groups,
+// at one chunk (the consumers' fragment reads) and at chunks 0 and 2 of 4 rows
+// (producers that write half a row per lane).  (row / 4) % 4 left rows r and r+2
+// on one bank group.
+__device__ __forceinline__ uint32_t swz(int row, int chunk) { return (uint32_t)(row * 64 + ((chunk ^ ((row >> 1) & 3)) * 16)); }
 
 __device__ __forceinline__ void lds_rel(int* p, int v) {
   __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
