@@ -99,6 +99,27 @@ def test_gemv_q6k_mfma(gpu, N, K):
     assert err.max() <= 1e-4
 
 
+@pytest.mark.parametrize("N,K", [(64, 4096), (4100, 14336), (13824, 5120)])
+def test_gemv_q6k_extremes(gpu, N, K):
+    """Q6_K rows at the ends of the value range: every scale -128 and every q6 0 or 63
+    (the weights -32 and 31, so the digit dots of q6 and the digit sums taken off them
+    both reach their largest sizes), x over 2^-30 .. 2^30 in every 32-element block.
+    Rows are checked one by one: a row read at a wrong dword phase or a wrong digit
+    sum stands out."""
+    rng = np.random.default_rng(N + K + 66)
+    t = tier_amd.Q6_K
+    blocks = oracle.random_blocks(rng, t, N * (K // 256)).reshape(N, -1)
+    b = blocks.reshape(-1, 210)
+    b[:, 192:208] = 0x80
+    b[:, :192] = rng.choice(np.array([0x00, 0xFF], np.uint8), size=(b.shape[0], 192))
+    x = (rng.standard_normal(K) * np.float32(2.0) ** rng.integers(-30, 31, K)).astype(np.float32)
+    y = _gemv(blocks, t, x, N, K)
+    want = oracle.gemv_f64(blocks, t, x, N, K)
+    assert oracle.rel_fro(y, want) <= TOL
+    err = np.abs(y - want) / np.maximum(np.abs(want), 1e-3 * np.abs(want).max())
+    assert err.max() <= 1e-4
+
+
 @pytest.mark.parametrize("t", [tier_amd.Q8_0, tier_amd.Q5_1])
 def test_gemv_block32_unaligned_rows(gpu, t):
     """Weights at an address that is not 16-byte aligned take the per-element kernel;
