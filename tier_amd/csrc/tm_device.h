@@ -103,6 +103,12 @@ __device__ __forceinline__ void ktile_unit(size_t u, size_t rows, size_t& row, i
 // compiler adds no vmcnt wait before an LDS read of a slot that
 // __builtin_amdgcn_global_load_lds writes), so the stage pipelines wait with explicit
 // vm_wait counts; every one of them was measured with this asm form.
+// dma16 / dma16_nt set M0 (the LDS destination) inside their asm, unseen by the
+// compiler, which treats M0 as reserved.  That is sound while the compiler puts
+// nothing of its own in M0 in the kernels that call them: in their gfx950 code the
+// only M0 references are these writes.  A kernel that adds an LDS-DMA builtin,
+// s_sendmsg or indexed register access must move to __builtin_amdgcn_global_load_lds,
+// which lets the compiler own M0.
 __device__ __forceinline__ void dma16(const void* p, uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(p),
                "s"(__builtin_amdgcn_readfirstlane(lds_addr))
