@@ -8,7 +8,12 @@ inputs resident in HBM.  The weight is rotated over enough copies (> 256 MiB in
 total) that the 256 MiB Infinity Cache cannot hold them, so each step streams
 its weight from HBM.  ``value`` is the whole-run rate: algorithmic bytes of K
 steps / wall time between HIP events recorded around them on the stream the
-kernels run on.  ``roofline.achieved`` is the same bytes per launch over the
+kernels run on.  The K tiermm_qgemv calls are issued from a C loop through the C
+ABI (libtiermm_probe.so's tiermm_bench_qgemv), as the engine's token loop calls
+gemv_q: from Python each call costs about as much host time as a short GEMV takes
+on the GPU.  They follow the W warm-up steps and, before those, ~30 ms of untimed
+launches that bring the clock back from the idle of the host-side input
+preparation.  ``roofline.achieved`` is the same bytes per launch over the
 same events' average time per launch (it includes the gap between back-to-back
 dispatches, about 1.5 us on MI355X, which a profiler's kernel duration leaves
 out).
@@ -78,6 +83,49 @@ class GemvCase:
         tier_amd.gemv_q(self.W[i % self.copies].ptr, self.qtype, self.rb, self.X.ptr, self.Y.ptr, self.N, self.K,
                         stream)
 
+    def launches(self, tier_amd, first: int, count: int, stream) -> None:
+        """`count` calls of tiermm_qgemv (copies first, first + 1, ...) issued from a C loop."""
+        P = probe_lib()
+        ws = (ctypes.c_void_p * self.copies)(*[w.ptr for w in self.W])
+        fn = ctypes.cast(tier_amd.lib().tiermm_qgemv, ctypes.c_void_p)
+        st = P.tiermm_bench_qgemv(fn, ws, self.copies, first, self.qtype, self.rb, self.X.ptr, self.Y.ptr, self.N,
+                                  self.K, count, stream.handle)
+        if st:
+            raise RuntimeError(f"tiermm_qgemv: status {st}: {tier_amd.last_error()}")
+
+
+_PROBE = None
+
+
+def probe_lib():
+    """libtiermm_probe.so (tier_amd/csrc/probe.hip): the read floor, the MFMA ceiling and
+    the C loop that issues a run of decode GEMVs."""
+    global _PROBE
+    if _PROBE is None:
+        vp, i = ctypes.c_void_p, ctypes.c_int
+        P = ctypes.CDLL(os.path.join(ROOT, "tier_amd", "libtiermm_probe.so"))
+        P.tiermm_probe_read.argtypes = [vp, ctypes.c_size_t, i, i, vp, vp]
+        P.tiermm_probe_mfma.argtypes = [vp, i, i, vp, vp]
+        P.tiermm_bench_qgemv.argtypes = [vp, vp, i, i, i, ctypes.c_size_t, vp, vp, i, i, i, vp]
+        _PROBE = P
+    return _PROBE
+
+
+def time_gemv(hip, stream, tier_amd, case: GemvCase, steps: int, warmup: int) -> float:
+    """Milliseconds per call: `steps` back-to-back tiermm_qgemv calls, issued from a C loop
+    through the C ABI, between two HIP events on `stream` (after `warmup` calls)."""
+    case.launches(tier_amd, 0, warmup, stream)
+    stream.synchronize()
+    t0, t1 = hip.Event(), hip.Event()
+    t0.record(stream)
+    case.launches(tier_amd, warmup, steps, stream)
+    t1.record(stream)
+    t1.synchronize()
+    per = t0.elapsed_ms(t1) / steps
+    t0.destroy()
+    t1.destroy()
+    return per
+
 
 def time_launches(hip, stream, launch, steps: int, warmup: int) -> float:
     """Milliseconds per launch: `steps` back-to-back launches between two HIP events on `stream`."""
@@ -94,6 +142,18 @@ def time_launches(hip, stream, launch, steps: int, warmup: int) -> float:
     t0.destroy()
     t1.destroy()
     return per
+
+
+def settle(hip, stream, launch, ms: float = 30.0) -> None:
+    """Untimed launches for `ms` milliseconds before a decode line's warm-up steps.  The
+    host-side input preparation (quantizing the weight) leaves the GPU idle for seconds,
+    and the clock controller then needs a few milliseconds of work to return to its
+    working clock: the 13824x5120 GEMV measured 9.05 us per step over the first 20 steps
+    after idle and 8.6-8.7 us once settled, same box."""
+    est = time_launches(hip, stream, launch, 4, 1)
+    for i in range(max(1, int(ms / max(est, 1e-3)))):
+        launch(i)
+    stream.synchronize()
 
 
 def time_steady(hip, stream, launch, steps: int, warm_ms: float = 60.0) -> float:
@@ -296,6 +356,43 @@ def bench_moe(tier_amd, hip, stream):
                         "(64 experts each); no activation between"}
 
 
+def bench_floors(hip, stream, head: GemvCase, head_ms: float):
+    """What the hardware gives the two roofs on this box, from libtiermm_probe.so
+    (tier_amd/csrc/probe.hip): one read of the headline's bytes with nothing else to
+    do (non-temporal 16-byte loads, 2048 workgroups, over the same number of rotated
+    copies as the headline), and a register-only v_mfma_f32_32x32x16_f16 loop on
+    random-like operands (1024 workgroups x 4 waves x 8 independent accumulators)."""
+    lib = probe_lib()
+    nbytes = head.N * head.rb // 16 * 16
+    bufs = [hip.DeviceBuffer(nbytes) for _ in range(head.copies)]
+    for b in bufs:
+        b.fill_bytes(1)
+    out = hip.DeviceBuffer(1 << 16)
+
+    def read(i):
+        if lib.tiermm_probe_read(bufs[i % head.copies].ptr, nbytes, 2048, 1, out.ptr, stream.handle):
+            raise RuntimeError("tiermm_probe_read")
+    log("bench: read floor")
+    rd = min(time_launches(hip, stream, read, 200, 20) for _ in range(3))
+    for b in bufs:
+        b.free()
+    seed = hip.to_device((np.arange(1024, dtype=np.uint64) * 2654435761 % (1 << 32)).astype(np.uint32))
+    mo = hip.DeviceBuffer(1024 * 256 * 4)
+
+    def mfma(_i):
+        if lib.tiermm_probe_mfma(seed.ptr, 1024, 4096, mo.ptr, stream.handle):
+            raise RuntimeError("tiermm_probe_mfma")
+    log("bench: mfma ceiling")
+    mm = time_steady(hip, stream, mfma, 5)
+    tf = 1024 * 4 * 8 * 4096 * 32768 / (mm * 1e-3) / 1e12
+    return {"read_once": {"bytes": nbytes, "us_per_launch": round(rd * 1e3, 3),
+                          "GB/s": round(nbytes / (rd * 1e-3) / 1e9, 1),
+                          "frac_hbm": round(nbytes / (rd * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                          "headline_over_read": round(head_ms / rd, 3)},
+            "mfma_f16": {"TFLOPS": round(tf, 1), "frac_dense_peak": round(tf / FP16_PEAK_TFLOPS, 4),
+                         "x3_target_over_this": round(0.6 * FP16_PEAK_TFLOPS / tf, 4)}}
+
+
 def measured_traffic():
     """HBM bytes per headline launch from the committed rocprofv3 PMC summary
     (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter's reading for a copy
@@ -382,7 +479,8 @@ def main() -> int:
     # ---------------------------------------------------------------- headline
     log("bench: preparing q4_K 13824x5120 GEMV inputs")
     head = GemvCase(tier_amd, hip, tier_amd.Q4_K, 13824, 5120, seed=3)
-    per = time_launches(hip, stream, lambda i: head.launch(tier_amd, i, stream), args.steps, args.warmup)
+    settle(hip, stream, lambda i: head.launch(tier_amd, i, stream))
+    per = time_gemv(hip, stream, tier_amd, head, args.steps, args.warmup)
     wall = per * args.steps
     value = head.bytes * args.steps / (wall * 1e-3) / 1e9
     achieved = head.bytes / (per * 1e-3) / 1e9
@@ -403,7 +501,8 @@ def main() -> int:
                 continue
             log(f"bench: {name}")
             c = GemvCase(tier_amd, hip, qt, N, K, seed=N + K)
-            km = time_launches(hip, stream, lambda i: c.launch(tier_amd, i, stream), reps, warm)
+            settle(hip, stream, lambda i: c.launch(tier_amd, i, stream))
+            km = time_gemv(hip, stream, tier_amd, c, reps, warm)
             secondary[name] = {"GB/s": round(c.bytes / (km * 1e-3) / 1e9, 1),
                                "frac_hbm": round(c.bytes / (km * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                                "us_per_step": round(km * 1e3, 2)}
@@ -453,6 +552,9 @@ def main() -> int:
         secondary["moe_t4096"] = bench_moe(tier_amd, hip, stream)
     if want("chat_streamed_4_layers"):
         secondary["chat_streamed_4_layers"] = bench_chat_stream(tier_amd, hip, stream)
+
+    if want("floors"):
+        secondary["floors"] = bench_floors(hip, stream, head, per)
 
     traffic, traffic_src = measured_traffic()
     cpu = None

@@ -28,6 +28,15 @@ def test_exports_every_declared_symbol():
     assert sorted(tier_amd.EXPORTS) == names
 
 
+def test_probe_library_loads():
+    """bench.py's measurement kernels (the read floor and the fp16 MFMA ceiling) build and load."""
+    import ctypes
+    import os
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(tier_amd.__file__), "libtiermm_probe.so"))
+    for n in ("tiermm_probe_read", "tiermm_probe_read_lds", "tiermm_probe_mfma", "tiermm_bench_qgemv"):
+        assert hasattr(lib, n), n
+
+
 def test_registry_matches_oracle_table():
     for t in (0, 1, 2, 3, 6, 7, 8, 10, 11, 12, 13, 14, 16, 17, 18, 19, 20, 21, 22, 23, 29, 30, 34, 35, 39, 200, 201):
         assert tier_amd.q_info(t) == oracle.block(t)

@@ -1,7 +1,8 @@
 """Build libtiermm.so in-tree for gfx950 (hipcc for the kernels, g++ for host-only code).
 
 Run ``python -m tier_amd.build`` or call ``build()``; ``__graft_entry__.build()``
-calls it.  Objects go to ``tier_amd/_build/``; the library to ``tier_amd/libtiermm.so``.
+calls it.  Objects go to ``tier_amd/_build/``; the library to ``tier_amd/libtiermm.so``,
+and bench.py's measurement kernels (probe.hip) to ``tier_amd/libtiermm_probe.so``.
 """
 from __future__ import annotations
 
@@ -14,6 +15,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libtiermm.so")
+# measurement kernels for bench.py only (the plain-read floor and the fp16 MFMA ceiling)
+PROBE_LIB = os.path.join(HERE, "libtiermm_probe.so")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 
@@ -57,6 +60,9 @@ def build(verbose: bool = False) -> str:
     _run([HIPCC, "-shared", "-fPIC", "--offload-arch=gfx950", "-o", tmp] + objs +
          ["-L", os.path.join(ROCM, "lib"), "-lamdhip64", "-pthread", "-Wl,-rpath," + os.path.join(ROCM, "lib")])
     os.replace(tmp, LIB)
+    tmp = PROBE_LIB + ".tmp"
+    _run([HIPCC] + HIP_FLAGS + ["-shared", "-o", tmp, os.path.join(CSRC, "probe.hip")])
+    os.replace(tmp, PROBE_LIB)
     return LIB
 
 
