@@ -84,25 +84,27 @@ __global__ __launch_bounds__(64 * RT * KS) void qgemv_q4k_mfma(const uint8_t* __
   float* red = (float*)(ring + RT * KS * STAGES * SBYTES);
   const int ngrp = (nsb + GS - 1) / GS;
 
-  // ---- x loads first, then the first STAGES-1 groups of weights; the x
-  // preparation overlaps their latency.  One thread per 16 elements of x
-  // (threads past K/16 load a clamped copy and skip the preparation).
+  // ---- x first, then the first STAGES-1 groups of weights; the x preparation
+  // overlaps their latency.  x (K floats, the size of the digit area xq) comes into
+  // xq by the same LDS DMA, 1 KiB per load spread over the waves; each wave waits for
+  // its own x loads (they are older than its weight loads), a barrier for everyone's.
+  // One thread per 16 elements of x (threads past K/16 read a clamped copy and skip
+  // the preparation).
   const uint32_t ring_lds = lds_addr(myring);
+  for (int j = wave; j < nsb_all; j += RT * KS) dma16(x + 256 * j + 4 * lane, lds_addr(xq) + 1024 * j);
+#pragma unroll
+  for (int p = 0; p < STAGES - 1; ++p)
+    load_group<GS, F::SBB>(base0, rb, roff, coff, lane, p, nsb, ring_lds + p * SBYTES);
+  vm_wait<NLD * (STAGES - 1)>();  // this wave's x has landed; the weight groups stay in flight
+  __syncthreads();                // every wave's
   u32x4 xr[XP][4];
 #pragma unroll
   for (int j = 0; j < XP; ++j) {
     const int hh = min(tid + j * NT, (K >> 4) - 1);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) xr[j][i] = gload16(x + hh * 16 + 4 * i);
+    for (int i = 0; i < 4; ++i) xr[j][i] = *(const u32x4*)(xq + 64 * hh + 16 * i);
   }
-#pragma unroll
-  for (int p = 0; p < STAGES - 1; ++p)
-    load_group<GS, F::SBB>(base0, rb, roff, coff, lane, p, nsb, ring_lds + p * SBYTES);
-  vm_wait<NLD * (STAGES - 1)>();  // x has landed; the weight groups stay in flight
-#pragma unroll
-  for (int j = 0; j < XP; ++j)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(xr[j][i]));
+  __syncthreads();  // x is in registers: the digits may overwrite it
 
   __shared__ int nf[RT * KS];  // per wave: x held a non-finite value
   for (int i = tid; i < ZERO_BYTES / 4; i += NT) ((uint32_t*)zero)[i] = 0u;

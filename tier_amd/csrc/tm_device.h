@@ -66,18 +66,13 @@ __device__ float nonfinite_terms(const uint8_t* row, const float* x, int k0, int
 // waiting for everything before LDS reads), which would serialise the stream.
 // Every vector load below is one instruction per wave regardless of the lane
 // mask, and loads retire in order, so "s_waitcnt vmcnt(N)" means all but the N
-// most recent ones have landed.  gload16's destination looks ready to the
-// compiler at once: use it only where nothing touches that register before the
-// explicit wait (straight-line code); a register ring carried around a loop can
-// be copied by the compiler while its load is in flight, so loops load with
-// plain loads and let the compiler place the waits.
+// most recent ones have landed.  Only loads into LDS are hand-issued: a register
+// that a hand-issued load fills looks ready to the compiler at once, which may
+// copy it while the load is in flight, so loads into registers are plain loads
+// whose waits the compiler places (x that a wave needs while its own LDS DMA is
+// in flight comes into LDS by the same DMA instead).
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ u32x4 gload16(const void* p) {
-  u32x4 r;
-  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p) : "memory");
-  return r;
-}
 // K-tiled plane layout of the internal fp16 operands of the big-tile GEMM:
 // element (row, col) of a plane with `rows` rows at ((col / 32) * rows + row) * 32
 // + col % 32, so that the 64 bytes of one K step of 16 consecutive rows are one
@@ -95,20 +90,18 @@ __device__ __forceinline__ void ktile_unit(size_t u, size_t rows, size_t& row, i
 
 // 16 bytes per lane from p into LDS at lds_addr + 16*lane (lds_addr wave-uniform, through M0).
 //
-// M0 is written here without the compiler's knowledge (it treats M0 as reserved, and an
-// "m0" clobber is not honoured).  This holds because nothing else in the kernels that
-// call these helpers uses M0: no LDS-DMA builtins, s_sendmsg, indexed register access or
-// LDS-direct reads; a kernel that adds such a use must not keep M0 live across a call
-// here.  Either form leaves the ordering of DMA and LDS reads to the program (the
-// compiler adds no vmcnt wait before an LDS read of a slot that
-// __builtin_amdgcn_global_load_lds writes), so the stage pipelines wait with explicit
-// vm_wait counts; every one of them was measured with this asm form.
 // dma16 / dma16_nt set M0 (the LDS destination) inside their asm, unseen by the
-// compiler, which treats M0 as reserved.  That is sound while the compiler puts
-// nothing of its own in M0 in the kernels that call them: in their gfx950 code the
-// only M0 references are these writes.  A kernel that adds an LDS-DMA builtin,
-// s_sendmsg or indexed register access must move to __builtin_amdgcn_global_load_lds,
-// which lets the compiler own M0.
+// compiler, which treats M0 as reserved (an "m0" clobber is not honoured).  That is
+// sound while the compiler puts nothing of its own in M0 in the kernels that call
+// them: no LDS-DMA builtins, s_sendmsg, indexed register access or LDS-direct reads;
+// in their gfx950 code the only M0 references are these writes.  The loads are
+// invisible to the compiler's wait insertion, so every pipeline waits with explicit
+// vm_wait counts.  __builtin_amdgcn_global_load_lds, which lets the compiler own M0,
+// makes the loads visible to it instead, and it then waits for all of them
+// (s_waitcnt vmcnt(0)) before every release store of a hand-off flag and before
+// every workgroup barrier: built that way, qgemv_q4k_ws.hip carries 498 -> 618
+// vmcnt waits and x3.hip 4408 -> 4746, and the stage in flight behind a
+// flag drains before the flag is set.  So the asm form stays.
 __device__ __forceinline__ void dma16(const void* p, uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(p),
                "s"(__builtin_amdgcn_readfirstlane(lds_addr))
