@@ -21,7 +21,8 @@ out).
 Secondary measurements in the same JSON line (``secondary``): the other config
 shapes at M=1, q8_0 4096x4096 (config 1), the fused-path quantized GEMM at
 M=512 (config 3, TFLOPS against fp16 peak/3), the x3-2x2 GEMM at M=4096
-(config 2), the seven projections of a decoder layer (config 4), the routed MoE
+(config 2), the fp32 products of the x3-off fallback (tiermm_sgemm, forward and dX at
+the decoder's down projection), the seven projections of a decoder layer (config 4), the routed MoE
 experts (config 5), and the chat linears of four config-4 layers streamed from
 pinned host memory against the host-to-device copy rate.
 
@@ -546,6 +547,32 @@ def main() -> int:
         secondary["x3s_4096x5120x5120"] = {"TFLOPS": round(tf, 2), "frac_x3_peak": round(tf / X3_PEAK_TFLOPS, 4),
                                            "us_per_call": round(km * 1e3, 1), "includes": "X split + GEMM"}
         del bufs, Wf, Xf
+    # the x3-off fallback's fp32 products (sgemm, tier.cpp:1196-1200, 1229-1236) at the
+    # decoder's down projection (W 5120x14336): forward and dX, 4096 tokens, beta = 1 for dX
+    for name, opA in (("sgemm_fwd_4096x5120x14336", tier_amd.OP_T), ("sgemm_dx_4096x14336x5120", tier_amd.OP_N)):
+        if not want(name):
+            continue
+        log(f"bench: {name}")
+        T, Nw, Kw = 4096, 5120, 14336
+        rng = np.random.default_rng(21)
+        Wf = hip.to_device(rng.standard_normal((Nw, Kw), dtype=np.float32) * np.float32(0.02))
+        if opA == tier_amd.OP_T:  # out[T][Nw] = x[T][Kw] W^T
+            m, n, k, lda, Bm = Nw, T, Kw, Kw, hip.to_device(rng.standard_normal((T, Kw), dtype=np.float32))
+        else:  # dX[T][Kw] = dY[T][Nw] W
+            m, n, k, lda, Bm = Kw, T, Nw, Kw, hip.to_device(rng.standard_normal((T, Nw), dtype=np.float32))
+        C = hip.DeviceBuffer(n * m * 4)
+        C.fill_bytes(0)
+        wsb = tier_amd.sgemm_ws_bytes(opA, m, n, k)
+        WS = hip.DeviceBuffer(wsb)
+        beta = 0.0 if opA == tier_amd.OP_T else 1.0
+        f = lambda i: tier_amd.sgemm(opA, m, n, k, Wf.ptr, lda, Bm.ptr, k, beta, C.ptr, m,  # noqa: E731
+                                     WS.ptr, wsb, stream)
+        km = time_steady(hip, stream, f, 10)
+        tf = 2.0 * m * n * k / (km * 1e-3) / 1e12
+        secondary[name] = {"TFLOPS": round(tf, 2), "frac_x3_peak": round(tf / X3_PEAK_TFLOPS, 4),
+                           "us_per_call": round(km * 1e3, 1), "beta": beta,
+                           "includes": "both operands' two-part splits (dX: column maxima + transposed split) + GEMM"}
+        del Wf, Bm, C, WS
     if want("decoder_layer_t4096"):
         secondary["decoder_layer_t4096"] = bench_decoder_layer(tier_amd, hip, stream)
     if want("moe_t4096"):

@@ -215,6 +215,21 @@ int tiermm_x3s_gemm(const uint16_t* Xhi, const uint16_t* Xlo, const int32_t* xex
                     const uint16_t* Whi, const uint16_t* Wlo, const int32_t* wexp, float* Y,
                     int M, int N, int K, int ldy, tiermm_stream_t stream);
 
+/* sgemm (tier.cpp:773-865) with opB = N in its BLAS column-major contract, on fp32
+ * operands: C(m x n) = op(A)(m x k) * B(k x n) + beta * C.  It is the x3-off fallback
+ * of low3_linear / linear / linear_dx / linear_dx_acc (tier.cpp:1196-1200, 1213,
+ * 1229-1230, 1235-1236) on the expanded fp32 weight.  opA = TIERMM_OP_T, lda >= k: A
+ * is [m][lda] row-major (the forward out[n][m] = x[n][k] * W[m][k]^T); opA =
+ * TIERMM_OP_N, lda >= m: A is [k][lda] row-major (the dX product dX[n][m] = dY[n][k] *
+ * W[k][m]).  B is [n][ldb] (ldb >= k), C is [n][ldc] (ldc >= m).  The rows of op(A)
+ * and of B are split into fp16 hi/lo parts scaled by a power of two per row, and
+ * hi*hi + hi*lo + lo*hi run on fp16 MFMA with fp32 accumulation (any k: rows are
+ * zero-padded to a multiple of 32 in the workspace): rel. Frobenius error <= 2^-20
+ * against fp64(op(A) * B). */
+int tiermm_sgemm(int opA, int m, int n, int k, const float* A, int lda, const float* B, int ldb, float beta,
+                 float* C, int ldc, void* ws, size_t ws_bytes, tiermm_stream_t stream);
+size_t tiermm_sgemm_ws_bytes(int opA, int m, int n, int k);
+
 /* -------------------------------------------------------- quantized GEMM */
 /* The M > 1 quantized linear: Y[M][ldy] = X[M][K] * dequant(W)^T + beta * Y.
  * mode TIERMM_MODE_X3REF: W is dequantized to fp16 (bit-exact with dq_k<tier_fp16>,

@@ -61,7 +61,7 @@ EXPORTS = (
     "tiermm_tq_read_rows", "tiermm_tq_write", "tiermm_dequant_host", "tiermm_chat_create", "tiermm_chat_destroy",
     "tiermm_chat_add", "tiermm_chat_place", "tiermm_chat_lin", "tiermm_chat_restart", "tiermm_chat_info",
     "tiermm_host_alloc", "tiermm_host_free", "tiermm_x3_rows_noalloc", "tiermm_chat_set_heads",
-    "tiermm_chat_heads", "tiermm_chat_set_lora", "tiermm_chat_lora_scale",
+    "tiermm_chat_heads", "tiermm_chat_set_lora", "tiermm_chat_lora_scale", "tiermm_sgemm", "tiermm_sgemm_ws_bytes",
 )
 
 
@@ -105,6 +105,8 @@ _sig("tiermm_x3_rows_ws_bytes", [_i, _i, _i], _sz)
 _sig("tiermm_x3s_split", [_vp, _vp, _vp, _vp, _i, _i, _vp])
 _sig("tiermm_x3s_gemm", [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp])
 _sig("tiermm_qgemm", [_vp, _i, _sz, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp, _sz, _vp])
+_sig("tiermm_sgemm", [_i, _i, _i, _i, _vp, _i, _vp, _i, _f, _vp, _i, _vp, _sz, _vp])
+_sig("tiermm_sgemm_ws_bytes", [_i, _i, _i, _i], _sz)
 _sig("tiermm_qgemm_ws_bytes", [_i, _i, _i, _i, _i], _sz)
 _sig("tiermm_quantize", [_i, _vp, _vp, _sz, _i, _i])
 _sig("tiermm_gemv", [_vp, _i, _vp, _vp, _i, _i, _vp])
@@ -289,6 +291,17 @@ def x3s_split(src: int, hi: int, lo: int, exps: int, rows: int, cols: int, strea
 def x3s_gemm(Xhi: int, Xlo: int, xexp: int, Whi: int, Wlo: int, wexp: int, Y: int, M: int, N: int, K: int,
              ldy: int | None = None, stream=None) -> None:
     _check(_L.tiermm_x3s_gemm(Xhi, Xlo, xexp, Whi, Wlo, wexp, Y, M, N, K, N if ldy is None else ldy, _s(stream)))
+
+
+def sgemm(opA: int, m: int, n: int, k: int, A: int, lda: int, B: int, ldb: int, beta: float, C: int, ldc: int,
+          ws: int | None = None, ws_bytes: int = 0, stream=None) -> None:
+    """sgemm (tier.cpp:773) with opB = N in its BLAS column-major contract: the x3-off
+    fallback's fp32 product (tier.cpp:1196-1200, 1229-1230, 1235-1236)."""
+    _check(_L.tiermm_sgemm(opA, m, n, k, A, lda, B, ldb, beta, C, ldc, ws, ws_bytes, _s(stream)))
+
+
+def sgemm_ws_bytes(opA: int, m: int, n: int, k: int) -> int:
+    return _L.tiermm_sgemm_ws_bytes(opA, m, n, k)
 
 
 def qgemm(W: int, qtype: int, rb: int, X: int, Y: int, M: int, N: int, K: int, ldy: int | None = None,

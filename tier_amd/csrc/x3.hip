@@ -196,6 +196,75 @@ __global__ __launch_bounds__(256) void x3s_split_kernel(const float* __restrict_
   if (threadIdx.x == 0) exps[blockIdx.x] = e;
 }
 
+// ---- two-part splits for the fp32 product (tiermm_sgemm): the x3s split of rows
+// [rows][cols] with row stride ld into rows of kp (zeros past cols), and of the
+// columns of a [k][ld] matrix, transposed (op(A) = A in the BLAS column-major view).
+
+// One workgroup per row: e = x3s_exp(max |row|), hi/lo of row * 2^e, kp columns.
+__global__ __launch_bounds__(256) void x3s_split_ld_kernel(const float* __restrict__ src, size_t ld, int cols,
+                                                           int kp, uint16_t* __restrict__ hi, uint16_t* __restrict__ lo,
+                                                           int32_t* __restrict__ exps) {
+  __shared__ float red[4];
+  const float* row = src + (size_t)blockIdx.x * ld;
+  const size_t base = (size_t)blockIdx.x * kp;
+  float amax = 0.f;
+  for (int k = threadIdx.x; k < cols; k += 256) amax = fmaxf(amax, fabsf(row[k]));
+  amax = block_max_256(amax, red);
+  const int e = x3s_exp(amax);
+  const float sc = ldexpf(1.f, e);
+  for (int k = threadIdx.x; k < kp; k += 256) {
+    const float v = k < cols ? row[k] * sc : 0.f;
+    const uint16_t h = f2h(v);
+    hi[base + k] = h;
+    lo[base + k] = f2h(v - h2f(h));
+  }
+  if (threadIdx.x == 0) exps[blockIdx.x] = e;
+}
+
+// n words set to zero (a fill kernel rather than hipMemsetAsync: safe in graph capture).
+__global__ __launch_bounds__(256) void zero32_kernel(uint32_t* __restrict__ p, size_t n) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+// amax[c] = max over r < rows of |src[r][c]| (c < cols), as the bits of a non-negative
+// float (their integer order is the float order): 256 columns x 256 rows per workgroup.
+__global__ __launch_bounds__(256) void col_absmax_kernel(const float* __restrict__ src, size_t ld, int rows, int cols,
+                                                         uint32_t* __restrict__ amax) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= cols) return;
+  const int r0 = blockIdx.y * 256, r1 = min(rows, r0 + 256);
+  float m = 0.f;
+  for (int r = r0; r < r1; ++r) m = fmaxf(m, fabsf(src[(size_t)r * ld + c]));
+  atomicMax(amax + c, __float_as_uint(m));
+}
+
+// hi/lo[c][r] of src[r][c] * 2^e_c (e_c = x3s_exp(amax[c])) for c < cols, r < kp
+// (zeros for r >= rows), through a 64x64 LDS tile; exps[c] = e_c.
+__global__ __launch_bounds__(256) void x3s_split_t_kernel(const float* __restrict__ src, size_t ld, int rows, int cols,
+                                                          int kp, const uint32_t* __restrict__ amax,
+                                                          uint16_t* __restrict__ hi, uint16_t* __restrict__ lo,
+                                                          int32_t* __restrict__ exps) {
+  __shared__ float t[64][65];
+  const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int i = ty; i < 64; i += 4) {
+    const int r = r0 + i, c = c0 + tx;
+    t[i][tx] = r < rows && c < cols ? src[(size_t)r * ld + c] : 0.f;
+  }
+  __syncthreads();
+  for (int i = ty; i < 64; i += 4) {
+    const int c = c0 + i, r = r0 + tx;
+    if (c >= cols || r >= kp) continue;
+    const int e = x3s_exp(__uint_as_float(amax[c]));
+    const float v = t[tx][i] * ldexpf(1.f, e);
+    const uint16_t h = f2h(v);
+    hi[(size_t)c * kp + r] = h;
+    lo[(size_t)c * kp + r] = f2h(v - h2f(h));
+    if (blockIdx.y == 0 && tx == 0) exps[c] = e;
+  }
+}
+
 // fp16 transpose: dst[c][r] = src[r][c] for r < rows, c < cols (src row stride ld,
 // dst row stride dld >= rows), through a 64x64 LDS tile (odd column stride: no bank
 // conflicts).
@@ -1258,6 +1327,67 @@ static int qgemm_padded(const void* W, int qtype, size_t rb, const float* X, flo
   pad_split3_kernel<false><<<elem_grid(mkp), 256, 0, s>>>(X, (size_t)K, parts, (size_t)M, K, kp);
   TM_LAUNCH_CHECK("tiermm_qgemm: padded split");
   return x3ref_nt(parts, mkp, w16, kp, Y, ldy, M, N, kp, beta, s, who);
+}
+
+size_t tiermm_sgemm_ws_bytes(int opA, int m, int n, int k) {
+  // hi/lo planes and exponents of op(A) (m rows) and of B (n rows), rows of kp; for
+  // TIERMM_OP_N the column maxima of A
+  const size_t kp = (size_t)pad32(k);
+  return 2 * al256((size_t)m * kp * 2) + al256((size_t)m * 4) + 2 * al256((size_t)n * kp * 2) + al256((size_t)n * 4) +
+         (opA == TIERMM_OP_N ? al256((size_t)m * 4) : 0);
+}
+
+int tiermm_sgemm(int opA, int m, int n, int k, const float* A, int lda, const float* B, int ldb, float beta, float* C,
+                 int ldc, void* ws, size_t ws_bytes, tiermm_stream_t stream) {
+  const char* who = "tiermm_sgemm";
+  if (opA != TIERMM_OP_T && opA != TIERMM_OP_N) return set_error(TIERMM_EINVAL, "%s: opA %d", who, opA);
+  int st = check_sizes(who, n, m, k);
+  if (st) return st;
+  if ((opA == TIERMM_OP_T && lda < k) || (opA == TIERMM_OP_N && lda < m) || ldb < k || ldc < m)
+    return set_error(TIERMM_EINVAL, "%s: lda, ldb or ldc too small", who);
+  if (m == 0 || n == 0) return TIERMM_OK;
+  if (!A || !B || !C) return set_error(TIERMM_EINVAL, "%s: null buffer", who);
+  void* w = nullptr;
+  st = get_workspace(ws, ws_bytes, tiermm_sgemm_ws_bytes(opA, m, n, k), &w, who);
+  if (st) return st;
+  hipStream_t s = (hipStream_t)stream;
+  const int kp = pad32(k);
+  uint8_t* b = (uint8_t*)w;
+  uint16_t* ahi = (uint16_t*)b; b += al256((size_t)m * kp * 2);
+  uint16_t* alo = (uint16_t*)b; b += al256((size_t)m * kp * 2);
+  int32_t* aexp = (int32_t*)b;  b += al256((size_t)m * 4);
+  uint16_t* bhi = (uint16_t*)b; b += al256((size_t)n * kp * 2);
+  uint16_t* blo = (uint16_t*)b; b += al256((size_t)n * kp * 2);
+  int32_t* bexp = (int32_t*)b;  b += al256((size_t)n * 4);
+  // rows [rows][ld] into rows of kp: the register-resident split when they are packed
+  // rows of a whole number of K steps, else the general one
+  auto split_rows = [&](const float* src, int ld, int rows, uint16_t* hi, uint16_t* lo, int32_t* ex) {
+    if (ld == kp && kp == k) x3s_split_launch(src, hi, lo, ex, rows, k, s);
+    else x3s_split_ld_kernel<<<rows, 256, 0, s>>>(src, (size_t)ld, k, kp, hi, lo, ex);
+  };
+  if (opA == TIERMM_OP_T) {  // op(A) rows are A's rows: [m][lda]
+    split_rows(A, lda, m, ahi, alo, aexp);
+    TM_LAUNCH_CHECK("tiermm_sgemm: split A");
+  } else {  // op(A) rows are A's columns: A is [k][lda] in memory (linear_dx, tier.cpp:1226)
+    uint32_t* amax = (uint32_t*)b;
+    zero32_kernel<<<(unsigned)((m + 255) / 256), 256, 0, s>>>(amax, (size_t)m);
+    TM_LAUNCH_CHECK("tiermm_sgemm: column maxima");
+    col_absmax_kernel<<<dim3((unsigned)((m + 255) / 256), (unsigned)((k + 255) / 256)), 256, 0, s>>>(A, (size_t)lda, k,
+                                                                                                  m, amax);
+    TM_LAUNCH_CHECK("tiermm_sgemm: column maxima");
+    x3s_split_t_kernel<<<dim3((unsigned)((m + 63) / 64), (unsigned)((kp + 63) / 64)), 256, 0, s>>>(
+        A, (size_t)lda, k, m, kp, amax, ahi, alo, aexp);
+    TM_LAUNCH_CHECK("tiermm_sgemm: split A");
+  }
+  split_rows(B, ldb, n, bhi, blo, bexp);
+  TM_LAUNCH_CHECK("tiermm_sgemm: split B");
+  // column-major C(m x n) with ldc == row-major out[n][ldc] = B^T[n][k] * op(A)^T
+  X3Args a{};
+  a.A[0] = bhi; a.A[1] = blo; a.B[0] = ahi; a.B[1] = alo;
+  a.lda = kp; a.ldb = kp; a.C = C; a.ldc = ldc; a.M = n; a.N = m; a.K = kp;
+  a.aexp = bexp; a.bexp = aexp; a.beta = beta;
+  if (big_tiles(n, m) >= 192) return launch_x3_big<X3_2X2>(a, s, who);
+  return launch_x3<128, 128, X3_2X2>(a, s, who);
 }
 
 size_t tiermm_qgemm_ws_bytes(int qtype, int M, int N, int K, int mode) {
