@@ -248,6 +248,11 @@ int tiermm_qgemm(const void* W, int qtype, size_t rb, const float* X, float* Y, 
                  int K, int ldy, int mode, float beta, void* ws, size_t ws_bytes,
                  tiermm_stream_t stream);
 size_t tiermm_qgemm_ws_bytes(int qtype, int M, int N, int K, int mode);
+/* No counterpart in the reference (an introspection aid for tuning and tests): the tile
+ * plan that tiermm_qgemm's fused dequant kernel takes for a TIERMM_MODE_X3REF product of
+ * this shape -- tile width *bn, K splits *ks, accumulation chunks *kc -- after
+ * TIERMM_QGEMM_TILE; TIERMM_UNSUPPORTED when the type or shape does not take it. */
+int tiermm_qgemm_plan(int qtype, int M, int N, int K, int* bn, int* ks, int* kc);
 
 /* ------------------------------------------------- grouped (MoE) GEMM */
 /* No reference function (the reference refuses MoE models, arch.py:158-159):

@@ -52,14 +52,16 @@ void orc_f2bf_n(const float* x, uint16_t* b, size_t n);
  * Pinned: numpy reference rounding in tests (random + boundary inputs). */
 uint16_t orc_f2bf(float f);
 
-/* Scalar dequant of one element, quant.h:59-121: every type except the
- * lattice-grid IQ2_*, IQ3_* and IQ1_* families (Q8_0, Q4_0, Q4_1, Q5_0, Q5_1,
- * Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS, TQ1_0, TQ2_0, MXFP4, NF4, FP4,
- * F32, F16, BF16); 0 for those, where q_val reads its grids.  Pinned: the
- * reference's golden vectors (Q4_0..Q6_K) and closed-form special cases in
- * tests/test_oracle.py; every type on random blocks, and the types without
- * golden vectors on every payload byte value, against oracle/_ref (the
- * reference's own q_val); MXFP4's levels against E2M1 by definition. */
+/* Scalar dequant of one element, quant.h:59-121, for every type q_val handles:
+ * Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS,
+ * TQ1_0, TQ2_0, MXFP4, NF4, FP4, F32, F16, BF16, and the lattice-grid IQ2_XXS,
+ * IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S and IQ1_M, whose grids come from the
+ * library's tier_amd/csrc/iq_grids.h (the same tables the GPU decoders read); 0
+ * for other ids.  Pinned: the reference's golden vectors (Q4_0..Q6_K and the
+ * lattice types) and closed-form special cases in tests/test_oracle.py; every type
+ * on random blocks, the types without golden vectors on every payload byte value,
+ * and the lattice types on every grid point, against oracle/_ref (the reference's
+ * own q_val); MXFP4's levels against E2M1 by definition. */
 float orc_q_val(const uint8_t* row, int type, int col);
 
 /* dq_k<T> / dq_launch (tier.cpp:293-298): out[i] = T(q_val(W+(r0+i/cols)*rb, type, i%cols))

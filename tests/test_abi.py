@@ -202,3 +202,17 @@ def test_recipe_types_hand_checked():
     assert of("Q4_K_M", mv, "self_attn.v_proj") == ["q4_K", "q4_K", "q6_K", "q4_K", "q4_K", "q6_K"]
     with pytest.raises(tier_amd.TiermmError):
         tier_amd.recipe_types("Q3_K", m8)
+
+
+def test_qgemm_plan_query(monkeypatch):
+    """The fused GEMM's plan query (no device needed): types it does not decode have none, a
+    valid TIERMM_QGEMM_TILE is the plan run, an invalid one falls back to the cost model."""
+    monkeypatch.delenv("TIERMM_QGEMM_TILE", raising=False)
+    assert tier_amd.qgemm_plan(tier_amd.Q4_0, 300, 1000, 8192) is None
+    model = tier_amd.qgemm_plan(tier_amd.Q4_K, 300, 1000, 8192)
+    bn, ks, kc = model
+    assert ks * kc >= 2  # K = 8192 needs at least two accumulators (K chunks of at most 6144)
+    monkeypatch.setenv("TIERMM_QGEMM_TILE", "128,1,2")
+    assert tier_amd.qgemm_plan(tier_amd.Q4_K, 300, 1000, 8192) == (128, 1, 2)
+    monkeypatch.setenv("TIERMM_QGEMM_TILE", "100,1,2")  # no such tile width
+    assert tier_amd.qgemm_plan(tier_amd.Q4_K, 300, 1000, 8192) == model

@@ -177,3 +177,92 @@ def test_moe_combine_shapes(gpu, N, topk):
     out = OUT.download(np.float32, T * N).reshape(T, N)
     ref = np.einsum("tj,tjn->tn", pw[tp].astype(np.float64), ys[tp].astype(np.float64))
     assert oracle.rel_fro(out, ref) <= BAR
+
+
+def _grouped_case(rng, types, counts, N, K, seed):
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    P = int(offsets[-1])
+    E = len(types)
+    blocks = [oracle.random_blocks(rng, types[e], N * (K // oracle.block(types[e])[0])).reshape(N, -1) for e in range(E)]
+    xs = activations(P, K, seed=seed)
+    return offsets, P, blocks, xs
+
+
+def _grouped_run(types, blocks, xs, offsets, N, K, with_ws=False):
+    P = xs.shape[0]
+    dW = [hip.to_device(b) for b in blocks]
+    X, Y = hip.to_device(xs), hip.DeviceBuffer(P * N * 4)
+    ws = wsb = None
+    if with_ws:
+        wsb = tier_amd.qgemm_grouped_ws_bytes(types, offsets.tolist(), N, K)
+        ws = hip.DeviceBuffer(wsb)
+    tier_amd.qgemm_grouped([w.ptr for w in dW], types, [tier_amd.q_row_bytes(q, K) for q in types], X.ptr,
+                           offsets.tolist(), Y.ptr, N, K, ws=ws.ptr if ws else None, ws_bytes=wsb or 0)
+    hip.synchronize()
+    return Y.download(np.float32, P * N).reshape(P, N)
+
+
+def _expert_ref(blocks, t, xs, N, K):
+    w16 = oracle.h2f(oracle.dequant(blocks, t, K, oracle.OUT_F16)).reshape(N, K).astype(np.float64)
+    return xs.astype(np.float64) @ w16.T
+
+
+def test_grouped_fused_long_k_bit_identical_per_expert(gpu, monkeypatch):
+    """All-q4_K experts at K = 8192, beyond one accumulator's 6144: the grouped call takes the
+    fused kernel over several expert groups with two accumulation chunks (it may not split
+    K).  Each expert against fp64, and bit for bit against tiermm_qgemm on that expert alone
+    with the same plan forced (BN 128, one split, two chunks)."""
+    monkeypatch.setenv("TIERMM_QGEMM_TILE", "128,1,2")
+    rng = np.random.default_rng(8192)
+    N, K = 320, 8192
+    counts = np.array([41, 0, 57, 1, 64, 38])
+    types = [tier_amd.Q4_K] * len(counts)
+    offsets, P, blocks, xs = _grouped_case(rng, types, counts, N, K, seed=73)
+    assert tier_amd.qgemm_plan(tier_amd.Q4_K, int(counts.max()), N, K) == (128, 1, 2)
+    ys = _grouped_run(types, blocks, xs, offsets, N, K)
+    for e in range(len(counts)):
+        a, b = offsets[e], offsets[e + 1]
+        if a == b:
+            continue
+        assert oracle.rel_fro(ys[a:b], _expert_ref(blocks[e], types[e], xs[a:b], N, K)) <= BAR, e
+        W, X, Y = hip.to_device(blocks[e]), hip.to_device(np.ascontiguousarray(xs[a:b])), hip.DeviceBuffer((b - a) * N * 4)
+        tier_amd.qgemm(W.ptr, types[e], tier_amd.q_row_bytes(types[e], K), X.ptr, Y.ptr, b - a, N, K)
+        hip.synchronize()
+        one = Y.download(np.float32, (b - a) * N).reshape(b - a, N)
+        assert np.array_equal(one.view(np.uint32), ys[a:b].view(np.uint32)), e
+
+
+def test_grouped_staged_long_k_fills_chip(gpu):
+    """q4_0 experts (staged through fp16, not decoded in the GEMM) at K = 8192 with enough
+    routed rows for the grouped 256-row big-tile launch, whose K chunks shift each expert's
+    weight pointer: three experts (the first, one in the middle, the last) in full against
+    fp64, and the whole output with and without a caller workspace bit for bit."""
+    rng = np.random.default_rng(8193)
+    E, N, K = 24, 1280, 8192
+    counts = rng.integers(257, 320, E)
+    types = [tier_amd.Q4_0] * E
+    offsets, P, blocks, xs = _grouped_case(rng, types, counts, N, K, seed=74)
+    ys = _grouped_run(types, blocks, xs, offsets, N, K)
+    ys_ws = _grouped_run(types, blocks, xs, offsets, N, K, with_ws=True)
+    assert np.array_equal(ys.view(np.uint32), ys_ws.view(np.uint32))
+    for e in (0, 11, E - 1):
+        a, b = offsets[e], offsets[e + 1]
+        assert oracle.rel_fro(ys[a:b], _expert_ref(blocks[e], types[e], xs[a:b], N, K)) <= BAR, e
+
+
+@pytest.mark.parametrize("with_ws", [False, True])
+def test_grouped_sparse_mixed_types(gpu, with_ws):
+    """A routed batch that does not fill the chip and mixes types the fused kernel decodes
+    (q4_K, q6_K: one fused launch per type over its experts) with one it does not (q4_0:
+    staged per expert), about 50 rows each: every expert against fp64."""
+    rng = np.random.default_rng(50)
+    N, K = 256, 1024
+    types = [tier_amd.Q4_K, tier_amd.Q4_0, tier_amd.Q6_K] * 3
+    counts = rng.integers(40, 60, len(types))
+    counts[4] = 0
+    offsets, P, blocks, xs = _grouped_case(rng, types, counts, N, K, seed=75)
+    ys = _grouped_run(types, blocks, xs, offsets, N, K, with_ws=with_ws)
+    for e in range(len(types)):
+        a, b = offsets[e], offsets[e + 1]
+        if a < b:
+            assert oracle.rel_fro(ys[a:b], _expert_ref(blocks[e], types[e], xs[a:b], N, K)) <= BAR, e

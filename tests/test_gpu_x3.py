@@ -274,6 +274,8 @@ def test_qgemm_fused_k_chunks(gpu, monkeypatch, t, plan):
     ks = int(plan.split(",")[1]) if plan != "default" else None
     if ks is not None:
         assert tier_amd.qgemm_ws_bytes(t, M, N, K) == 3 * M * K * 2 + (ks * M * N * 4 if ks > 1 else 0)
+        want = tuple(int(v) for v in plan.split(",")) + ((1,) if plan.count(",") == 1 else ())
+        assert tier_amd.qgemm_plan(t, M, N, K) == want  # the forced plan is the one run
     rng = np.random.default_rng(K + t + len(plan))
     blocks = oracle.random_blocks(rng, t, N * (K // 256)).reshape(N, -1)
     x = activations(M, K, seed=27)

@@ -66,3 +66,12 @@ def test_noalloc_refuses_past_the_scratch(gpu):
     assert code == tier_amd.UNSUPPORTED
     assert "scratch" in tier_amd.last_error()
     assert not tier_amd.chat_fp3_noalloc(B.ptr, B.ptr, B.ptr, M, K, N, N)
+
+
+def test_noalloc_refuses_k_not_a_multiple_of_32(gpu):
+    """tiermm_x3_rows pads any K; the allocation-free form has no room for padded copies and
+    refuses K % 32 != 0 on the host, before any launch, so a caller can fall back."""
+    B = hip.DeviceBuffer(1024)  # never read
+    code = tier_amd.lib().tiermm_x3_rows_noalloc(B.ptr, B.ptr, B.ptr, 4, 1000, 8, 8, None)
+    assert code == tier_amd.UNSUPPORTED
+    assert "multiple of 32" in tier_amd.last_error()

@@ -62,6 +62,7 @@ EXPORTS = (
     "tiermm_chat_add", "tiermm_chat_place", "tiermm_chat_lin", "tiermm_chat_restart", "tiermm_chat_info",
     "tiermm_host_alloc", "tiermm_host_free", "tiermm_x3_rows_noalloc", "tiermm_chat_set_heads",
     "tiermm_chat_heads", "tiermm_chat_set_lora", "tiermm_chat_lora_scale", "tiermm_sgemm", "tiermm_sgemm_ws_bytes",
+    "tiermm_qgemm_plan",
 )
 
 
@@ -107,6 +108,7 @@ _sig("tiermm_x3s_gemm", [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]
 _sig("tiermm_qgemm", [_vp, _i, _sz, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp, _sz, _vp])
 _sig("tiermm_sgemm", [_i, _i, _i, _i, _vp, _i, _vp, _i, _f, _vp, _i, _vp, _sz, _vp])
 _sig("tiermm_sgemm_ws_bytes", [_i, _i, _i, _i], _sz)
+_sig("tiermm_qgemm_plan", [_i, _i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i), ctypes.POINTER(_i)])
 _sig("tiermm_qgemm_ws_bytes", [_i, _i, _i, _i, _i], _sz)
 _sig("tiermm_quantize", [_i, _vp, _vp, _sz, _i, _i])
 _sig("tiermm_gemv", [_vp, _i, _vp, _vp, _i, _i, _vp])
@@ -308,6 +310,16 @@ def qgemm(W: int, qtype: int, rb: int, X: int, Y: int, M: int, N: int, K: int, l
           mode: int = MODE_X3REF, beta: float = 0.0, ws: int | None = None, ws_bytes: int = 0, stream=None) -> None:
     _check(_L.tiermm_qgemm(W, qtype, rb, X, Y, M, N, K, N if ldy is None else ldy, mode, beta, ws, ws_bytes,
                            _s(stream)))
+
+
+def qgemm_plan(qtype: int, M: int, N: int, K: int):
+    """(BN, KS, KC) of the fused dequant GEMM for this shape, or None when it does not take it."""
+    bn, ks, kc = _i(), _i(), _i()
+    code = _L.tiermm_qgemm_plan(qtype, M, N, K, ctypes.byref(bn), ctypes.byref(ks), ctypes.byref(kc))
+    if code == UNSUPPORTED:
+        return None
+    _check(code)
+    return bn.value, ks.value, kc.value
 
 
 def qgemm_ws_bytes(qtype: int, M: int, N: int, K: int, mode: int = MODE_X3REF) -> int:

@@ -927,3 +927,18 @@ int qgemm_fused(const void* W, int qtype, size_t rb, const uint16_t* xparts, siz
 }
 
 }  // namespace tiermm
+
+// The plan tiermm_qgemm's fused kernel takes for one MODE_X3REF product of this shape
+// (the cost model, or TIERMM_QGEMM_TILE when valid for the shape): tile width, K
+// splits and accumulation chunks.
+extern "C" int tiermm_qgemm_plan(int qtype, int M, int N, int K, int* bn, int* ks, int* kc) {
+  using namespace tiermm;
+  if (M < 1 || N < 1 || K < 1 || !bn || !ks || !kc)
+    return set_error(TIERMM_EINVAL, "tiermm_qgemm_plan: M=%d N=%d K=%d and three outputs", M, N, K);
+  const QPlan pl = q_plan(qtype, &M, 1, N, K, cus_or_default(), true);
+  if (!pl.bn) return set_error(TIERMM_UNSUPPORTED, "tiermm_qgemm_plan: type %d N=%d K=%d is not decoded in the GEMM", qtype, N, K);
+  *bn = pl.bn;
+  *ks = pl.ks;
+  *kc = pl.kc;
+  return TIERMM_OK;
+}
