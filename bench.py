@@ -188,27 +188,31 @@ def _quantize(tier_amd, qtype, N, K, seed):
     return tier_amd.q_row(qtype, rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
 
 
-def bench_decoder_layer(tier_amd, hip, stream):
+def bench_decoder_layer(tier_amd, hip, stream, T=4096, mode=None):
     """Config 4: the 7 projections of one decoder layer (hidden 5120, 32 q / 8 kv heads x 128,
-    ffn 14336) on a packed 4096-token batch, q4_K_S recipe (q/k/o/gate/up q4_K, v/down q5_K),
-    each a tiermm_qgemm (fp16-dequant x3 semantics)."""
-    T, H, Q, KV, F = 4096, 5120, 4096, 1024, 14336
+    ffn 14336) on a packed T-token batch, q4_K_S recipe (q/k/o/gate/up q4_K, v/down q5_K),
+    each a tiermm_qgemm: fp16-dequant x3 semantics (MODE_X3REF, the training forward), or
+    MODE_F32 (chat_lin's prefill semantics, tier.cpp:2358-2359: fp32 dequant, fp32-accurate
+    product; its chunk is 256 rows, tier.cpp:2538), whose kernels decode W inside the GEMM
+    after one pass over W for its row exponents."""
+    mode = tier_amd.MODE_X3REF if mode is None else mode
+    H, Q, KV, F = 5120, 4096, 1024, 14336
     mats = (("q", tier_amd.Q4_K, Q, H), ("k", tier_amd.Q4_K, KV, H), ("v", tier_amd.Q5_K, KV, H),
             ("o", tier_amd.Q4_K, H, Q), ("gate", tier_amd.Q4_K, F, H), ("up", tier_amd.Q4_K, F, H),
             ("down", tier_amd.Q5_K, H, F))
     rng = np.random.default_rng(10)
     xs = {K: hip.to_device(rng.standard_normal((T, K), dtype=np.float32)) for K in (H, Q, F)}
     Y = hip.DeviceBuffer(T * F * 4)
-    wsb = max(tier_amd.qgemm_ws_bytes(qt, T, N, K) for _, qt, N, K in mats)
+    wsb = max(tier_amd.qgemm_ws_bytes(qt, T, N, K, mode) for _, qt, N, K in mats)
     WS = hip.DeviceBuffer(wsb)
     out, total_us, total_flop = {}, 0.0, 0.0
     for i, (name, qt, N, K) in enumerate(mats):
-        log(f"bench: decoder layer {name} {N}x{K}")
+        log(f"bench: decoder layer {name} {N}x{K} T={T} mode={mode}")
         Wd = hip.to_device(_quantized(tier_amd, qt, N, K, 11 + i))
         rb = tier_amd.q_row_bytes(qt, K)
         f = lambda _i: tier_amd.qgemm(Wd.ptr, qt, rb, xs[K].ptr, Y.ptr, T, N, K, N,  # noqa: E731
-                                      tier_amd.MODE_X3REF, 0.0, WS.ptr, wsb, stream)
-        km = time_steady(hip, stream, f, 10)
+                                      mode, 0.0, WS.ptr, wsb, stream)
+        km = time_steady(hip, stream, f, 10 if T >= 1024 else 40)
         flop = 2.0 * T * N * K
         out[name] = {"type": tier_amd.TYPE_NAMES[qt], "N": N, "K": K, "us": round(km * 1e3, 1),
                      "TFLOPS": round(flop / (km * 1e-3) / 1e12, 1)}
@@ -216,7 +220,8 @@ def bench_decoder_layer(tier_amd, hip, stream):
         total_flop += flop
         del Wd
     tf = total_flop / (total_us * 1e-6) / 1e12
-    return {"recipe": "q4_K_S (v, down q5_K)", "T": T, "total_us": round(total_us, 1),
+    return {"recipe": "q4_K_S (v, down q5_K)", "T": T, "mode": "f32" if mode == tier_amd.MODE_F32 else "x3ref",
+            "workspace_bytes": wsb, "total_us": round(total_us, 1),
             "TFLOPS": round(tf, 1), "frac_x3_peak": round(tf / X3_PEAK_TFLOPS, 4), "per_matrix": out}
 
 
@@ -575,6 +580,9 @@ def main() -> int:
         del Wf, Bm, C, WS
     if want("decoder_layer_t4096"):
         secondary["decoder_layer_t4096"] = bench_decoder_layer(tier_amd, hip, stream)
+    for T in (256, 4096):  # chat prefill: chunks of 256 rows (tier.cpp:2538), and the config's batch
+        if want(f"chat_prefill_t{T}"):
+            secondary[f"chat_prefill_t{T}"] = bench_decoder_layer(tier_amd, hip, stream, T, tier_amd.MODE_F32)
     if want("moe_t4096"):
         secondary["moe_t4096"] = bench_moe(tier_amd, hip, stream)
     if want("chat_streamed_4_layers"):

@@ -154,6 +154,17 @@ def test_workspace_sizes():
     assert tier_amd.qgemm_ws_bytes(tier_amd.Q5_K, 16384, 5120, 14336) == 3 * 16384 * 14336 * 2
     # other types stage fp16 W in the workspace as well
     assert tier_amd.qgemm_ws_bytes(tier_amd.Q4_0, 512, 5120, 5120) == 5120 * 5120 * 2 + 3 * 512 * 5120 * 2
+    # the fp32 semantics: the fused types keep no copy of W (x's hi and lo planes, both
+    # exponent rows, and at K = 14336 four K splits of partial sums); the others expand
+    # W in chunks of rows within 256 MiB (1600 rows of K = 20480: 1638 rounded down to
+    # whole 320-row tiles)
+    F32 = tier_amd.MODE_F32
+    assert tier_amd.qgemm_ws_bytes(tier_amd.Q4_K, 256, 14336, 5120, F32) == 2 * 256 * 5120 * 2 + 1024 + 14336 * 4
+    assert tier_amd.qgemm_ws_bytes(tier_amd.Q6_K, 256, 5120, 14336, F32) == \
+        2 * 256 * 14336 * 2 + 1024 + 5120 * 4 + 4 * 256 * 5120 * 4
+    K = 20480
+    assert tier_amd.qgemm_ws_bytes(tier_amd.Q4_0, 256, 14336, K, F32) == \
+        1600 * K * 4 + 2 * 1600 * K * 2 + 1600 * 4 + 2 * 256 * K * 2 + 1024
     # routed experts: 256-row tiles that fill the chip stage the fp16 weights of
     # up to 64 experts (1 GiB at most); few or mostly empty tiles keep one expert's
     E, N, K = 64, 1408, 2048

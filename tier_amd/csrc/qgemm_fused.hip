@@ -74,7 +74,7 @@ constexpr int QNBR = 4;  // decoded B stages in the LDS ring
 // weight W[g]; its tiles are workgroups [tile0[g], tile0[g+1]).
 constexpr int QG = 64;
 struct QArgs {
-  const uint16_t* X;  // parts at X, X + xs, X + 2 xs (hi, mid, lo), rows of K halfs
+  const uint16_t* X;  // parts at X, X + xs, X + 2 xs (hi, mid, lo; F32: hi, lo), rows of K halfs
   size_t xs;
   size_t xt;          // > 0: the planes are K-tiled (ktile_index) over xt rows
   float* Y;
@@ -89,6 +89,10 @@ struct QArgs {
   int row0[QG];
   int rows[QG];
   const uint8_t* W[QG];
+  // F32 (one group): the exponents of x's rows and of the weight's rows (x3s_exp); Y
+  // takes acc * 2^-(xexp[m] + wexp[n])
+  const int32_t* xexp;
+  const int32_t* wexp;
 };
 
 // Byte of 16-byte chunk `chunk` (of 4) of B-tile row `row` (64 bytes, 32 halfs of K):
@@ -161,6 +165,32 @@ __device__ __forceinline__ void pack4(float f0, float f1, float f2, float f3, ui
   hi = __builtin_bit_cast(uint32_t, p1);
 }
 
+// Where a producer lane's decoded values go.  x3-ref: fp16 of q_val (RNE) into o.
+// F32 (the fp32-dequant semantics of tiermm_qgemm's TIERMM_MODE_F32): v = q_val * 2^e of
+// its row, split as x3s_split splits the fp32 dequant -- hi = fp16(v) into o, lo =
+// fp16(v - hi) into ol.
+template <bool F32>
+struct Emit {
+  uint32_t o[8], ol[8];
+  float sc;  // 2^e of the row (F32)
+  __device__ __forceinline__ void put(int k, float f0, float f1, float f2, float f3) {
+    if constexpr (!F32) {
+      pack4(f0, f1, f2, f3, o[2 * k], o[2 * k + 1]);
+    } else {
+      float v[4] = {f0 * sc, f1 * sc, f2 * sc, f3 * sc};
+      asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]));
+      const h2v h0 = {(_Float16)v[0], (_Float16)v[1]}, h1 = {(_Float16)v[2], (_Float16)v[3]};
+      float r[4] = {v[0] - (float)h0[0], v[1] - (float)h0[1], v[2] - (float)h1[0], v[3] - (float)h1[1]};
+      asm volatile("" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]));
+      const h2v l0 = {(_Float16)r[0], (_Float16)r[1]}, l1 = {(_Float16)r[2], (_Float16)r[3]};
+      o[2 * k] = __builtin_bit_cast(uint32_t, h0);
+      o[2 * k + 1] = __builtin_bit_cast(uint32_t, h1);
+      ol[2 * k] = __builtin_bit_cast(uint32_t, l0);
+      ol[2 * k + 1] = __builtin_bit_cast(uint32_t, l1);
+    }
+  }
+};
+
 // 16 bytes at a 2-byte aligned address s, as five dwords from s rounded down to a
 // multiple of 4.  Each dword holds a byte of [s, s + 16) (the fifth repeats the fourth
 // when s is 4-aligned), so no load reaches past the bytes the weight holds.
@@ -202,7 +232,8 @@ struct Unit<QT_Q8_0> {
         q[i].issue(b + 2 + 16 * (h0 + i));
       }
     }
-    __device__ __forceinline__ void decode(const uint8_t* row, int k0, int t, int i, int h, uint32_t o[8]) const {
+    template <class E>
+    __device__ __forceinline__ void decode(const uint8_t* row, int k0, int t, int i, int h, E& o) const {
       const uint8_t* b = row + (size_t)k0 * 34;
       const uint32_t sb = sh_of(b);  // the q bytes at b + 2 + 16h sit at bit offset sb ^ 16
       const float dv = h2f((d[i] >> sb) & 0xffffu);
@@ -213,7 +244,7 @@ struct Unit<QT_Q8_0> {
         float f[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) f[e] = dv * (float)(int8_t)(uint8_t)(w[k] >> (8 * e));
-        pack4(f[0], f[1], f[2], f[3], o[2 * k], o[2 * k + 1]);
+        o.put(k, f[0], f[1], f[2], f[3]);
       }
     }
   };
@@ -235,7 +266,8 @@ struct Unit<QT_Q5_0> {
       a = ld16(f);
       b = ld8(f + 16);
     }
-    __device__ __forceinline__ void decode(const uint8_t* row, int k0, int, int, int h, uint32_t o[8]) const {
+    template <class E>
+    __device__ __forceinline__ void decode(const uint8_t* row, int k0, int, int, int h, E& o) const {
       const uint32_t sh = sh_of(row + (size_t)k0 * 22);
       // the block as if 4-aligned: S[j] = bytes 4j .. 4j + 3
       const uint32_t S0 = abit(a[1], a[0], sh), S1 = abit(a[2], a[1], sh), S2 = abit(a[3], a[2], sh),
@@ -251,7 +283,7 @@ struct Unit<QT_Q5_0> {
         float f[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) f[e] = dv * ((float)((v >> (8 * e)) & 0xffu) - 16.f);
-        pack4(f[0], f[1], f[2], f[3], o[2 * k], o[2 * k + 1]);
+        o.put(k, f[0], f[1], f[2], f[3]);
       }
     }
   };
@@ -276,7 +308,8 @@ struct Unit<QT_Q5_K> {
         qs[i] = ld16(b + 48 + 32 * ((k0 & 7) >> 1) + 16 * (h0 + i));
       }
     }
-    __device__ __forceinline__ void decode(const uint8_t*, int k0, int t, int i, int, uint32_t o[8]) const {
+    template <class E>
+    __device__ __forceinline__ void decode(const uint8_t*, int k0, int t, int i, int, E& o) const {
       const int s = (k0 & 7) + t;
       int sc, mn;
       kq_scale_min(s, hd[1], hd[2], hd[3], sc, mn);
@@ -288,7 +321,7 @@ struct Unit<QT_Q5_K> {
         float f[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) f[e] = fmaf(dsc, (float)((v >> (8 * e)) & 0xffu), -dm);
-        pack4(f[0], f[1], f[2], f[3], o[2 * k], o[2 * k + 1]);
+        o.put(k, f[0], f[1], f[2], f[3]);
       }
     }
   };
@@ -321,7 +354,8 @@ struct Unit<QT_Q6_K> {
       sw = ld16(f);
       se = ld4(f + 16);
     }
-    __device__ __forceinline__ void decode(const uint8_t* row, int k0, int t, int i, int h, uint32_t o[8]) const {
+    template <class E>
+    __device__ __forceinline__ void decode(const uint8_t* row, int k0, int t, int i, int h, E& o) const {
       const uint8_t* b = row + (size_t)(k0 >> 3) * 210;
       const uint32_t sh = sh_of(b);  // every region of the super-block shares it
       const bool a = (k0 & 4) != 0;
@@ -340,7 +374,7 @@ struct Unit<QT_Q6_K> {
         float f[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) f[e] = ds * ((float)((v >> (8 * e)) & 0xffu) - 32.f);
-        pack4(f[0], f[1], f[2], f[3], o[2 * k], o[2 * k + 1]);
+        o.put(k, f[0], f[1], f[2], f[3]);
       }
     }
   };
@@ -354,7 +388,7 @@ struct Unit<QT_Q6_K> {
 // writes the pair q, q + 1 once stage q + 1 - NBR is read).  That stage is
 // below q, its ready published by every producer, so each wait ends; a consumer
 // waits only for its own loads and for ready.
-template <int QT, int BN, int KS, bool CH>
+template <int QT, int BN, int KS, bool CH, bool F32>
 __global__ __launch_bounds__(512) void qgemm_fused_x3ref(const QArgs p) {
   constexpr int NB = BN / 16;
   // x fragments XR stages ahead: the depth is not what limits (2 and 4 time alike), so the
@@ -363,8 +397,10 @@ __global__ __launch_bounds__(512) void qgemm_fused_x3ref(const QArgs p) {
   constexpr int PR = BN / 4;
   constexpr int LPR = 2 * PR <= 64 ? 2 : 1, HPL = 2 / LPR;  // decode: lanes per row, halves per lane
   constexpr int NL = 1 + HPL;                                // producer loads per sub-block pair
-  constexpr int BPART = BN * 64;
-  constexpr int FLAGOFF = NBR * BPART;
+  constexpr int BPART = BN * 64;                     // one B plane of a stage
+  constexpr int BSLOT = F32 ? 2 * BPART : BPART;      // F32: the hi plane, then the lo plane
+  constexpr int NPART = F32 ? 2 : 3;                  // x planes
+  constexpr int FLAGOFF = NBR * BSLOT;
   static_assert(BN % 16 == 0 && BN <= 256, "tile width");
   static_assert(LPR * PR <= 64, "one decode pass per producer");
   static_assert(NBR <= FL && NBR >= 3 && NL * DP <= 63, "ring depths");
@@ -405,6 +441,8 @@ __global__ __launch_bounds__(512) void qgemm_fused_x3ref(const QArgs p) {
     const int dr = min(lane / LPR, PR - 1), h0 = (lane % LPR) * HPL;
     const int r = pw * PR + dr;
     const uint8_t* rowp = Wg + (size_t)min(n0 + r, p.N - 1) * p.rb;
+    Emit<F32> em;
+    em.sc = F32 ? ldexpf(1.f, p.wexp[min(n0 + r, p.N - 1)]) : 1.f;
     const int nu = nk / U;  // units of this split
     R reg[DPU];
     // unit j into register slot u (j >= nu: unit nu - 1 again)
@@ -426,13 +464,18 @@ __global__ __launch_bounds__(512) void qgemm_fused_x3ref(const QArgs p) {
             const int q = U * j + t;
             if (q >= NBR) poll4(done + 4 * ((q - NBR) % FL), q - NBR);  // slot q % NBR read by all
             if (act) {
-              uint8_t* bt = lds + (q % NBR) * BPART;
+              uint8_t* bt = lds + (q % NBR) * BSLOT;
 #pragma unroll
               for (int i = 0; i < HPL; ++i) {
-                uint32_t o[8];
-                reg[u].decode(rowp, k0, t, i, h0 + i, o);
+                reg[u].decode(rowp, k0, t, i, h0 + i, em);
+                const uint32_t* o = em.o;
                 *(u32x4*)(bt + swz(r, 2 * (h0 + i))) = u32x4{o[0], o[1], o[2], o[3]};
                 *(u32x4*)(bt + swz(r, 2 * (h0 + i) + 1)) = u32x4{o[4], o[5], o[6], o[7]};
+                if constexpr (F32) {
+                  const uint32_t* ol = em.ol;
+                  *(u32x4*)(bt + BPART + swz(r, 2 * (h0 + i))) = u32x4{ol[0], ol[1], ol[2], ol[3]};
+                  *(u32x4*)(bt + BPART + swz(r, 2 * (h0 + i) + 1)) = u32x4{ol[4], ol[5], ol[6], ol[7]};
+                }
               }
             }
             if (lane == 0) lds_rel(&ready[4 * (q % FL) + pw], q);
@@ -454,6 +497,8 @@ __global__ __launch_bounds__(512) void qgemm_fused_x3ref(const QArgs p) {
     const int dr = min(lane / LPR, PR - 1), h0 = (lane % LPR) * HPL;
     const int r = pw * PR + dr;
     const uint8_t* rowp = Wg + (size_t)min(n0 + r, p.N - 1) * p.rb;
+    Emit<F32> em;
+    em.sc = F32 ? ldexpf(1.f, p.wexp[min(n0 + r, p.N - 1)]) : 1.f;
     const int np = nk / 2;  // pairs of this split (a multiple of 4)
     u32x4 Hr[DP], Qr[DP][HPL];
     // pair j into register slot u (j >= np: pair np - 1 again, so every pair issues NL loads
@@ -482,10 +527,9 @@ __global__ __launch_bounds__(512) void qgemm_fused_x3ref(const QArgs p) {
             int sc, mn;
             kq_scale_min(((kq0 + q) & 7) + t, H[1], H[2], H[3], sc, mn);
             const float dsc = d * (float)sc, dm = dmin * (float)mn;
-            uint8_t* bt = lds + ((q + t) % NBR) * BPART;
+            uint8_t* bt = lds + ((q + t) % NBR) * BSLOT;
 #pragma unroll
             for (int i = 0; i < HPL; ++i) {
-              uint32_t o[8];
 #pragma unroll
               for (int w = 0; w < 4; ++w) {
                 // elements 4w..4w+3 of the half, one per byte (the empty asm keeps the
@@ -497,13 +541,16 @@ __global__ __launch_bounds__(512) void qgemm_fused_x3ref(const QArgs p) {
                 float f[4];
 #pragma unroll
                 for (int b = 0; b < 4; ++b) f[b] = fmaf(dsc, (float)((v >> (8 * b)) & 0xffu), -dm);
-                asm volatile("" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]));
-                const h2v p0 = {(_Float16)f[0], (_Float16)f[1]}, p1 = {(_Float16)f[2], (_Float16)f[3]};
-                o[2 * w] = __builtin_bit_cast(uint32_t, p0);
-                o[2 * w + 1] = __builtin_bit_cast(uint32_t, p1);
+                em.put(w, f[0], f[1], f[2], f[3]);
               }
+              const uint32_t* o = em.o;
               *(u32x4*)(bt + swz(r, 2 * (h0 + i))) = u32x4{o[0], o[1], o[2], o[3]};
               *(u32x4*)(bt + swz(r, 2 * (h0 + i) + 1)) = u32x4{o[4], o[5], o[6], o[7]};
+              if constexpr (F32) {
+                const uint32_t* ol = em.ol;
+                *(u32x4*)(bt + BPART + swz(r, 2 * (h0 + i))) = u32x4{ol[0], ol[1], ol[2], ol[3]};
+                *(u32x4*)(bt + BPART + swz(r, 2 * (h0 + i) + 1)) = u32x4{ol[4], ol[5], ol[6], ol[7]};
+              }
             }
           }
         }
@@ -531,21 +578,21 @@ __global__ __launch_bounds__(512) void qgemm_fused_x3ref(const QArgs p) {
   // A fragment (part, i): row c*32 + 16i + fr of the tile, halfs 8fc.. of stage q
   // K-tiled planes: K step qq of row r at (qq * xt + r) * 32, so a fragment's 16
   // rows are one contiguous kilobyte; row-major: row r at r * K + qq * 32
-  const uint16_t* xa[3][2];
+  const uint16_t* xa[NPART][2];
   const size_t kstep = p.xt ? p.xt * QBK : (size_t)QBK;
 #pragma unroll
-  for (int part = 0; part < 3; ++part)
+  for (int part = 0; part < NPART; ++part)
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const size_t r = (size_t)min(m0 + c * 32 + i * 16 + fr, M - 1);
       xa[part][i] = p.xt ? p.X + part * p.xs + ((size_t)p.row0[grp] + r) * QBK + 8 * fc
                          : Xg + part * p.xs + r * p.K + 8 * fc;
     }
-  u32x4 A[XR][3][2];
-  auto loadA = [&](int q, u32x4 (&dst)[3][2]) __attribute__((always_inline)) {
-    const int qq = kq0 + min(q, nk - 1);  // past the end: a re-read, so every stage issues 6 loads
+  u32x4 A[XR][NPART][2];
+  auto loadA = [&](int q, u32x4 (&dst)[NPART][2]) __attribute__((always_inline)) {
+    const int qq = kq0 + min(q, nk - 1);  // past the end: a re-read, so every stage issues 2 NPART loads
 #pragma unroll
-    for (int part = 0; part < 3; ++part)
+    for (int part = 0; part < NPART; ++part)
 #pragma unroll
       for (int i = 0; i < 2; ++i) dst[part][i] = ld16(xa[part][i] + (size_t)qq * kstep);
   };
@@ -560,7 +607,21 @@ __global__ __launch_bounds__(512) void qgemm_fused_x3ref(const QArgs p) {
   // of a 16x16 block): into Y, Y = acc + beta Y, or split kz's partial sums.  With
   // accumulation chunks (kcs) it runs at the end of each chunk, which adds the
   // chunk's sum into Y (beta = 1 after the first) and starts the next from zero.
+  // F32: acc * 2^-(xexp[row] + wexp[col]), the exponents read once per store
+  auto scaled = [&](float v, int ea, int eb) __attribute__((always_inline)) {
+    return F32 ? ldexpf(v, -(ea + eb)) : v;
+  };
   auto store = [&](float beta) __attribute__((always_inline)) {
+    int ea[2][4] = {}, eb[NB] = {};
+    if constexpr (F32) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          ea[i][r] = p.xexp[min(m0 + c * 32 + i * 16 + 4 * (lane >> 4) + r, M - 1)];
+#pragma unroll
+      for (int j = 0; j < NB; ++j) eb[j] = p.wexp[min(n0 + j * 16 + (lane & 15), p.N - 1)];
+    }
     // A consumer whose 32 rows and the tile's BN columns all exist (every tile but the
     // last of a row or column of tiles) stores without per-element tests: one row
     // pointer per register row, the 16-column blocks at immediate offsets from it.
@@ -574,10 +635,10 @@ __global__ __launch_bounds__(512) void qgemm_fused_x3ref(const QArgs p) {
           float* rp = KS == 1 ? Yg + row * p.ldy + cb : p.P + (size_t)kz * p.ps + row * p.N + cb;
           if (KS == 1 && beta != 0.f) {
 #pragma unroll
-            for (int j = 0; j < NB; ++j) rp[16 * j] = fmaf(beta, rp[16 * j], acc[i][j][r]);
+            for (int j = 0; j < NB; ++j) rp[16 * j] = fmaf(beta, rp[16 * j], scaled(acc[i][j][r], ea[i][r], eb[j]));
           } else {
 #pragma unroll
-            for (int j = 0; j < NB; ++j) rp[16 * j] = acc[i][j][r];
+            for (int j = 0; j < NB; ++j) rp[16 * j] = scaled(acc[i][j][r], ea[i][r], eb[j]);
           }
         }
       return;
@@ -594,11 +655,11 @@ __global__ __launch_bounds__(512) void qgemm_fused_x3ref(const QArgs p) {
           if (row >= M) continue;
           if constexpr (KS == 1) {
             float* cp = Yg + (size_t)row * p.ldy + col;
-            float v = acc[i][j][r];
+            float v = scaled(acc[i][j][r], ea[i][r], eb[j]);
             if (beta != 0.f) v = fmaf(beta, *cp, v);
             *cp = v;
-          } else {
-            p.P[(size_t)kz * p.ps + (size_t)row * p.N + col] = acc[i][j][r];  // split K: one group
+          } else {  // split K: one group; the reduce adds the scaled partials
+            p.P[(size_t)kz * p.ps + (size_t)row * p.N + col] = scaled(acc[i][j][r], ea[i][r], eb[j]);
           }
         }
     }
@@ -611,13 +672,18 @@ __global__ __launch_bounds__(512) void qgemm_fused_x3ref(const QArgs p) {
   // released once its fragments are in registers, before its last MFMAs.
   // (At BN = 160, and with accumulation chunks, the second set does not fit in
   // registers: fragments are read when the stage starts.)
-  constexpr bool PIPE = NB <= 8 && !CH;
+  constexpr bool PIPE = NB <= 8 && !CH && !F32;
   static_assert(XR % 2 == 0, "B register sets follow u");
   half8 bf[PIPE ? 2 : 1][NB];
+  half8 bl[F32 ? NB : 1];  // F32: the lo plane of the stage
   auto readB = [&](int q, half8 (&dst)[NB]) __attribute__((always_inline)) {
-    const uint8_t* bs = lds + (q % NBR) * BPART;
+    const uint8_t* bs = lds + (q % NBR) * BSLOT;
 #pragma unroll
     for (int j = 0; j < NB; ++j) dst[j] = *(const half8*)(bs + j * 1024 + fo);
+    if constexpr (F32) {
+#pragma unroll
+      for (int j = 0; j < NB; ++j) bl[j] = *(const half8*)(bs + BPART + j * 1024 + fo);
+    }
   };
   if constexpr (PIPE) {
     poll4(ready, 0);
@@ -628,7 +694,7 @@ __global__ __launch_bounds__(512) void qgemm_fused_x3ref(const QArgs p) {
     for (int u = 0; u < XR; ++u) {
       const int q = q0 + u;
       loadA(q + XR - 1, A[(u + XR - 1) % XR]);
-      __builtin_amdgcn_s_waitcnt(WAITVM(6 * (XR - 1)));  // stage q's fragments are in registers
+      __builtin_amdgcn_s_waitcnt(WAITVM(2 * NPART * (XR - 1)));  // stage q's fragments are in registers
       if (q < nk) {
         const bool more = PIPE && q + 1 < nk;
         const int* fn = ready + 4 * ((q + 1) % FL);
@@ -639,15 +705,19 @@ __global__ __launch_bounds__(512) void qgemm_fused_x3ref(const QArgs p) {
           readB(q, bf[0]);
         }
         const int cur = PIPE ? (u & 1) : 0;  // u is a constant after unrolling
-        // parts lo, mid, hi (tier.cpp:940) into one fp32 accumulator
+        // parts lo, mid, hi (tier.cpp:940) into one fp32 accumulator; F32: x lo * W hi,
+        // x hi * W lo, x hi * W hi (the x3-2x2 products, smallest first)
 #pragma unroll
         for (int part = 2; part >= 0; --part) {
 #pragma unroll
           for (int j = 0; j < NB; ++j)
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, A[u][part][i]),
-                                                                 bf[cur][j], acc[i][j], 0, 0, 0);
+            for (int i = 0; i < 2; ++i) {
+              const int ap = F32 ? (part == 2 ? 1 : 0) : part;
+              const half8 b = F32 && part == 1 ? bl[j] : bf[cur][j];
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, A[u][ap][i]), b, acc[i][j],
+                                                                 0, 0, 0);
+            }
           if (part == 2) {
             if (lane == 0) lds_rel(&done[4 * (q % FL) + c], q);  // stage q's B tile is in registers
             if (more) {
@@ -705,14 +775,14 @@ __global__ __launch_bounds__(256) void qgemm_splitk_reduce4(const float* __restr
   *y = v;
 }
 
-template <int QT, int BN, int KS, bool CH = false>
+template <int QT, int BN, int KS, bool CH = false, bool F32 = false>
 int launch_q(const QArgs& a, hipStream_t s, const char* who) {
-  constexpr size_t lds = QNBR * (size_t)BN * 64 + 2 * 4 * 4 * 4;
+  constexpr size_t lds = QNBR * (size_t)BN * 64 * (F32 ? 2 : 1) + 2 * 4 * 4 * 4;
   static_assert(lds <= 160 * 1024, "LDS budget");
   static std::atomic<uint64_t> attr{0};
-  int st = lds_attr_once(attr, (const void*)qgemm_fused_x3ref<QT, BN, KS, CH>, (int)lds, who);
+  int st = lds_attr_once(attr, (const void*)qgemm_fused_x3ref<QT, BN, KS, CH, F32>, (int)lds, who);
   if (st) return st;
-  qgemm_fused_x3ref<QT, BN, KS, CH><<<(unsigned)a.tile0[a.ngroups] * KS, 512, lds, s>>>(a);
+  qgemm_fused_x3ref<QT, BN, KS, CH, F32><<<(unsigned)a.tile0[a.ngroups] * KS, 512, lds, s>>>(a);
   TM_LAUNCH_CHECK(who);
   return TIERMM_OK;
 }
@@ -743,8 +813,27 @@ int launch_q_bn(int bn, const QArgs& a, hipStream_t s, const char* who) {
   }
 }
 
+// The F32 (fp32-dequant) kernels: BN 160, 128 or 64 (wider tiles do not keep both B
+// planes' fragments in registers) and KS 1, 2 or 4; no accumulation chunks (their
+// in-loop store spills at these widths), so K up to 4 x 4096.
+template <int QT, int KS>
+int launch_q_f32_bn(int bn, const QArgs& a, hipStream_t s, const char* who) {
+  switch (bn) {
+    case 160: return launch_q<QT, 160, KS, false, true>(a, s, who);
+    case 128: return launch_q<QT, 128, KS, false, true>(a, s, who);
+    default: return launch_q<QT, 64, KS, false, true>(a, s, who);
+  }
+}
+
 template <int QT>
 int launch_q_plan(int bn, int ks, const QArgs& a, hipStream_t s, const char* who) {
+  if (a.xexp) {  // F32
+    switch (ks) {
+      case 4: return launch_q_f32_bn<QT, 4>(bn, a, s, who);
+      case 2: return launch_q_f32_bn<QT, 2>(bn, a, s, who);
+      default: return launch_q_f32_bn<QT, 1>(bn, a, s, who);
+    }
+  }
   if (a.kcs) {  // accumulation chunks: KS = 1, BN = 160 or 128 (wider ones spill with the chunk store)
     if (bn == 160) return launch_q<QT, 160, 1, true>(a, s, who);
     return launch_q<QT, 128, 1, true>(a, s, who);
@@ -800,7 +889,7 @@ int fused_unit(int qt) {
   }
 }
 
-bool plan_ok(int qt, int bn, int ks, int kc, int K, size_t rows_total, int N, bool split) {
+bool plan_ok(int qt, int bn, int ks, int kc, int K, size_t rows_total, int N, bool split, bool f32) {
   const int unit = fused_unit(qt);
   if (!unit || K % QBK || (K / QBK) % (unit * ks * kc)) return false;
   if (ks > 1 && (!split || kc > 1 || (size_t)ks * rows_total * N * 4 > kMaxPartials)) return false;
@@ -808,6 +897,7 @@ bool plan_ok(int qt, int bn, int ks, int kc, int K, size_t rows_total, int N, bo
   if ((ks != 1 && ks != 2 && ks != 4) || kc < 1 || kc > 8) return false;
   if (kc > 1 && ((K / QBK / kc) % 4 || ks > 1 || (bn != 160 && bn != 128)))
     return false;  // chunks end where the consumer's unrolled steps do; the chunked widths
+  if (f32) return kc == 1 && (bn == 160 || bn == 128 || bn == 64);  // the F32 kernels' plans
   if (qt == QT_Q4_K) {
     for (int b : kBns)
       if (b == bn) return true;
@@ -818,12 +908,12 @@ bool plan_ok(int qt, int bn, int ks, int kc, int K, size_t rows_total, int N, bo
 
 // (BN, KS, KC) for the fused kernel.  TIERMM_QGEMM_TILE="BN,KS[,KC]" overrides the model
 // when the plan is valid for the shape (tests and tuning).
-QPlan q_plan(int qt, const int* rows, int n, int N, int K, int cus, bool split) {
+QPlan q_plan(int qt, const int* rows, int n, int N, int K, int cus, bool split, bool f32 = false) {
   size_t rows_total = 0;
   for (int g = 0; g < n; ++g) rows_total += (size_t)rows[g];
   if (const char* e = getenv("TIERMM_QGEMM_TILE")) {
     int bn = 0, ks = 0, kc = 1;
-    if (sscanf(e, "%d,%d,%d", &bn, &ks, &kc) >= 2 && plan_ok(qt, bn, ks, kc, K, rows_total, N, split))
+    if (sscanf(e, "%d,%d,%d", &bn, &ks, &kc) >= 2 && plan_ok(qt, bn, ks, kc, K, rows_total, N, split, f32))
       return {bn, ks, kc};
   }
   const int nk = K / QBK;
@@ -833,7 +923,7 @@ QPlan q_plan(int qt, const int* rows, int n, int N, int K, int cus, bool split) 
   for (int i = 0; i < kNbn; ++i)
     for (int ks = 1; ks <= 4; ks *= 2)
       for (int kc : {1, need}) {
-        if (!plan_ok(qt, kBns[i], ks, kc, K, rows_total, N, split)) continue;
+        if (!plan_ok(qt, kBns[i], ks, kc, K, rows_total, N, split, f32)) continue;
         const long wg = q_tiles(rows, n, N, kBns[i]) * ks;
         double t = (double)((wg + cus - 1) / cus) * (kRound + kUnit[i] * kBns[i] * nk / ks);
         if (kc > 1) t *= kChunkCost;
@@ -857,32 +947,39 @@ int cus_or_default() {
 }  // namespace
 
 // Bytes of split-K partial sums the fused GEMM of one M x N x K problem needs.
-size_t qgemm_fused_partials_bytes(int qtype, int M, int N, int K) {
-  const QPlan pl = q_plan(qtype, &M, 1, N, K, cus_or_default(), true);
+size_t qgemm_fused_partials_bytes(int qtype, int M, int N, int K, bool f32) {
+  const QPlan pl = q_plan(qtype, &M, 1, N, K, cus_or_default(), true, f32);
   return pl.ks > 1 ? (size_t)pl.ks * M * N * sizeof(float) : 0;
 }
 
 // Whether the fused kernel takes n groups of these row counts of a qtype weight: the
 // type is decoded in the kernel, some (BN, KS) fits, KS > 1 only when `split` (one
 // group with a partial-sum workspace), and every split short enough for one fp32
-// accumulator (acc_chunks).
-bool qgemm_fusable(int qtype, const int* rows, int n, int N, int K, bool split) {
-  return q_plan(qtype, rows, n, N, K, cus_or_default(), split && n == 1).bn != 0;
+// accumulator (acc_chunks).  f32: the F32 kernels (one group).
+bool qgemm_fusable(int qtype, const int* rows, int n, int N, int K, bool split, bool f32) {
+  if (f32 && n != 1) return false;
+  return q_plan(qtype, rows, n, N, K, cus_or_default(), split && n == 1, f32).bn != 0;
 }
 
 // Fused x3-ref GEMM over n groups (rows[g] rows of x from row0[g], qtype weight W[g]);
 // the x planes hold every group's rows (plane stride xs).  A single group may split K,
-// with `partials` (qgemm_fused_partials_bytes) holding the partial sums.
+// with `partials` (qgemm_fused_partials_bytes) holding the partial sums.  xexp and
+// wexp given: the F32 kernels (one group, two row-major x planes).
 int qgemm_fused_groups(const void* const* W, int qtype, const int* row0, const int* rows, int n, size_t rb,
                        const uint16_t* xparts, size_t xs, size_t xt, float* Y, int ldy, int N, int K, float beta,
-                       int cus, hipStream_t s, const char* who, float* partials) {
-  const QPlan pl = q_plan(qtype, rows, n, N, K, cus, n == 1 && partials != nullptr);
+                       int cus, hipStream_t s, const char* who, float* partials, const int32_t* xexp,
+                       const int32_t* wexp) {
+  const bool f32 = xexp != nullptr;
+  if (f32 && (n != 1 || !wexp || xt))
+    return set_error(TIERMM_EINVAL, "%s: the fp32 kernels take one group of row-major planes", who);
+  const QPlan pl = q_plan(qtype, rows, n, N, K, cus, n == 1 && partials != nullptr, f32);
   if (pl.bn == 0) return set_error(TIERMM_UNSUPPORTED, "%s: no fused plan for type %d N=%d K=%d", who, qtype, N, K);
   for (int g0 = 0; g0 < n; g0 += QG) {
     QArgs a{};
     a.X = xparts; a.xs = xs; a.xt = xt; a.Y = Y; a.rb = rb; a.ldy = ldy; a.N = N; a.K = K; a.beta = beta;
     a.kcs = pl.kc > 1 ? K / QBK / pl.kc : 0;
     a.P = partials; a.ps = n == 1 ? (size_t)rows[0] * N : 0;
+    a.xexp = xexp; a.wexp = wexp;
     a.ngroups = 0;
     a.tile0[0] = 0;
     for (int g = g0; g < n && g < g0 + QG; ++g) {
@@ -921,9 +1018,48 @@ int qgemm_fused_groups(const void* const* W, int qtype, const int* row0, const i
 }
 
 int qgemm_fused(const void* W, int qtype, size_t rb, const uint16_t* xparts, size_t xs, size_t xt, float* Y, int ldy,
-                int M, int N, int K, float beta, int cus, hipStream_t s, const char* who, float* partials) {
+                int M, int N, int K, float beta, int cus, hipStream_t s, const char* who, float* partials,
+                const int32_t* xexp, const int32_t* wexp) {
   const int row0 = 0;
-  return qgemm_fused_groups(&W, qtype, &row0, &M, 1, rb, xparts, xs, xt, Y, ldy, N, K, beta, cus, s, who, partials);
+  return qgemm_fused_groups(&W, qtype, &row0, &M, 1, rb, xparts, xs, xt, Y, ldy, N, K, beta, cus, s, who, partials,
+                            xexp, wexp);
+}
+
+// wexp[n] = x3s_exp(max |q_val| over row n): one wave a row, 8 columns a lane and step
+// (K a multiple of 32).  The decode is Dec's, the one the fp32 dequant and the fused
+// producers' values agree with.
+template <int QT>
+__global__ __launch_bounds__(256) void qrow_exp_kernel(const uint8_t* __restrict__ W, size_t rb, int N, int K,
+                                                      int32_t* __restrict__ wexp) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const uint8_t* row = W + (size_t)n * rb;
+  float amax = 0.f;
+  for (int c = 8 * lane; c < K; c += 512) {
+    float v[8];
+    Dec<QT>::run(row, c, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+  if (lane == 0) wexp[n] = x3s_exp(amax);
+}
+
+int qrow_exps(const void* W, int qtype, size_t rb, int N, int K, int32_t* wexp, hipStream_t s) {
+  const unsigned grid = (unsigned)((N + 3) / 4);
+  const uint8_t* w = (const uint8_t*)W;
+  switch (qtype) {
+    case QT_Q4_K: qrow_exp_kernel<QT_Q4_K><<<grid, 256, 0, s>>>(w, rb, N, K, wexp); break;
+    case QT_Q5_K: qrow_exp_kernel<QT_Q5_K><<<grid, 256, 0, s>>>(w, rb, N, K, wexp); break;
+    case QT_Q6_K: qrow_exp_kernel<QT_Q6_K><<<grid, 256, 0, s>>>(w, rb, N, K, wexp); break;
+    case QT_Q8_0: qrow_exp_kernel<QT_Q8_0><<<grid, 256, 0, s>>>(w, rb, N, K, wexp); break;
+    case QT_Q5_0: qrow_exp_kernel<QT_Q5_0><<<grid, 256, 0, s>>>(w, rb, N, K, wexp); break;
+    default: return set_error(TIERMM_UNSUPPORTED, "qrow_exps: type %d", qtype);
+  }
+  TM_LAUNCH_CHECK("tiermm_qgemm: weight row exponents");
+  return TIERMM_OK;
 }
 
 }  // namespace tiermm

@@ -61,6 +61,16 @@ __device__ float nonfinite_terms(const uint8_t* row, const float* x, int k0, int
   return s;
 }
 
+// The exponent of a row of the two-part (x3s) split: with amax = m * 2^ex (m in
+// [0.5, 1)), e = 15 - ex puts amax * 2^e in [2^14, 2^15); clamped to [-100, 100], and
+// 0 for an all-zero or non-finite maximum.
+__device__ __forceinline__ int x3s_exp(float amax) {
+  if (!(amax > 0.f) || !isfinite(amax)) return 0;
+  int ex;
+  (void)frexpf(amax, &ex);
+  return min(100, max(-100, 15 - ex));
+}
+
 // Hand-issued vector memory for the kernels that stream through LDS: the
 // compiler's wait insertion cannot follow global->LDS loads (it falls back to
 // waiting for everything before LDS reads), which would serialise the stream.

@@ -31,13 +31,20 @@ int dequant_f16_group(const void* const* W, uint16_t* const* out, int n, int qty
                       size_t nrows, hipStream_t s, bool tiled = false);
 // Fused dequant + x3-ref GEMM (q4_K, q5_K, q6_K, q8_0, q5_0 weights).  xparts: three
 // fp16 planes (stride xs), row-major (xt = 0) or K-tiled over xt rows.
+// F32 (xexp and wexp given, one group): two fp16 planes, hi and lo of x's x3s split
+// (row-major), and the weight decoded to fp32, scaled by 2^wexp of its row and split
+// the same way inside the GEMM (the x3-2x2 products).
 int qgemm_fused(const void* W, int qtype, size_t rb, const uint16_t* xparts, size_t xs, size_t xt, float* Y, int ldy,
-                int M, int N, int K, float beta, int cus, hipStream_t s, const char* who, float* partials);
+                int M, int N, int K, float beta, int cus, hipStream_t s, const char* who, float* partials,
+                const int32_t* xexp = nullptr, const int32_t* wexp = nullptr);
 int qgemm_fused_groups(const void* const* W, int qtype, const int* row0, const int* rows, int n, size_t rb,
                        const uint16_t* xparts, size_t xs, size_t xt, float* Y, int ldy, int N, int K, float beta,
-                       int cus, hipStream_t s, const char* who, float* partials);
-size_t qgemm_fused_partials_bytes(int qtype, int M, int N, int K);
-bool qgemm_fusable(int qtype, const int* rows, int n, int N, int K, bool split);
+                       int cus, hipStream_t s, const char* who, float* partials, const int32_t* xexp = nullptr,
+                       const int32_t* wexp = nullptr);
+size_t qgemm_fused_partials_bytes(int qtype, int M, int N, int K, bool f32 = false);
+bool qgemm_fusable(int qtype, const int* rows, int n, int N, int K, bool split, bool f32 = false);
+// wexp[n] = x3s_exp(max |q_val| of weight row n), rows [0, N) of K columns.
+int qrow_exps(const void* W, int qtype, size_t rb, int N, int K, int32_t* wexp, hipStream_t s);
 int device_cus(int* cus);
 
 namespace {
@@ -128,14 +135,6 @@ __device__ __forceinline__ float block_max_256(float v, float* red) {
   v = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   __syncthreads();
   return v;
-}
-
-// Row exponent e = 14 - floor(log2(amax)) so that amax * 2^e lies in [2^14, 2^15).
-__device__ __forceinline__ int x3s_exp(float amax) {
-  if (!(amax > 0.f) || !isfinite(amax)) return 0;
-  int ex;
-  (void)frexpf(amax, &ex);
-  return min(100, max(-100, 15 - ex));
 }
 
 // One pass over a row held in registers: 4 consecutive elements per thread and
@@ -1272,6 +1271,16 @@ int tiermm_x3_rows_bf16(const uint16_t* W, const float* x, float* y, int M, int 
 }
 
 
+// Weight rows the unfused fp32 path expands at a time: fp32 rows and their two-part
+// split take 8 bytes a weight, kept within kF32ExpandBytes in whole 320-row big tiles
+// (at least one such tile).
+constexpr size_t kF32ExpandBytes = (size_t)256 << 20;
+static int f32_rows(int N, int kp) {
+  const size_t r = kF32ExpandBytes / ((size_t)kp * 8);
+  if (r >= (size_t)N) return N;
+  return std::min(N, std::max(320, (int)(r / 320 * 320)));
+}
+
 // tiermm_qgemm for dense rows (F32 / F16 / BF16) whose length K is not a multiple of
 // the 32-wide K step (every block type is): W and x are copied into the workspace
 // as rows of Kp = roundup(K, 32) with zeros past K, then multiplied as usual.
@@ -1282,47 +1291,54 @@ static int qgemm_padded(const void* W, int qtype, size_t rb, const float* X, flo
   const int kp = pad32(K);
   const size_t nkp = (size_t)N * kp, mkp = (size_t)M * kp;
   const uint8_t* wq = (const uint8_t*)W;
-  auto dense_pad = [&](void* out, bool f16) {
-    const unsigned g = elem_grid(nkp);
+  // rows [n0, n0 + nr) of W into out, as rows of kp
+  auto dense_pad = [&](void* out, bool f16, int n0, int nr) {
+    const unsigned g = elem_grid((size_t)nr * kp);
+    const uint8_t* src = wq + (size_t)n0 * rb;
     if (qtype == TIERMM_F32) {
-      if (f16) dense_pad_kernel<QT_F32, true><<<g, 256, 0, s>>>(wq, rb, out, (size_t)N, K, kp);
-      else dense_pad_kernel<QT_F32, false><<<g, 256, 0, s>>>(wq, rb, out, (size_t)N, K, kp);
+      if (f16) dense_pad_kernel<QT_F32, true><<<g, 256, 0, s>>>(src, rb, out, (size_t)nr, K, kp);
+      else dense_pad_kernel<QT_F32, false><<<g, 256, 0, s>>>(src, rb, out, (size_t)nr, K, kp);
     } else if (qtype == TIERMM_F16) {
-      if (f16) dense_pad_kernel<QT_F16, true><<<g, 256, 0, s>>>(wq, rb, out, (size_t)N, K, kp);
-      else dense_pad_kernel<QT_F16, false><<<g, 256, 0, s>>>(wq, rb, out, (size_t)N, K, kp);
+      if (f16) dense_pad_kernel<QT_F16, true><<<g, 256, 0, s>>>(src, rb, out, (size_t)nr, K, kp);
+      else dense_pad_kernel<QT_F16, false><<<g, 256, 0, s>>>(src, rb, out, (size_t)nr, K, kp);
     } else {
-      if (f16) dense_pad_kernel<QT_BF16, true><<<g, 256, 0, s>>>(wq, rb, out, (size_t)N, K, kp);
-      else dense_pad_kernel<QT_BF16, false><<<g, 256, 0, s>>>(wq, rb, out, (size_t)N, K, kp);
+      if (f16) dense_pad_kernel<QT_BF16, true><<<g, 256, 0, s>>>(src, rb, out, (size_t)nr, K, kp);
+      else dense_pad_kernel<QT_BF16, false><<<g, 256, 0, s>>>(src, rb, out, (size_t)nr, K, kp);
     }
   };
-  if (mode == TIERMM_MODE_F32) {
+  if (mode == TIERMM_MODE_F32) {  // chunks of f32_rows weight rows, as in tiermm_qgemm
+    const int nc = f32_rows(N, kp);
     uint8_t* b = (uint8_t*)w;
-    float* wf = (float*)b;       b += al256(nkp * 4);
-    uint16_t* whi = (uint16_t*)b; b += al256(nkp * 2);
-    uint16_t* wlo = (uint16_t*)b; b += al256(nkp * 2);
-    int32_t* wexp = (int32_t*)b;  b += al256((size_t)N * 4);
+    float* wf = (float*)b;       b += al256((size_t)nc * kp * 4);
+    uint16_t* whi = (uint16_t*)b; b += al256((size_t)nc * kp * 2);
+    uint16_t* wlo = (uint16_t*)b; b += al256((size_t)nc * kp * 2);
+    int32_t* wexp = (int32_t*)b;  b += al256((size_t)nc * 4);
     float* xf = (float*)b;        b += al256(mkp * 4);
     uint16_t* xhi = (uint16_t*)b; b += al256(mkp * 2);
     uint16_t* xlo = (uint16_t*)b; b += al256(mkp * 2);
     int32_t* xexp = (int32_t*)b;
-    dense_pad(wf, false);
-    TM_LAUNCH_CHECK("tiermm_qgemm: padded W");
     pad32_kernel<<<elem_grid(mkp), 256, 0, s>>>(X, (size_t)K, xf, (size_t)M, K, kp);
     TM_LAUNCH_CHECK("tiermm_qgemm: padded x");
-    x3s_split_launch(wf, whi, wlo, wexp, N, kp, s);
-    TM_LAUNCH_CHECK("tiermm_qgemm: split W");
     x3s_split_launch(xf, xhi, xlo, xexp, M, kp, s);
     TM_LAUNCH_CHECK("tiermm_qgemm: split x");
-    X3Args a{};
-    a.A[0] = xhi; a.A[1] = xlo; a.B[0] = whi; a.B[1] = wlo;
-    a.lda = kp; a.ldb = kp; a.C = Y; a.ldc = ldy; a.M = M; a.N = N; a.K = kp;
-    a.aexp = xexp; a.bexp = wexp; a.beta = beta;
-    if (big_tiles(M, N) >= 192) return launch_x3_big<X3_2X2>(a, s, who);
-    return launch_x3<128, 128, X3_2X2>(a, s, who);
+    for (int n0 = 0; n0 < N; n0 += nc) {
+      const int nr = std::min(nc, N - n0);
+      dense_pad(wf, false, n0, nr);
+      TM_LAUNCH_CHECK("tiermm_qgemm: padded W");
+      x3s_split_launch(wf, whi, wlo, wexp, nr, kp, s);
+      TM_LAUNCH_CHECK("tiermm_qgemm: split W");
+      X3Args a{};
+      a.A[0] = xhi; a.A[1] = xlo; a.B[0] = whi; a.B[1] = wlo;
+      a.lda = kp; a.ldb = kp; a.C = Y + n0; a.ldc = ldy; a.M = M; a.N = nr; a.K = kp;
+      a.aexp = xexp; a.bexp = wexp; a.beta = beta;
+      int st = big_tiles(M, nr) >= 192 ? launch_x3_big<X3_2X2>(a, s, who) : launch_x3<128, 128, X3_2X2>(a, s, who);
+      if (st) return st;
+    }
+    return TIERMM_OK;
   }
   uint16_t* w16 = (uint16_t*)w;
   uint16_t* parts = (uint16_t*)((uint8_t*)w + al256(nkp * 2));
-  dense_pad(w16, true);
+  dense_pad(w16, true, 0, N);
   TM_LAUNCH_CHECK("tiermm_qgemm: padded W");
   pad_split3_kernel<false><<<elem_grid(mkp), 256, 0, s>>>(X, (size_t)K, parts, (size_t)M, K, kp);
   TM_LAUNCH_CHECK("tiermm_qgemm: padded split");
@@ -1393,14 +1409,22 @@ int tiermm_sgemm(int opA, int m, int n, int k, const float* A, int lda, const fl
 size_t tiermm_qgemm_ws_bytes(int qtype, int M, int N, int K, int mode) {
   if (K % BK) {  // dense rows of an odd length: W and x padded to rows of Kp
     const size_t kp = (size_t)pad32(K);
-    if (mode == TIERMM_MODE_F32)  // padded fp32 W and x, their two-part splits
-      return al256((size_t)N * kp * 4) + 2 * al256((size_t)N * kp * 2) + al256((size_t)N * 4) +
-             al256((size_t)M * kp * 4) + 2 * al256((size_t)M * kp * 2) + al256((size_t)M * 4);
+    if (mode == TIERMM_MODE_F32) {  // a chunk of padded fp32 W rows, padded fp32 x, their two-part splits
+      const size_t nc = (size_t)f32_rows(N, (int)kp);
+      return al256(nc * kp * 4) + 2 * al256(nc * kp * 2) + al256(nc * 4) + al256((size_t)M * kp * 4) +
+             2 * al256((size_t)M * kp * 2) + al256((size_t)M * 4);
+    }
     return al256((size_t)N * kp * 2) + (size_t)3 * M * kp * sizeof(uint16_t);  // padded W16, x planes
   }
-  if (mode == TIERMM_MODE_F32)  // fp32 W, its two-part split, and x's
-    return al256((size_t)N * K * 4) + 2 * al256((size_t)N * K * 2) + al256((size_t)N * 4) +
-           2 * al256((size_t)M * K * 2) + al256((size_t)M * 4);
+  if (mode == TIERMM_MODE_F32) {
+    if (qgemm_fusable(qtype, &M, 1, N, K, true, true))  // x's two-part split, both exponent rows; split-K partials
+      return 2 * al256((size_t)M * K * 2) + al256((size_t)M * 4) + al256((size_t)N * 4) +
+             qgemm_fused_partials_bytes(qtype, M, N, K, true);
+    // a chunk of fp32 W rows, their two-part split, and x's
+    const size_t nc = (size_t)f32_rows(N, K);
+    return al256(nc * K * 4) + 2 * al256(nc * K * 2) + al256(nc * 4) + 2 * al256((size_t)M * K * 2) +
+           al256((size_t)M * 4);
+  }
   const size_t parts = (size_t)3 * M * K * sizeof(uint16_t);  // x split in three fp16 planes
   if (qgemm_fusable(qtype, &M, 1, N, K, true))
     return al256(parts) + qgemm_fused_partials_bytes(qtype, M, N, K);  // W decoded inside the GEMM; split-K partials
@@ -1424,29 +1448,55 @@ int tiermm_qgemm(const void* W, int qtype, size_t rb, const float* X, float* Y, 
   hipStream_t s = (hipStream_t)stream;
   if (K % BK) return qgemm_padded(W, qtype, rb, X, Y, M, N, K, ldy, mode, beta, w, s, who);
   const size_t mk = (size_t)M * K;
+  if (mode == TIERMM_MODE_F32 && qgemm_fusable(qtype, &M, 1, N, K, true, true)) {
+    // the same semantics with W decoded inside the GEMM: no fp32 or fp16 copy of W
+    // in memory, one pass over W for its row exponents first
+    uint8_t* b = (uint8_t*)w;
+    uint16_t* xhi = (uint16_t*)b;             b += al256(mk * 2);
+    b += al256(mk * 2);                       // xlo, one plane stride after xhi
+    int32_t* xexp = (int32_t*)b;              b += al256((size_t)M * 4);
+    int32_t* wexp = (int32_t*)b;              b += al256((size_t)N * 4);
+    float* partials = (float*)b;
+    const size_t xs = al256(mk * 2) / 2;
+    x3s_split_launch(X, xhi, xhi + xs, xexp, M, K, s);
+    TM_LAUNCH_CHECK("tiermm_qgemm: split x");
+    st = qrow_exps(W, qtype, rb, N, K, wexp, s);
+    if (st) return st;
+    int cus = 0;
+    st = device_cus(&cus);
+    if (st) return st;
+    return qgemm_fused(W, qtype, rb, xhi, xs, 0, Y, ldy, M, N, K, beta, cus, s, who, partials, xexp, wexp);
+  }
   if (mode == TIERMM_MODE_F32) {
     // chat prefill semantics (tier.cpp:2358-2359): fp32 dequant, fp32-accurate
-    // product -- here the two-part split GEMM (relative error ~2^-21 of fp64)
+    // product -- here the two-part split GEMM (relative error ~2^-21 of fp64) over
+    // chunks of f32_rows weight rows, each expanded to fp32 and split in the
+    // workspace (the reference expands a bounded chunk too, tier.cpp:2225-2227)
+    const int nc = f32_rows(N, K);
     uint8_t* b = (uint8_t*)w;
-    float* wf = (float*)b;                    b += al256((size_t)N * K * 4);
-    uint16_t* whi = (uint16_t*)b;             b += al256((size_t)N * K * 2);
-    uint16_t* wlo = (uint16_t*)b;             b += al256((size_t)N * K * 2);
-    int32_t* wexp = (int32_t*)b;              b += al256((size_t)N * 4);
+    float* wf = (float*)b;                    b += al256((size_t)nc * K * 4);
+    uint16_t* whi = (uint16_t*)b;             b += al256((size_t)nc * K * 2);
+    uint16_t* wlo = (uint16_t*)b;             b += al256((size_t)nc * K * 2);
+    int32_t* wexp = (int32_t*)b;              b += al256((size_t)nc * 4);
     uint16_t* xhi = (uint16_t*)b;             b += al256(mk * 2);
     uint16_t* xlo = (uint16_t*)b;             b += al256(mk * 2);
     int32_t* xexp = (int32_t*)b;
-    st = tiermm_dequant(W, qtype, rb, K, 0, (size_t)N, wf, TIERMM_OUT_F32, stream);
-    if (st) return st;
-    x3s_split_launch(wf, whi, wlo, wexp, N, K, s);
-    TM_LAUNCH_CHECK("tiermm_qgemm: split W");
     x3s_split_launch(X, xhi, xlo, xexp, M, K, s);
     TM_LAUNCH_CHECK("tiermm_qgemm: split x");
-    X3Args a{};
-    a.A[0] = xhi; a.A[1] = xlo; a.B[0] = whi; a.B[1] = wlo;
-    a.lda = K; a.ldb = K; a.C = Y; a.ldc = ldy; a.M = M; a.N = N; a.K = K;
-    a.aexp = xexp; a.bexp = wexp; a.beta = beta;
-    if (big_tiles(M, N) >= 192) return launch_x3_big<X3_2X2>(a, s, who);
-    return launch_x3<128, 128, X3_2X2>(a, s, who);
+    for (int n0 = 0; n0 < N; n0 += nc) {
+      const int nr = std::min(nc, N - n0);
+      st = tiermm_dequant(W, qtype, rb, K, (size_t)n0, (size_t)nr, wf, TIERMM_OUT_F32, stream);
+      if (st) return st;
+      x3s_split_launch(wf, whi, wlo, wexp, nr, K, s);
+      TM_LAUNCH_CHECK("tiermm_qgemm: split W");
+      X3Args a{};
+      a.A[0] = xhi; a.A[1] = xlo; a.B[0] = whi; a.B[1] = wlo;
+      a.lda = K; a.ldb = K; a.C = Y + n0; a.ldc = ldy; a.M = M; a.N = nr; a.K = K;
+      a.aexp = xexp; a.bexp = wexp; a.beta = beta;
+      st = big_tiles(M, nr) >= 192 ? launch_x3_big<X3_2X2>(a, s, who) : launch_x3<128, 128, X3_2X2>(a, s, who);
+      if (st) return st;
+    }
+    return TIERMM_OK;
   }
   // The types the fused kernel decodes, at every M: W is decoded inside the GEMM (at
   // M = 4096 the wide-tile plans beat fp16 staging + the big-tile GEMM by 5-25 %).
