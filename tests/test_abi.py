@@ -154,8 +154,8 @@ def test_workspace_sizes():
     assert tier_amd.qgemm_ws_bytes(tier_amd.Q5_K, 16384, 5120, 14336) == 3 * 16384 * 14336 * 2
     # other types stage fp16 W in the workspace as well
     assert tier_amd.qgemm_ws_bytes(tier_amd.Q4_0, 512, 5120, 5120) == 5120 * 5120 * 2 + 3 * 512 * 5120 * 2
-    # the fp32 semantics: the fused types keep no copy of W (x's hi and lo planes, both
-    # exponent rows, and at K = 14336 four K splits of partial sums); the others expand
+    # the fp32 semantics: the fused types keep no copy of W (x's hi and lo planes, the
+    # row exponents of x and W, and at K = 14336 four K splits of partial sums); the others expand
     # W in chunks of rows within 256 MiB (1600 rows of K = 20480: 1638 rounded down to
     # whole 320-row tiles)
     F32 = tier_amd.MODE_F32

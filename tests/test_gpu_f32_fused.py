@@ -73,7 +73,7 @@ def test_f32_config4(gpu, M, name, t, N, K):
     """The chat prefill product at its chunk size (M = 256, tier.cpp:2538) and at the
     config's 4096-token batch: decoded inside the GEMM (no fp32 W in the workspace),
     fp64-checked on every row at M = 256 and on 64 sampled rows at M = 4096."""
-    # x's planes, the exponents and at most four K splits' partial sums: no copy of W
+    # x's planes, both exponent rows and at most four K splits' partial sums: no copy of W
     assert tier_amd.qgemm_ws_bytes(t, M, N, K, tier_amd.MODE_F32) <= fused_ws(M, N, K, 4)
     blocks = quantized_weight(t, N, K, seed=N + K + t)
     x = activations(M, K, seed=M + t)

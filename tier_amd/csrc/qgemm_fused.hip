@@ -89,8 +89,8 @@ struct QArgs {
   int row0[QG];
   int rows[QG];
   const uint8_t* W[QG];
-  // F32 (one group): the exponents of x's rows and of the weight's rows (x3s_exp); Y
-  // takes acc * 2^-(xexp[m] + wexp[n])
+  // F32 (one group): the exponents of x's rows (x3s_exp) and of the weight's rows
+  // (qrow_exps); Y takes acc * 2^-(xexp[m] + wexp[n])
   const int32_t* xexp;
   const int32_t* wexp;
 };
@@ -165,6 +165,45 @@ __device__ __forceinline__ void pack4(float f0, float f1, float f2, float f3, ui
   hi = __builtin_bit_cast(uint32_t, p1);
 }
 
+// An upper bound of |q_val| over block `blk` of a row (the F32 weight row exponent).
+// q_val is monotone in the block's code and fp32 rounding is monotone, so q_val's own
+// fp32 arithmetic at the extreme codes gives the largest |q_val| those scales allow:
+//   q4_K / q5_K (quant.h:83-87): d*sc*q - dmin*m, q in [0, 15] / [0, 31], per sub-block;
+//   q6_K (quant.h:88-90): (d*sc)*(q - 32), q - 32 in [-32, 31], per 16 elements;
+//   q8_0 (quant.h:68): d*q, q in [-128, 127];  q5_0 (quant.h:66): d*(q - 16), q in [0, 31].
+// The bound is the row's max |q_val| when every block holds its extreme codes, and
+// above it otherwise: the split never overflows fp16 either way.
+template <int QT>
+__device__ __forceinline__ float blk_bound(const uint8_t* row, int blk) {
+  if constexpr (QT == QT_Q4_K || QT == QT_Q5_K) {
+    constexpr float QMAX = QT == QT_Q4_K ? 15.f : 31.f;
+    const u32x4 h = *(const u32x4*)(row + (size_t)blk * (QT == QT_Q4_K ? 144 : 176));
+    const float d = h2f(h[0] & 0xffffu), dmin = h2f(h[0] >> 16);
+    float b = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      int sc, mn;
+      kq_scale_min(j, h[1], h[2], h[3], sc, mn);
+      const float dsc = d * (float)sc, dm = dmin * (float)mn;
+      b = fmaxf(b, fmaxf(fabsf(fmaf(dsc, QMAX, -dm)), fabsf(dm)));
+    }
+    return b;
+  } else if constexpr (QT == QT_Q6_K) {
+    const uint8_t* b = row + (size_t)blk * 210;
+    const uint2 s0 = ld_u64_a2(b + 192), s1 = ld_u64_a2(b + 200);
+    const float d = h2f(ld_u16(b + 208));
+    int m = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) m = max(m, max(abs((int)(int8_t)byte_at(s0, k)), abs((int)(int8_t)byte_at(s1, k))));
+    return fabsf(d * (float)m) * 32.f;
+  } else if constexpr (QT == QT_Q8_0) {
+    return fabsf(h2f(ld_u16(row + (size_t)blk * 34))) * 128.f;
+  } else {
+    static_assert(QT == QT_Q5_0, "fused types");
+    return fabsf(h2f(ld_u16(row + (size_t)blk * 22))) * 16.f;
+  }
+}
+
 // Where a producer lane's decoded values go.  x3-ref: fp16 of q_val (RNE) into o.
 // F32 (the fp32-dequant semantics of tiermm_qgemm's TIERMM_MODE_F32): v = q_val * 2^e of
 // its row, split as x3s_split splits the fp32 dequant -- hi = fp16(v) into o, lo =
@@ -177,7 +216,14 @@ struct Emit {
     if constexpr (!F32) {
       pack4(f0, f1, f2, f3, o[2 * k], o[2 * k + 1]);
     } else {
-      float v[4] = {f0 * sc, f1 * sc, f2 * sc, f3 * sc};
+      put_scaled(k, f0 * sc, f1 * sc, f2 * sc, f3 * sc);
+    }
+  }
+  // F32, values already scaled by 2^e (a producer that folds 2^e into its block scales:
+  // exact, as scaling by a power of two commutes with the rounding of q_val)
+  __device__ __forceinline__ void put_scaled(int k, float f0, float f1, float f2, float f3) {
+    if constexpr (F32) {
+      float v[4] = {f0, f1, f2, f3};
       asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]));
       const h2v h0 = {(_Float16)v[0], (_Float16)v[1]}, h1 = {(_Float16)v[2], (_Float16)v[3]};
       float r[4] = {v[0] - (float)h0[0], v[1] - (float)h0[1], v[2] - (float)h1[0], v[3] - (float)h1[1]};
@@ -526,7 +572,8 @@ __global__ __launch_bounds__(512) void qgemm_fused_x3ref(const QArgs p) {
           for (int t = 0; t < 2; ++t) {
             int sc, mn;
             kq_scale_min(((kq0 + q) & 7) + t, H[1], H[2], H[3], sc, mn);
-            const float dsc = d * (float)sc, dm = dmin * (float)mn;
+            // F32: 2^e folded into both scales
+            const float dsc = d * (float)sc * (F32 ? em.sc : 1.f), dm = dmin * (float)mn * (F32 ? em.sc : 1.f);
             uint8_t* bt = lds + ((q + t) % NBR) * BSLOT;
 #pragma unroll
             for (int i = 0; i < HPL; ++i) {
@@ -541,7 +588,8 @@ __global__ __launch_bounds__(512) void qgemm_fused_x3ref(const QArgs p) {
                 float f[4];
 #pragma unroll
                 for (int b = 0; b < 4; ++b) f[b] = fmaf(dsc, (float)((v >> (8 * b)) & 0xffu), -dm);
-                em.put(w, f[0], f[1], f[2], f[3]);
+                if constexpr (F32) em.put_scaled(w, f[0], f[1], f[2], f[3]);
+                else em.put(w, f[0], f[1], f[2], f[3]);
               }
               const uint32_t* o = em.o;
               *(u32x4*)(bt + swz(r, 2 * (h0 + i))) = u32x4{o[0], o[1], o[2], o[3]};
@@ -671,8 +719,10 @@ __global__ __launch_bounds__(512) void qgemm_fused_x3ref(const QArgs p) {
   // flag read nor the fragment reads stall the MFMA issue.  Stage q's slot is
   // released once its fragments are in registers, before its last MFMAs.
   // (At BN = 160, and with accumulation chunks, the second set does not fit in
-  // registers: fragments are read when the stage starts.)
-  constexpr bool PIPE = NB <= 8 && !CH && !F32;
+  // registers: fragments are read when the stage starts.)  F32: only the hi plane's
+  // fragments come a stage ahead; the lo plane's are read when the stage starts and
+  // first used by its second part, so the first part's MFMAs cover their latency.
+  constexpr bool PIPE = NB <= 8 && !CH;
   static_assert(XR % 2 == 0, "B register sets follow u");
   half8 bf[PIPE ? 2 : 1][NB];
   half8 bl[F32 ? NB : 1];  // F32: the lo plane of the stage
@@ -680,10 +730,11 @@ __global__ __launch_bounds__(512) void qgemm_fused_x3ref(const QArgs p) {
     const uint8_t* bs = lds + (q % NBR) * BSLOT;
 #pragma unroll
     for (int j = 0; j < NB; ++j) dst[j] = *(const half8*)(bs + j * 1024 + fo);
-    if constexpr (F32) {
+  };
+  auto readBl = [&](int q) __attribute__((always_inline)) {
+    const uint8_t* bs = lds + (q % NBR) * BSLOT + BPART;
 #pragma unroll
-      for (int j = 0; j < NB; ++j) bl[j] = *(const half8*)(bs + BPART + j * 1024 + fo);
-    }
+    for (int j = 0; j < NB; ++j) bl[j] = *(const half8*)(bs + j * 1024 + fo);
   };
   if constexpr (PIPE) {
     poll4(ready, 0);
@@ -704,6 +755,7 @@ __global__ __launch_bounds__(512) void qgemm_fused_x3ref(const QArgs p) {
           poll4(ready + 4 * (q % FL), q);
           readB(q, bf[0]);
         }
+        if constexpr (F32) readBl(q);
         const int cur = PIPE ? (u & 1) : 0;  // u is a constant after unrolling
         // parts lo, mid, hi (tier.cpp:940) into one fp32 accumulator; F32: x lo * W hi,
         // x hi * W lo, x hi * W hi (the x3-2x2 products, smallest first)
@@ -1025,37 +1077,31 @@ int qgemm_fused(const void* W, int qtype, size_t rb, const uint16_t* xparts, siz
                             xexp, wexp);
 }
 
-// wexp[n] = x3s_exp(max |q_val| over row n): one wave a row, 8 columns a lane and step
-// (K a multiple of 32).  The decode is Dec's, the one the fp32 dequant and the fused
-// producers' values agree with.
+// wexp[n] = x3s_exp(the bound of row n's |q_val|, blk_bound over its blocks): one wave a
+// row, the row's blocks over its lanes.  Only the block scales are read.
 template <int QT>
-__global__ __launch_bounds__(256) void qrow_exp_kernel(const uint8_t* __restrict__ W, size_t rb, int N, int K,
+__global__ __launch_bounds__(256) void qrow_exp_kernel(const uint8_t* __restrict__ W, size_t rb, int N, int nblk,
                                                       int32_t* __restrict__ wexp) {
   const int lane = threadIdx.x & 63;
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
   const uint8_t* row = W + (size_t)n * rb;
-  float amax = 0.f;
-  for (int c = 8 * lane; c < K; c += 512) {
-    float v[8];
-    Dec<QT>::run(row, c, v);
+  float b = 0.f;
+  for (int i = lane; i < nblk; i += 64) b = fmaxf(b, blk_bound<QT>(row, i));
 #pragma unroll
-    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-  }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-  if (lane == 0) wexp[n] = x3s_exp(amax);
+  for (int o = 32; o > 0; o >>= 1) b = fmaxf(b, __shfl_xor(b, o, 64));
+  if (lane == 0) wexp[n] = x3s_exp(b);
 }
 
 int qrow_exps(const void* W, int qtype, size_t rb, int N, int K, int32_t* wexp, hipStream_t s) {
   const unsigned grid = (unsigned)((N + 3) / 4);
   const uint8_t* w = (const uint8_t*)W;
   switch (qtype) {
-    case QT_Q4_K: qrow_exp_kernel<QT_Q4_K><<<grid, 256, 0, s>>>(w, rb, N, K, wexp); break;
-    case QT_Q5_K: qrow_exp_kernel<QT_Q5_K><<<grid, 256, 0, s>>>(w, rb, N, K, wexp); break;
-    case QT_Q6_K: qrow_exp_kernel<QT_Q6_K><<<grid, 256, 0, s>>>(w, rb, N, K, wexp); break;
-    case QT_Q8_0: qrow_exp_kernel<QT_Q8_0><<<grid, 256, 0, s>>>(w, rb, N, K, wexp); break;
-    case QT_Q5_0: qrow_exp_kernel<QT_Q5_0><<<grid, 256, 0, s>>>(w, rb, N, K, wexp); break;
+    case QT_Q4_K: qrow_exp_kernel<QT_Q4_K><<<grid, 256, 0, s>>>(w, rb, N, K / 256, wexp); break;
+    case QT_Q5_K: qrow_exp_kernel<QT_Q5_K><<<grid, 256, 0, s>>>(w, rb, N, K / 256, wexp); break;
+    case QT_Q6_K: qrow_exp_kernel<QT_Q6_K><<<grid, 256, 0, s>>>(w, rb, N, K / 256, wexp); break;
+    case QT_Q8_0: qrow_exp_kernel<QT_Q8_0><<<grid, 256, 0, s>>>(w, rb, N, K / 32, wexp); break;
+    case QT_Q5_0: qrow_exp_kernel<QT_Q5_0><<<grid, 256, 0, s>>>(w, rb, N, K / 32, wexp); break;
     default: return set_error(TIERMM_UNSUPPORTED, "qrow_exps: type %d", qtype);
   }
   TM_LAUNCH_CHECK("tiermm_qgemm: weight row exponents");

@@ -43,7 +43,8 @@ int qgemm_fused_groups(const void* const* W, int qtype, const int* row0, const i
                        const int32_t* wexp = nullptr);
 size_t qgemm_fused_partials_bytes(int qtype, int M, int N, int K, bool f32 = false);
 bool qgemm_fusable(int qtype, const int* rows, int n, int N, int K, bool split, bool f32 = false);
-// wexp[n] = x3s_exp(max |q_val| of weight row n), rows [0, N) of K columns.
+// wexp[n] = the x3s exponent of a bound of weight row n's |q_val| (from the block
+// scales), rows [0, N) of K columns, for the fused fp32 kernels.
 int qrow_exps(const void* W, int qtype, size_t rb, int N, int K, int32_t* wexp, hipStream_t s);
 int device_cus(int* cus);
 
@@ -1450,7 +1451,7 @@ int tiermm_qgemm(const void* W, int qtype, size_t rb, const float* X, float* Y, 
   const size_t mk = (size_t)M * K;
   if (mode == TIERMM_MODE_F32 && qgemm_fusable(qtype, &M, 1, N, K, true, true)) {
     // the same semantics with W decoded inside the GEMM: no fp32 or fp16 copy of W
-    // in memory, one pass over W for its row exponents first
+    // in memory; one pass over the weight's block scales for its row exponents first
     uint8_t* b = (uint8_t*)w;
     uint16_t* xhi = (uint16_t*)b;             b += al256(mk * 2);
     b += al256(mk * 2);                       // xlo, one plane stride after xhi
