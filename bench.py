@@ -502,7 +502,11 @@ def main() -> int:
                                ("q4_K_5120x14336_m1", tier_amd.Q4_K, 5120, 14336),
                                ("q8_0_4096x4096_m1", tier_amd.Q8_0, 4096, 4096),
                                ("q5_K_5120x14336_m1", tier_amd.Q5_K, 5120, 14336),
-                               ("q6_K_5120x14336_m1", tier_amd.Q6_K, 5120, 14336)):
+                               ("q6_K_5120x14336_m1", tier_amd.Q6_K, 5120, 14336),
+                               # long rows (gemv_q has no K bound, tier.cpp:300-306)
+                               ("q4_K_8192x28672_m1", tier_amd.Q4_K, 8192, 28672),
+                               ("q5_K_8192x28672_m1", tier_amd.Q5_K, 8192, 28672),
+                               ("q8_0_4096x28672_m1", tier_amd.Q8_0, 4096, 28672)):
             if not want(name):
                 continue
             log(f"bench: {name}")

@@ -11,8 +11,11 @@ gemv_q's own lane-order fp32 sum (orc_gemv_lanes), whose NaN / +Inf / -Inf
 pattern must match exactly; the fp64 closed form (orc_gemv_f64) must agree with
 it, which pins the pattern independently of the summation order.
 
-Long K.  The reference loop has no K bound; above 16384 x no longer fits the
-LDS the kernels stage it in.  Bar: relative Frobenius error <= 1e-5 against fp64.
+Long K.  The reference loop has no K bound.  q4_K, q5_K and q8_0 rows up to
+K = 28672 run on the int8-MFMA kernel (x digits of the whole row in 121 KiB of
+LDS); q6_K above 14336 and the other types above 16384 on the generic kernel,
+which reads x from global memory.  Bar: relative Frobenius error <= 1e-5 against
+fp64.
 """
 import numpy as np
 import pytest

@@ -381,7 +381,7 @@ bool qgemv_mfma_fits(const void* W, int qtype, size_t rb, int K);
 bool qgemv_q6k_fits(const void* W, size_t rb, int N, int K);
 int qgemv_q6k(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s);
 int qgemv_mfma(const void* W, int qtype, size_t rb, const float* x, float* y, int N, int K, hipStream_t s);
-constexpr int kQ4kMaxK = 14336;  // equals the limit in qgemv_q4k.hip
+constexpr int kQ4kMaxK = 28672;  // equals the limit in qgemv_q4k.hip
 
 int qgemv_dispatch(const void* W, int qtype, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
   switch (qtype) {

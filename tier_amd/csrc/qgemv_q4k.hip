@@ -214,8 +214,9 @@ int launch(const void* W, size_t rb, const float* x, float* y, int N, int K, hip
 
 }  // namespace
 
-// Largest K handled (the x digits of the whole row stay in LDS).
-constexpr int kQ4kMaxK = 14336;
+// Largest K handled (the x digits of the whole row stay in LDS: 121 KiB at this K,
+// with the weight ring in the remaining 39 KiB).
+constexpr int kQ4kMaxK = 28672;
 
 // Launch shapes by measurement (MI355X; 200 launches over rotated copies).  At
 // most one row tile per CU: one tile per workgroup, K in four parts (q8_0
@@ -235,6 +236,8 @@ int qgemv_q4k(const void* W, size_t rb, const float* x, float* y, int N, int K, 
     if (tiles <= 256) return launch<QT_Q4_K, 2, 2, 2, 3, 2, 8192>(W, rb, x, y, N, K, s);
     return launch<QT_Q4_K, 2, 4, 2, 2, 1, 8192>(W, rb, x, y, N, K, s);
   }
+  // K above 14336: eight waves (two tiles x four K parts), one super-block per stage
+  if (K > 14336) return launch<QT_Q4_K, 2, 4, 1, 2, 4, 28672>(W, rb, x, y, N, K, s);
   if (tiles >= 640) return launch<QT_Q4_K, 4, 1, 4, 2, 4, 14336>(W, rb, x, y, N, K, s);  // 24.2 against 25.5 us
   // up to one tile per CU: one tile, K in eight parts (4096x14336: 9.4-9.6 against 11.7 us;
   // 1024x14336: 7.1 against 9.4 us)
@@ -261,6 +264,7 @@ int qgemv_mfma(const void* W, int qtype, size_t rb, const float* x, float* y, in
       if (tiles < 640) return launch<QT_Q5_K, 2, 2, 2, 3, 2, 8192>(W, rb, x, y, N, K, s);
       return launch<QT_Q5_K, 4, 2, 2, 2, 2, 8192>(W, rb, x, y, N, K, s);
     }
+    if (K > 14336) return launch<QT_Q5_K, 2, 3, 1, 2, 5, 28672>(W, rb, x, y, N, K, s);  // six waves fit the ring
     if (tiles >= 640) return launch<QT_Q5_K, 4, 2, 1, 2, 2, 14336>(W, rb, x, y, N, K, s);
     if (tiles <= 256) return launch<QT_Q5_K, 1, 8, 1, 2, 2, 14336>(W, rb, x, y, N, K, s);  // 4096x14336: 11.0 against 13.8 us
     return launch<QT_Q5_K, 2, 4, 2, 2, 2, 14336>(W, rb, x, y, N, K, s);
@@ -275,6 +279,7 @@ int qgemv_mfma(const void* W, int qtype, size_t rb, const float* x, float* y, in
     if (tiles < 640) return launch<QT_Q8_0, 2, 2, 1, 3, 2, 8192>(W, rb, x, y, N, K, s);
     return launch<QT_Q8_0, 4, 2, 1, 2, 2, 8192>(W, rb, x, y, N, K, s);
   }
+  if (K > 14336) return launch<QT_Q8_0, 1, 4, 1, 2, 7, 28672>(W, rb, x, y, N, K, s);  // four waves fit the ring
   if (tiles >= 640) return launch<QT_Q8_0, 4, 2, 1, 2, 2, 14336>(W, rb, x, y, N, K, s);
   // 1024x14336: 9.3 against 16.7 us; 4096x14336: 14.5 against 18.9 us
   if (tiles <= 256) return launch<QT_Q8_0, 1, 8, 1, 2, 2, 14336>(W, rb, x, y, N, K, s);
