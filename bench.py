@@ -225,6 +225,41 @@ def bench_decoder_layer(tier_amd, hip, stream, T=4096, mode=None):
             "TFLOPS": round(tf, 1), "frac_x3_peak": round(tf / X3_PEAK_TFLOPS, 4), "per_matrix": out}
 
 
+def bench_decoder_layer_shared(tier_amd, hip, stream, T=4096):
+    """Config 4's layer as the engine would issue it with x split once per activation
+    (tiermm_split3_f16_ktiled, then tiermm_qgemm_x3parts on the K-tiled planes): one split
+    for q/k/v, one for o, one for gate/up, one for down -- four splits and seven products
+    per step, timed together."""
+    H, Q, KV, F = 5120, 4096, 1024, 14336
+    mats = (("q", tier_amd.Q4_K, Q, H), ("k", tier_amd.Q4_K, KV, H), ("v", tier_amd.Q5_K, KV, H),
+            ("o", tier_amd.Q4_K, H, Q), ("gate", tier_amd.Q4_K, F, H), ("up", tier_amd.Q4_K, F, H),
+            ("down", tier_amd.Q5_K, H, F))
+    groups = ((H, ("q", "k", "v")), (Q, ("o",)), (H, ("gate", "up")), (F, ("down",)))
+    rng = np.random.default_rng(10)
+    xs = {K: hip.to_device(rng.standard_normal((T, K), dtype=np.float32)) for K in (H, Q, F)}
+    P = {K: hip.DeviceBuffer(3 * T * K * 2) for K in (H, Q, F)}
+    Y = hip.DeviceBuffer(T * F * 4)
+    wsb = max(tier_amd.qgemm_x3parts_ws_bytes(qt, T, N, K) for _, qt, N, K in mats)
+    WS = hip.DeviceBuffer(max(wsb, 256))
+    W = {name: (hip.to_device(_quantized(tier_amd, qt, N, K, 11 + i)), qt, N, K)
+         for i, (name, qt, N, K) in enumerate(mats)}
+    log(f"bench: decoder layer, shared splits, T={T}")
+
+    def step(_i):
+        for K, names in groups:
+            tier_amd.split3_ktiled(xs[K].ptr, P[K].ptr, T, K, T * K, stream)
+            for nm in names:
+                Wd, qt, N, Kw = W[nm]
+                tier_amd.qgemm_x3parts(Wd.ptr, qt, tier_amd.q_row_bytes(qt, Kw), P[K].ptr, T * K, Y.ptr, T, N, Kw, N,
+                                       0.0, WS.ptr, wsb, stream)
+    km = time_steady(hip, stream, step, 10)
+    flop = sum(2.0 * T * N * K for _, _, N, K in mats)
+    tf = flop / (km * 1e-3) / 1e12
+    del W
+    return {"recipe": "q4_K_S (v, down q5_K)", "T": T, "splits": 4, "total_us": round(km * 1e3, 1),
+            "TFLOPS": round(tf, 1), "frac_x3_peak": round(tf / X3_PEAK_TFLOPS, 4)}
+
+
 def bench_chat_stream(tier_amd, hip, stream, layers=4):
     """chat_lin with weight streaming (tier.cpp:2283-2285, 2351-2378): the 28 linears of
     `layers` config-4 decoder layers (q4_K_S, 155.6 MiB each) with every matrix streamed from
@@ -584,6 +619,8 @@ def main() -> int:
         del Wf, Bm, C, WS
     if want("decoder_layer_t4096"):
         secondary["decoder_layer_t4096"] = bench_decoder_layer(tier_amd, hip, stream)
+    if want("decoder_layer_t4096_shared_splits"):
+        secondary["decoder_layer_t4096_shared_splits"] = bench_decoder_layer_shared(tier_amd, hip, stream)
     for T in (256, 4096):  # chat prefill: chunks of 256 rows (tier.cpp:2538), and the config's batch
         if want(f"chat_prefill_t{T}"):
             secondary[f"chat_prefill_t{T}"] = bench_decoder_layer(tier_amd, hip, stream, T, tier_amd.MODE_F32)

@@ -253,6 +253,31 @@ size_t tiermm_qgemm_ws_bytes(int qtype, int M, int N, int K, int mode);
  * this shape -- tile width *bn, K splits *ks, accumulation chunks *kc -- after
  * TIERMM_QGEMM_TILE; TIERMM_UNSUPPORTED when the type or shape does not take it. */
 int tiermm_qgemm_plan(int qtype, int M, int N, int K, int* bn, int* ks, int* kc);
+/* No counterpart in the reference as an entry point (fp3gemm, tier.cpp:922-943, splits
+ * its B operand on every call): tiermm_qgemm's TIERMM_MODE_X3REF product with x
+ * already split, so products that read the same activations (the q / k / v
+ * projections, gate / up) split them once.  xparts: the three fp16 planes of x[M][K]
+ * in TIERMM_HML order, 16-byte aligned, part_stride (a multiple of 8, >= M*K)
+ * elements apart, laid out as `layout` says:
+ *   TIERMM_PARTS_ROWS   -- row-major, as tiermm_split3_f16 writes them;
+ *   TIERMM_PARTS_KTILED -- K-tiled, as tiermm_split3_f16_ktiled writes them (element
+ *                          (r, c) at ((c/32)*M + r)*32 + c%32): each MFMA operand load
+ *                          is one contiguous kilobyte, the layout tiermm_qgemm uses
+ *                          itself, and the faster one.
+ * K a multiple of 32 (TIERMM_UNSUPPORTED otherwise).  Same result, bit for bit, as
+ * tiermm_qgemm on the unsplit x.  Workspace (tiermm_qgemm_x3parts_ws_bytes): the fused
+ * kernel's split-K partial sums, or the fp16 weight for the types it does not decode. */
+#define TIERMM_PARTS_ROWS 0
+#define TIERMM_PARTS_KTILED 1
+int tiermm_qgemm_x3parts(const void* W, int qtype, size_t rb, const uint16_t* xparts, size_t part_stride,
+                         int layout, float* Y, int M, int N, int K, int ldy, float beta, void* ws,
+                         size_t ws_bytes, tiermm_stream_t stream);
+size_t tiermm_qgemm_x3parts_ws_bytes(int qtype, int M, int N, int K);
+/* split3_fp_k (tier.cpp:869-870) of x[M][K] (16-byte aligned, K a multiple of 32) into
+ * the K-tiled planes of TIERMM_PARTS_KTILED, in TIERMM_HML order, part_stride (a
+ * multiple of 8, >= M*K) elements apart: the same values as tiermm_split3_f16. */
+int tiermm_split3_f16_ktiled(const float* x, uint16_t* parts, int M, int K, size_t part_stride,
+                             tiermm_stream_t stream);
 
 /* ------------------------------------------------- grouped (MoE) GEMM */
 /* No reference function (the reference refuses MoE models, arch.py:158-159):

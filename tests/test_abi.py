@@ -112,6 +112,16 @@ def test_argument_checks_return_before_device_work():
     assert L.tiermm_x3s_gemm(16, 16, 16, 16, 16, 16, 16, 4, 4, 48, 4, None) == tier_amd.UNSUPPORTED
     assert L.tiermm_split3_f16(16, 16, 10, 5, 0, None) == tier_amd.EINVAL
     assert "part_stride" in tier_amd.last_error()
+    # pre-split x: K in whole 32-steps, aligned planes at least M*K apart
+    assert L.tiermm_qgemm_x3parts(16, tier_amd.F16, 96, 16, 96, 0, 16, 2, 4, 48, 4, 0.0, None, 0,
+                                  None) == tier_amd.UNSUPPORTED
+    assert L.tiermm_qgemm_x3parts(16, tier_amd.Q4_K, 144, 16, 511, 0, 16, 2, 4, 256, 4, 0.0, None, 0,
+                                  None) == tier_amd.EINVAL
+    assert L.tiermm_qgemm_x3parts(16, tier_amd.Q4_K, 144, 18, 512, 1, 16, 2, 4, 256, 4, 0.0, None, 0,
+                                  None) == tier_amd.EINVAL
+    assert L.tiermm_qgemm_x3parts(16, tier_amd.Q4_K, 144, 16, 512, 2, 16, 2, 4, 256, 4, 0.0, None, 0,
+                                  None) == tier_amd.EINVAL  # unknown layout
+    assert L.tiermm_split3_f16_ktiled(16, 16, 2, 48, 96, None) == tier_amd.UNSUPPORTED
     # chat_fp3 mirrors: an unsupported shape -> False, not an exception (the allocation-free
     # variant keeps K a multiple of 32: it has no workspace to pad into)
     assert tier_amd.chat_fp3_noalloc(16, 16, 16, 4, 48, 4, 4) is False

@@ -63,6 +63,9 @@ EXPORTS = (
     "tiermm_host_alloc", "tiermm_host_free", "tiermm_x3_rows_noalloc", "tiermm_chat_set_heads",
     "tiermm_chat_heads", "tiermm_chat_set_lora", "tiermm_chat_lora_scale", "tiermm_sgemm", "tiermm_sgemm_ws_bytes",
     "tiermm_qgemm_plan",
+    "tiermm_qgemm_x3parts",
+    "tiermm_qgemm_x3parts_ws_bytes",
+    "tiermm_split3_f16_ktiled",
 )
 
 
@@ -110,6 +113,9 @@ _sig("tiermm_sgemm", [_i, _i, _i, _i, _vp, _i, _vp, _i, _f, _vp, _i, _vp, _sz, _
 _sig("tiermm_sgemm_ws_bytes", [_i, _i, _i, _i], _sz)
 _sig("tiermm_qgemm_plan", [_i, _i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i), ctypes.POINTER(_i)])
 _sig("tiermm_qgemm_ws_bytes", [_i, _i, _i, _i, _i], _sz)
+_sig("tiermm_qgemm_x3parts", [_vp, _i, _sz, _vp, _sz, _i, _vp, _i, _i, _i, _i, _f, _vp, _sz, _vp])
+_sig("tiermm_split3_f16_ktiled", [_vp, _vp, _i, _i, _sz, _vp])
+_sig("tiermm_qgemm_x3parts_ws_bytes", [_i, _i, _i, _i], _sz)
 _sig("tiermm_quantize", [_i, _vp, _vp, _sz, _i, _i])
 _sig("tiermm_gemv", [_vp, _i, _vp, _vp, _i, _i, _vp])
 _pi = ctypes.POINTER(_i)
@@ -324,6 +330,27 @@ def qgemm_plan(qtype: int, M: int, N: int, K: int):
 
 def qgemm_ws_bytes(qtype: int, M: int, N: int, K: int, mode: int = MODE_X3REF) -> int:
     return _L.tiermm_qgemm_ws_bytes(qtype, M, N, K, mode)
+
+
+PARTS_ROWS, PARTS_KTILED = 0, 1
+
+
+def qgemm_x3parts(W: int, qtype: int, rb: int, xparts: int, part_stride: int, Y: int, M: int, N: int, K: int,
+                  ldy: int | None = None, beta: float = 0.0, ws: int | None = None, ws_bytes: int = 0,
+                  stream=None, layout: int = PARTS_KTILED) -> None:
+    """tiermm_qgemm (x3-ref) on x already split: HML planes part_stride apart, row-major
+    (split3) or K-tiled (split3_ktiled)."""
+    _check(_L.tiermm_qgemm_x3parts(W, qtype, rb, xparts, part_stride, layout, Y, M, N, K,
+                                   N if ldy is None else ldy, beta, ws, ws_bytes, _s(stream)))
+
+
+def split3_ktiled(x: int, parts: int, M: int, K: int, stride: int | None = None, stream=None) -> None:
+    """split3_fp_k of x[M][K] into K-tiled HML planes (the layout qgemm_x3parts reads fastest)."""
+    _check(_L.tiermm_split3_f16_ktiled(x, parts, M, K, M * K if stride is None else stride, _s(stream)))
+
+
+def qgemm_x3parts_ws_bytes(qtype: int, M: int, N: int, K: int) -> int:
+    return _L.tiermm_qgemm_x3parts_ws_bytes(qtype, M, N, K)
 
 
 def gemv(W: int, wtype: int, x: int, y: int, N: int, K: int, stream=None) -> None:

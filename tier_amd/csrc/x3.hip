@@ -1107,6 +1107,17 @@ int tiermm_split3_f16(const float* x, uint16_t* parts, size_t n, size_t part_str
   return split3_launch(x, parts, n, part_stride, order, (hipStream_t)stream);
 }
 
+int tiermm_split3_f16_ktiled(const float* x, uint16_t* parts, int M, int K, size_t part_stride,
+                             tiermm_stream_t stream) {
+  const char* who = "tiermm_split3_f16_ktiled";
+  if (M < 0 || K < 0) return set_error(TIERMM_EINVAL, "%s: negative size", who);
+  if (K % BK) return set_error(TIERMM_UNSUPPORTED, "%s: K=%d is not a multiple of %d", who, K, BK);
+  const size_t mk = (size_t)M * K;
+  if (mk == 0) return TIERMM_OK;
+  if (!x || !parts || part_stride < mk) return set_error(TIERMM_EINVAL, "%s: null buffer or part_stride < M*K", who);
+  return split3_launch(x, parts, mk, part_stride, TIERMM_HML, (hipStream_t)stream, false, (size_t)M, K);
+}
+
 int tiermm_split3_bf16(const float* x, uint16_t* parts, size_t n, size_t part_stride, int order,
                        tiermm_stream_t stream) {
   if (order != TIERMM_HML && order != TIERMM_LMH)
@@ -1525,6 +1536,51 @@ int tiermm_qgemm(const void* W, int qtype, size_t rb, const float* X, float* Y, 
   if (!tiled) return x3ref_nt(parts, mk, w16, K, Y, ldy, M, N, K, beta, s, who);
   X3Args a{};
   a.A[0] = parts; a.A[1] = parts + mk; a.A[2] = parts + 2 * mk;
+  a.B[0] = w16;
+  a.lda = K; a.ldb = K; a.atile = M; a.btile = N;
+  a.C = Y; a.ldc = ldy; a.M = M; a.N = N; a.K = K; a.beta = beta;
+  return launch_x3_big<X3_REF>(a, s, who);
+}
+
+size_t tiermm_qgemm_x3parts_ws_bytes(int qtype, int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % BK) return 0;
+  if (qgemm_fusable(qtype, &M, 1, N, K, true)) return qgemm_fused_partials_bytes(qtype, M, N, K);
+  return (size_t)N * K * sizeof(uint16_t);  // the fp16 weight
+}
+
+int tiermm_qgemm_x3parts(const void* W, int qtype, size_t rb, const uint16_t* xparts, size_t part_stride,
+                         int layout, float* Y, int M, int N, int K, int ldy, float beta, void* ws, size_t ws_bytes,
+                         tiermm_stream_t stream) {
+  const char* who = "tiermm_qgemm_x3parts";
+  int st = check_qweight(who, W, qtype, rb, K, 1);
+  if (st) return st;
+  st = check_nt(who, M, N, K);
+  if (st) return st;
+  if (ldy < N) return set_error(TIERMM_EINVAL, "%s: ldy < N", who);
+  if (layout != TIERMM_PARTS_ROWS && layout != TIERMM_PARTS_KTILED)
+    return set_error(TIERMM_EINVAL, "%s: layout %d", who, layout);
+  const bool tiled = layout == TIERMM_PARTS_KTILED;
+  if (M == 0 || N == 0) return TIERMM_OK;
+  if (!xparts || !Y || !aligned16(xparts) || part_stride < (size_t)M * K || part_stride % 8)
+    return set_error(TIERMM_EINVAL, "%s: x planes must be 16-byte aligned, part_stride >= M*K and a multiple of 8",
+                     who);
+  void* w = nullptr;
+  st = get_workspace(ws, ws_bytes, tiermm_qgemm_x3parts_ws_bytes(qtype, M, N, K), &w, who);
+  if (st) return st;
+  hipStream_t s = (hipStream_t)stream;
+  if (qgemm_fusable(qtype, &M, 1, N, K, true)) {
+    int cus = 0;
+    st = device_cus(&cus);
+    if (st) return st;
+    return qgemm_fused(W, qtype, rb, xparts, part_stride, tiled ? (size_t)M : 0, Y, ldy, M, N, K, beta, cus, s, who,
+                       (float*)w);
+  }
+  uint16_t* w16 = (uint16_t*)w;
+  st = dequant_f16_rows(W, qtype, rb, K, (size_t)N, w16, s, tiled);
+  if (st) return st;
+  if (!tiled) return x3ref_nt(xparts, part_stride, w16, K, Y, ldy, M, N, K, beta, s, who);
+  X3Args a{};  // both operands K-tiled: the big-tile kernel (rows past M or N read clamped)
+  a.A[0] = xparts; a.A[1] = xparts + part_stride; a.A[2] = xparts + 2 * part_stride;
   a.B[0] = w16;
   a.lda = K; a.ldb = K; a.atile = M; a.btile = N;
   a.C = Y; a.ldc = ldy; a.M = M; a.N = N; a.K = K; a.beta = beta;
