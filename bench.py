@@ -591,6 +591,33 @@ def main() -> int:
         secondary["x3s_4096x5120x5120"] = {"TFLOPS": round(tf, 2), "frac_x3_peak": round(tf / X3_PEAK_TFLOPS, 4),
                                            "us_per_call": round(km * 1e3, 1), "includes": "X split + GEMM"}
         del bufs, Wf, Xf
+    # fp3gemm (tier.cpp:922-943) on the decoder's down-projection weight (fp16 W 5120x14336),
+    # 4096 tokens: the forward (OP_T) and the dX product (OP_N, W read in place), equal flops
+    for name, opA in (("x3_fwd_4096x5120x14336", tier_amd.OP_T), ("x3_dx_4096x14336x5120", tier_amd.OP_N)):
+        if not want(name):
+            continue
+        log(f"bench: {name}")
+        T, Nw, Kw = 4096, 5120, 14336
+        rng = np.random.default_rng(22)
+        Wh = hip.to_device((rng.standard_normal((Nw, Kw), dtype=np.float32) * np.float32(0.02)).astype(np.float16))
+        if opA == tier_amd.OP_T:  # out[T][Nw] = x[T][Kw] W^T
+            m, n, k = Nw, T, Kw
+        else:  # dX[T][Kw] = dY[T][Nw] W
+            m, n, k = Kw, T, Nw
+        Bm = hip.to_device(rng.standard_normal((n, k), dtype=np.float32))
+        C = hip.DeviceBuffer(n * m * 4)
+        C.fill_bytes(0)
+        wsb = tier_amd.x3_gemm_ws_bytes(m, n, k)
+        WS = hip.DeviceBuffer(wsb)
+        beta = 0.0 if opA == tier_amd.OP_T else 1.0
+        f = lambda i: tier_amd.fp3gemm(opA, m, n, k, Wh.ptr, Kw, Bm.ptr, beta, C.ptr, m, WS.ptr, wsb,  # noqa: E731
+                                       stream)
+        km = time_steady(hip, stream, f, 10)
+        tf = 2.0 * m * n * k / (km * 1e-3) / 1e12
+        secondary[name] = {"TFLOPS": round(tf, 2), "frac_x3_peak": round(tf / X3_PEAK_TFLOPS, 4),
+                           "us_per_call": round(km * 1e3, 1), "beta": beta,
+                           "includes": "x split into three fp16 parts + GEMM (dX: W read in place, no transpose)"}
+        del Wh, Bm, C, WS
     # the x3-off fallback's fp32 products (sgemm, tier.cpp:1196-1200, 1229-1236) at the
     # decoder's down projection (W 5120x14336): forward and dX, 4096 tokens, beta = 1 for dX
     for name, opA in (("sgemm_fwd_4096x5120x14336", tier_amd.OP_T), ("sgemm_dx_4096x14336x5120", tier_amd.OP_N)):

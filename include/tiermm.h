@@ -163,8 +163,11 @@ int tiermm_split3_bf16(const float* x, uint16_t* parts, size_t n, size_t part_st
  * forward linear out[n][m] = x[n][k] * W[m][k]^T (low3_linear, tier.cpp:1212);
  * with opA = TIERMM_OP_N and lda = m it is the dX product of linear_dx /
  * linear_dx_acc (tier.cpp:1226, 1234): A is m x k column-major (W[k][m] in
- * memory) and is transposed into the workspace first.  ldc >= m.  Accuracy:
- * rel. Frobenius error <= 2^-20 against fp64(A * B). */
+ * memory).  The large-tile kernel reads that layout in place (the reference's
+ * TR operand, tier_wmma.h:34-37) when k is a multiple of 32, m and lda multiples
+ * of 8 and A 16-byte aligned; otherwise A is transposed into the workspace first
+ * (same result, bit for bit).  ldc >= m.  Accuracy: rel. Frobenius error <= 2^-20
+ * against fp64(A * B). */
 int tiermm_x3_gemm(int opA, int m, int n, int k, const uint16_t* A, int lda, const float* B,
                    float beta, float* C, int ldc, void* ws, size_t ws_bytes,
                    tiermm_stream_t stream);

@@ -532,3 +532,38 @@ def test_chat_bf3_rows(gpu):
     hip.synchronize()
     got = Y.download(np.float32, M * ldo).reshape(M, ldo)[:, :N]
     assert oracle.rel_fro(got, x.astype(np.float64) @ _bf16_to_f64(w16).T) <= BAR
+
+
+def _dx_case(m, n, k, lda, beta, seed, bf16=False):
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((k, m)) * 0.02).astype(np.float32)
+    w16 = np.zeros((k, lda), np.uint16)
+    w16[:, :m] = (_bf16(w) if bf16 else oracle.f2h(w).reshape(k, m))
+    dy = activations(n, k, seed=seed + 1)
+    dx0 = rng.standard_normal((n, m)).astype(np.float32)
+    A, B, C = hip.to_device(w16), hip.to_device(dy), hip.to_device(dx0)
+    (tier_amd.bf3gemm if bf16 else tier_amd.fp3gemm)(tier_amd.OP_N, m, n, k, A.ptr, lda, B.ptr, beta, C.ptr, m)
+    hip.synchronize()
+    return C.download(np.float32, n * m).reshape(n, m), w16, dy, dx0
+
+
+@pytest.mark.parametrize("beta", [0.0, 1.0])
+@pytest.mark.parametrize("name,m,k,bf16", [("q", 5120, 4096, False), ("gate", 5120, 14336, False),
+                                           ("down", 14336, 5120, False), ("ragged", 4104, 2080, False),
+                                           ("q_bf16", 5120, 4096, True)])
+def test_x3_gemm_dx_in_place(gpu, name, m, k, bf16, beta):
+    """The dX product (linear_dx / linear_dx_acc, tier.cpp:1226, 1234) at config 4's shapes
+    (4096 tokens; W[k][m] in memory), fp16 (fp3gemm) and bf16 (bf3gemm): the big-tile kernel
+    reads W in place (TR), with K in accumulation chunks at k = 14336 and partial column
+    tiles at m = 4104.  Bit-identical with the transpose-first path (the same W with
+    lda = m + 4, which the in-place read does not take), and within 2^-20 of fp64 on 64
+    sampled rows."""
+    n = 4096
+    got, w16, dy, dx0 = _dx_case(m, n, k, m, beta, m + k, bf16)
+    ref_t, _, _, _ = _dx_case(m, n, k, m + 4, beta, m + k, bf16)
+    assert np.array_equal(got.view(np.uint32), ref_t.view(np.uint32))
+    rows = np.random.default_rng(5).choice(n, 64, replace=False)
+    wm = np.ascontiguousarray(w16[:, :m])
+    wf = (_bf16_to_f64(wm) if bf16 else oracle.h2f(wm.ravel()).reshape(k, m).astype(np.float64))
+    ref = dy[rows].astype(np.float64) @ wf + beta * dx0[rows].astype(np.float64)
+    assert oracle.rel_fro(got[rows], ref) <= BAR

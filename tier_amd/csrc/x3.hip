@@ -449,6 +449,9 @@ struct X3Args {
   const int32_t* aexp;  // per-row exponent of A (x3-2x2) or null
   const int32_t* bexp;  // per-row exponent of B or null
   float beta;
+  // Big-tile kernel, x3-ref modes only: B[0] is given transposed, [K][ldb] with the N
+  // index contiguous (the dX layout of W), and read in place (x3_big_tile<.., true>).
+  int btr;
 };
 
 // Stores a wave's WM x WN blocks of 32x32 accumulators at rows r0 + 32i.., columns
@@ -650,7 +653,27 @@ __global__ __launch_bounds__(256) void gemm_x3_kernel(const X3Args p) {
 // Per k-substep a wave reads NA*WM + NB*WN fragments for 3*WM*WN MFMAs (11 for
 // 30 in the 320 shape, 14 for 33 in the 352 shape, x3-ref), which keeps LDS
 // below half its bandwidth at full MFMA rate.
+//
+// TR (x3-ref modes): the weight comes as [K][ldb] with the N index contiguous (W
+// itself in the dX product, read in place instead of transposed first).  A stage
+// of it lands as 32 K-rows of TN halfs, each row padded by 16 bytes (TrB); a B
+// fragment is then two ds_read_b64_tr_b16.  That instruction treats each group
+// of 16 lanes as a 16 x 4 block -- lane s supplies the 4 halfs at its own address
+// -- and gives lane i the halfs (4e + i/4, i%4), e = 0..3, of that block.  So
+// lane s of group g addresses K-row kb + s/4, columns nb + 4(s%4).., with kb the
+// fragment's k base plus 8(g/2) and nb its column base plus 16(g%2), and receives
+// K-rows kb..kb+3 of column nb + s: the MFMA B operand's four k values, twice
+// (kb, kb + 4) for the eight.  K-rows are padded to 16 (mod 64) dwords, so the 32
+// bytes that each of a pair of groups reads from each of its four K-rows fall on
+// eight distinct 8-dword bank groups.
 constexpr int XB_M = 256;
+template <int TN>
+struct TrB {
+  static constexpr int DW = TN / 2 + (16 - (TN / 2) % 64 + 64) % 64;  // dwords per K-row in LDS
+  static constexpr int ROWB = DW * 4;
+  static constexpr int PART = (BK * ROWB + 1023) / 1024 * 1024;      // one stage, whole 1 KiB loads
+  static_assert(DW % 64 == 16 && DW * 2 >= TN, "K-row padding");
+};
 template <int TN>
 struct XbShape;
 template <>
@@ -663,14 +686,15 @@ struct XbShape<352> {
 };
 
 // One 256 x TN output tile t of the problem p (t < ceil(M/256) * ceil(N/TN)).
-template <int MODE, int TN>
+template <int MODE, int TN, bool TR = false>
 __device__ __forceinline__ void x3_big_tile(const X3Args& p, int t) {
   using Md = X3Mode<MODE>;
   using Sh = XbShape<TN>;
   constexpr int NA = Md::NA, NB = Md::NB, WM = Sh::WM, WN = Sh::WN, WAVES_N = Sh::WAVES_N;
-  constexpr int A_PART = XB_M * 64, B_PART = TN * 64;  // bytes of one part per stage
+  static_assert(!TR || NB == 1, "TR: the x3-ref modes");
+  constexpr int A_PART = XB_M * 64, B_PART = TR ? TrB<TN>::PART : TN * 64;  // bytes of one part per stage
   constexpr int STAGE = NA * A_PART + NB * B_PART;
-  constexpr int A_INST = XB_M * 64 / 1024, B_INST = TN * 64 / 1024;  // 1 KiB loads per part
+  constexpr int A_INST = A_PART / 1024, B_INST = B_PART / 1024;  // 1 KiB loads per part
   constexpr int NINST = NA * A_INST + NB * B_INST;
   constexpr int PER_WAVE = (NINST + 7) / 8;
   static_assert(WM * 32 * (8 / WAVES_N) == XB_M && WN * 32 * WAVES_N == TN, "wave grid covers the tile");
@@ -710,6 +734,16 @@ __device__ __forceinline__ void x3_big_tile(const X3Args& p, int t) {
         src = q == 0 ? p.A[0] : q == 1 ? p.A[1] : p.A[2];
         ld = p.atile ? 32 : p.lda; lim = p.M; r0 = m0; base = q * A_PART;
         gstep[u] = p.atile ? (size_t)p.atile * 32 : BK;
+      } else if constexpr (TR) {
+        // byte o of the padded [BK][ROWB] image: K-row o / ROWB, column (o % ROWB) / 2;
+        // padding and the tail past BK rows load row 0's first chunk again (unread)
+        ch = t - NA * A_INST;
+        const int o = ch * 1024 + lane * 16, kr = o / TrB<TN>::ROWB, cb = o % TrB<TN>::ROWB;
+        const bool pad = kr >= BK || cb >= TN * 2;
+        gsrc[u] = p.B[0] + (size_t)(pad ? 0 : kr) * p.ldb + min(n0 + (pad ? 0 : cb / 2), p.N - 8);
+        loff[u] = (uint32_t)(NA * A_PART + ch * 1024);
+        gstep[u] = (size_t)BK * p.ldb;
+        continue;
       } else {
         const int q = (t - NA * A_INST) / B_INST;
         ch = (t - NA * A_INST) % B_INST;
@@ -742,6 +776,9 @@ __device__ __forceinline__ void x3_big_tile(const X3Args& p, int t) {
   // byte offsets of this lane's fragment rows: chunk (2*kk + fh) of row fr
   const uint32_t cofs0 = (uint32_t)(fr * 64 + ((fh ^ sw) * 16));
   const uint32_t cofs1 = (uint32_t)(fr * 64 + (((2 + fh) ^ sw) * 16));
+  // TR: this lane's transposed-read address within a 32-column block (kk = 0)
+  const uint32_t trofs = (uint32_t)((8 * (lane >> 5) + ((lane & 15) >> 2)) * TrB<TN>::ROWB +
+                                    (16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * 2);
   const int nk = p.K / BK;
   issue(0, 0);
   for (int kt = 0; kt < nk; ++kt) {
@@ -761,11 +798,24 @@ __device__ __forceinline__ void x3_big_tile(const X3Args& p, int t) {
 #pragma unroll
         for (int i = 0; i < WM; ++i)
           af[q][i] = *(const half8*)(s + q * A_PART + (wm * WM * 32 + i * 32) * 64 + co);
+      if constexpr (TR) {
+        typedef short short4v __attribute__((ext_vector_type(4)));
+        typedef __attribute__((address_space(3))) short4v lds_s4;
 #pragma unroll
-      for (int q = 0; q < NB; ++q)
+        for (int j = 0; j < WN; ++j) {
+          const uint32_t a = lds_addr(s) + NA * A_PART + kk * 16 * TrB<TN>::ROWB + (wn * WN * 32 + j * 32) * 2 + trofs;
+          const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(size_t)a);
+          const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(size_t)(a + 4 * TrB<TN>::ROWB));
+          const short4v v8[2] = {lo, hi};
+          bf[0][j] = __builtin_bit_cast(half8, v8);
+        }
+      } else {
 #pragma unroll
-        for (int j = 0; j < WN; ++j)
-          bf[q][j] = *(const half8*)(s + NA * A_PART + q * B_PART + (wn * WN * 32 + j * 32) * 64 + co);
+        for (int q = 0; q < NB; ++q)
+#pragma unroll
+          for (int j = 0; j < WN; ++j)
+            bf[q][j] = *(const half8*)(s + NA * A_PART + q * B_PART + (wn * WN * 32 + j * 32) * 64 + co);
+      }
       if constexpr (MODE != X3_2X2) {  // lo, mid, hi times the weight (tier.cpp:940, 918)
 #pragma unroll
         for (int pa = 2; pa >= 0; --pa)
@@ -790,7 +840,7 @@ __device__ __forceinline__ void x3_big_tile(const X3Args& p, int t) {
   x3_store<WM, WN>(p, acc, m0 + wm * WM * 32, n0 + wn * WN * 32, lane);
 }
 
-template <int MODE, int TN>
+template <int MODE, int TN, bool TR = false>
 __global__ __launch_bounds__(512) void gemm_x3_big(const X3Args p) {
   // Workgroups go round-robin over the 8 XCDs, so XCD x gets the x-th eighth of
   // the tile sequence: a compact block of tiles (4 x 8 at 4096 x 5120) whose
@@ -798,7 +848,7 @@ __global__ __launch_bounds__(512) void gemm_x3_big(const X3Args p) {
   const int nt = ((p.M + XB_M - 1) / XB_M) * ((p.N + TN - 1) / TN);
   int t = blockIdx.x;
   if ((nt & 7) == 0) t = (t & 7) * (nt >> 3) + (t >> 3);
-  x3_big_tile<MODE, TN>(p, t);
+  x3_big_tile<MODE, TN, TR>(p, t);
 }
 
 // Grouped problems (routed experts): group g multiplies rows [row0[g], row0[g] +
@@ -836,9 +886,9 @@ int big_tn(int N) {
   return p352 < p320 ? 352 : 320;
 }
 
-template <int MODE, int TN>
+template <int MODE, int TN, bool TR = false>
 constexpr size_t big_lds() {
-  return 2 * (size_t)(X3Mode<MODE>::NA * XB_M + X3Mode<MODE>::NB * TN) * 64;
+  return 2 * ((size_t)X3Mode<MODE>::NA * XB_M * 64 + (TR ? TrB<TN>::PART : (size_t)X3Mode<MODE>::NB * TN * 64));
 }
 
 // ---- K chunks.  The fp32 accumulator's rounding error grows like sqrt(K): one
@@ -868,7 +918,7 @@ int run_k_chunks(const X3Args& a, L&& launch, S&& shift) {
     for (int i = 0; i < 3; ++i)
       if (q.A[i]) q.A[i] += k_offset(s0 * BK, q.atile);
     for (int i = 0; i < 2; ++i)
-      if (q.B[i]) q.B[i] += k_offset(s0 * BK, q.btile);
+      if (q.B[i]) q.B[i] += q.btr ? (size_t)s0 * BK * q.ldb : k_offset(s0 * BK, q.btile);
     shift(s0 * BK);
     q.K = (s1 - s0) * BK;
     if (c > 0) q.beta = 1.f;
@@ -882,15 +932,15 @@ int run_k_chunks(const X3Args& a, L&& launch) {
   return run_k_chunks(a, launch, [](int) {});
 }
 
-template <int MODE, int TN>
+template <int MODE, int TN, bool TR = false>
 int launch_x3_big_tn(const X3Args& a, hipStream_t s, const char* who) {
-  constexpr size_t lds = big_lds<MODE, TN>();
+  constexpr size_t lds = big_lds<MODE, TN, TR>();
   static_assert(lds <= 160 * 1024, "LDS budget");
   static std::atomic<uint64_t> attr{0};
-  int st = lds_attr_once(attr, (const void*)gemm_x3_big<MODE, TN>, (int)lds, who);
+  int st = lds_attr_once(attr, (const void*)gemm_x3_big<MODE, TN, TR>, (int)lds, who);
   if (st) return st;
   const int nt = ((a.M + XB_M - 1) / XB_M) * ((a.N + TN - 1) / TN);
-  gemm_x3_big<MODE, TN><<<nt, 512, lds, s>>>(a);
+  gemm_x3_big<MODE, TN, TR><<<nt, 512, lds, s>>>(a);
   TM_LAUNCH_CHECK(who);
   return TIERMM_OK;
 }
@@ -898,6 +948,11 @@ int launch_x3_big_tn(const X3Args& a, hipStream_t s, const char* who) {
 template <int MODE>
 int launch_x3_big(const X3Args& a, hipStream_t s, const char* who) {
   return run_k_chunks(a, [&](const X3Args& q) {
+    if constexpr (MODE == X3_REF || MODE == X3_REF_BF16) {
+      if (q.btr)
+        return big_tn(q.N) == 352 ? launch_x3_big_tn<MODE, 352, true>(q, s, who)
+                                  : launch_x3_big_tn<MODE, 320, true>(q, s, who);
+    }
     return big_tn(q.N) == 352 ? launch_x3_big_tn<MODE, 352>(q, s, who) : launch_x3_big_tn<MODE, 320>(q, s, who);
   });
 }
@@ -1203,6 +1258,14 @@ static int x3_gemm_impl(int opA, int m, int n, int k, const uint16_t* A, int lda
   if (st) return st;
   const uint16_t* At = A;
   int ldt = lda;
+  if (opA == TIERMM_OP_N && kp == k && m % 8 == 0 && lda % 8 == 0 && aligned16(A) && big_tiles(n, m) >= 192) {
+    // the big-tile kernel reads A ([k][lda], m contiguous) in place: no transpose
+    X3Args a{};
+    a.A[0] = parts; a.A[1] = parts + nk; a.A[2] = parts + 2 * nk;
+    a.B[0] = A; a.btr = 1;
+    a.lda = kp; a.ldb = lda; a.C = C; a.ldc = ldc; a.M = n; a.N = m; a.K = kp; a.beta = beta;
+    return bf16 ? launch_x3_big<X3_REF_BF16>(a, s, who) : launch_x3_big<X3_REF>(a, s, who);
+  }
   if (opA == TIERMM_OP_N) {
     // A is m x k column-major ([k][lda] in memory, the dX layout of tier.cpp:1226):
     // transpose it to [m][kp] so the product runs in the NT form below
