@@ -1347,13 +1347,17 @@ int tiermm_x3_rows_bf16(const uint16_t* W, const float* x, float* y, int M, int 
 
 
 // Weight rows the unfused fp32 path expands at a time: fp32 rows and their two-part
-// split take 8 bytes a weight, kept within kF32ExpandBytes in whole 320-row big tiles
-// (at least one such tile).
+// split take 8 bytes a weight, kept within kF32ExpandBytes in whole 320-row big tiles;
+// where N allows, at least the rows that give an M-row product 192 big tiles (the
+// big-tile kernel's threshold: 3840 rows at M = 4096, where smaller chunks ran on the
+// 128x128 kernel at half the speed).
 constexpr size_t kF32ExpandBytes = (size_t)256 << 20;
-static int f32_rows(int N, int kp) {
+static int f32_rows(int N, int kp, int M) {
   const size_t r = kF32ExpandBytes / ((size_t)kp * 8);
   if (r >= (size_t)N) return N;
-  return std::min(N, std::max(320, (int)(r / 320 * 320)));
+  const int ntm = (M + 255) / 256, big = (192 + ntm - 1) / ntm * 320;
+  const int bounded = std::max(320, (int)(r / 320 * 320));
+  return std::min(N, big <= N ? std::max(big, bounded) : bounded);
 }
 
 // tiermm_qgemm for dense rows (F32 / F16 / BF16) whose length K is not a multiple of
@@ -1382,7 +1386,7 @@ static int qgemm_padded(const void* W, int qtype, size_t rb, const float* X, flo
     }
   };
   if (mode == TIERMM_MODE_F32) {  // chunks of f32_rows weight rows, as in tiermm_qgemm
-    const int nc = f32_rows(N, kp);
+    const int nc = f32_rows(N, kp, M);
     uint8_t* b = (uint8_t*)w;
     float* wf = (float*)b;       b += al256((size_t)nc * kp * 4);
     uint16_t* whi = (uint16_t*)b; b += al256((size_t)nc * kp * 2);
@@ -1485,7 +1489,7 @@ size_t tiermm_qgemm_ws_bytes(int qtype, int M, int N, int K, int mode) {
   if (K % BK) {  // dense rows of an odd length: W and x padded to rows of Kp
     const size_t kp = (size_t)pad32(K);
     if (mode == TIERMM_MODE_F32) {  // a chunk of padded fp32 W rows, padded fp32 x, their two-part splits
-      const size_t nc = (size_t)f32_rows(N, (int)kp);
+      const size_t nc = (size_t)f32_rows(N, (int)kp, M);
       return al256(nc * kp * 4) + 2 * al256(nc * kp * 2) + al256(nc * 4) + al256((size_t)M * kp * 4) +
              2 * al256((size_t)M * kp * 2) + al256((size_t)M * 4);
     }
@@ -1496,7 +1500,7 @@ size_t tiermm_qgemm_ws_bytes(int qtype, int M, int N, int K, int mode) {
       return 2 * al256((size_t)M * K * 2) + al256((size_t)M * 4) + al256((size_t)N * 4) +
              qgemm_fused_partials_bytes(qtype, M, N, K, true);
     // a chunk of fp32 W rows, their two-part split, and x's
-    const size_t nc = (size_t)f32_rows(N, K);
+    const size_t nc = (size_t)f32_rows(N, K, M);
     return al256(nc * K * 4) + 2 * al256(nc * K * 2) + al256(nc * 4) + 2 * al256((size_t)M * K * 2) +
            al256((size_t)M * 4);
   }
@@ -1547,7 +1551,7 @@ int tiermm_qgemm(const void* W, int qtype, size_t rb, const float* X, float* Y, 
     // product -- here the two-part split GEMM (relative error ~2^-21 of fp64) over
     // chunks of f32_rows weight rows, each expanded to fp32 and split in the
     // workspace (the reference expands a bounded chunk too, tier.cpp:2225-2227)
-    const int nc = f32_rows(N, K);
+    const int nc = f32_rows(N, K, M);
     uint8_t* b = (uint8_t*)w;
     float* wf = (float*)b;                    b += al256((size_t)nc * K * 4);
     uint16_t* whi = (uint16_t*)b;             b += al256((size_t)nc * K * 2);
