@@ -175,6 +175,12 @@ def test_workspace_sizes():
     K = 20480
     assert tier_amd.qgemm_ws_bytes(tier_amd.Q4_0, 256, 14336, K, F32) == \
         1600 * K * 4 + 2 * 1600 * K * 2 + 1600 * 4 + 2 * 256 * K * 2 + 1024
+    # at M = 4096 the chunk grows to the 3840 rows that give the big-tile kernel its
+    # 192 tiles (16 x 12), where the weight has them
+    assert tier_amd.qgemm_ws_bytes(tier_amd.Q4_0, 4096, 14336, K, F32) == \
+        3840 * K * 4 + 2 * 3840 * K * 2 + 3840 * 4 + 2 * 4096 * K * 2 + 4096 * 4
+    assert tier_amd.qgemm_ws_bytes(tier_amd.Q4_0, 4096, 3000, K, F32) == \
+        1600 * K * 4 + 2 * 1600 * K * 2 + 1600 * 4 + 2 * 4096 * K * 2 + 4096 * 4
     # routed experts: 256-row tiles that fill the chip stage the fp16 weights of
     # up to 64 experts (1 GiB at most); few or mostly empty tiles keep one expert's
     E, N, K = 64, 1408, 2048
