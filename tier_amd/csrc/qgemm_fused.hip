@@ -42,6 +42,14 @@
 // distinct bank groups.  x comes in K-tiled planes (ktile_index) where the
 // caller's x allows it, so a fragment load is one contiguous kilobyte.
 //
+// F32 (tiermm_qgemm's TIERMM_MODE_F32, the chat prefill semantics, tier.cpp:2358-2359:
+// fp32 dequant and an fp32-accurate product): the same kernel with the x3-2x2
+// products.  x comes as the hi and lo planes of its two-part split with a power-of-two
+// exponent per row; the producers scale each fp32 q_val by its weight row's power of
+// two (qrow_exps, from the block scales) and emit hi = fp16(v) and lo = fp16(v - hi)
+// into two B planes of the stage (Emit<true>); the consumers run x_lo*W_hi, x_hi*W_lo
+// and x_hi*W_hi into one fp32 accumulator and store it scaled back by both exponents.
+//
 // Measured, q4_K at M = 512 (bench.py lines; x split and split-K reduce included):
 // 5120x5120 81 us, 14336x5120 195 us, 5120x14336 204 us, against 97-100,
 // 224-234 and 246-254 us when the producers streamed raw bytes through an LDS
