@@ -293,11 +293,16 @@ struct Unit<QT_Q8_0> {
       const float dv = h2f((d[i] >> sb) & 0xffffu);
       uint32_t w[4];
       q[i].get(sb ^ 16u, w);
+      // d*q as fma(d, q + 128, -128d): q + 128 is the byte with its top bit flipped
+      // (one xor for four, then v_cvt_f32_ubyte<n>); both forms are the exact d*q
+      const float dm = -128.f * dv;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
+        uint32_t wb = w[k] ^ 0x80808080u;
+        asm volatile("" : "+v"(wb));
         float f[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) f[e] = dv * (float)(int8_t)(uint8_t)(w[k] >> (8 * e));
+        for (int e = 0; e < 4; ++e) f[e] = fmaf(dv, (float)((wb >> (8 * e)) & 0xffu), dm);
         o.put(k, f[0], f[1], f[2], f[3]);
       }
     }
@@ -334,9 +339,11 @@ struct Unit<QT_Q5_0> {
         const uint32_t hb = (qh >> (16 * h + 4 * k)) & 15u;
         // bit e of hb to bit 4 of byte e
         const uint32_t v = ((qs[k] >> (4 * h)) & 0x0f0f0f0fu) | (((hb * 0x00204081u) & 0x01010101u) << 4);
+        // d*(q - 16) as fma(d, q, -16d): -16d is exact and the fma rounds the same
+        // real value once (the product is exact in either form)
         float f[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) f[e] = dv * ((float)((v >> (8 * e)) & 0xffu) - 16.f);
+        for (int e = 0; e < 4; ++e) f[e] = fmaf(dv, (float)((v >> (8 * e)) & 0xffu), -16.f * dv);
         o.put(k, f[0], f[1], f[2], f[3]);
       }
     }
@@ -425,9 +432,11 @@ struct Unit<QT_Q6_K> {
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const uint32_t v = ((wl[k] >> (4 * (t >> 1))) & 0x0f0f0f0fu) | (((wh[k] >> (2 * t)) & 0x03030303u) << 4);
+        // ds*(q - 32) as fma(ds, q, -32ds): -32ds is exact and both forms round the
+        // same real value once
         float f[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) f[e] = ds * ((float)((v >> (8 * e)) & 0xffu) - 32.f);
+        for (int e = 0; e < 4; ++e) f[e] = fmaf(ds, (float)((v >> (8 * e)) & 0xffu), -32.f * ds);
         o.put(k, f[0], f[1], f[2], f[3]);
       }
     }
