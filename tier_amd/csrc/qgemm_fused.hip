@@ -216,21 +216,17 @@ __device__ __forceinline__ float blk_bound(const uint8_t* row, int blk) {
 // F32 (the fp32-dequant semantics of tiermm_qgemm's TIERMM_MODE_F32): v = q_val * 2^e of
 // its row, split as x3s_split splits the fp32 dequant -- hi = fp16(v) into o, lo =
 // fp16(v - hi) into ol.
+// The producers fold 2^e into their block scales (scale()): exact, as scaling by a
+// power of two commutes with the rounding of q_val, so put() receives v itself.
 template <bool F32>
 struct Emit {
   uint32_t o[8], ol[8];
   float sc;  // 2^e of the row (F32)
+  __device__ __forceinline__ float scale(float d) const { return F32 ? d * sc : d; }
   __device__ __forceinline__ void put(int k, float f0, float f1, float f2, float f3) {
     if constexpr (!F32) {
       pack4(f0, f1, f2, f3, o[2 * k], o[2 * k + 1]);
     } else {
-      put_scaled(k, f0 * sc, f1 * sc, f2 * sc, f3 * sc);
-    }
-  }
-  // F32, values already scaled by 2^e (a producer that folds 2^e into its block scales:
-  // exact, as scaling by a power of two commutes with the rounding of q_val)
-  __device__ __forceinline__ void put_scaled(int k, float f0, float f1, float f2, float f3) {
-    if constexpr (F32) {
       float v[4] = {f0, f1, f2, f3};
       asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]));
       const h2v h0 = {(_Float16)v[0], (_Float16)v[1]}, h1 = {(_Float16)v[2], (_Float16)v[3]};
@@ -290,7 +286,7 @@ struct Unit<QT_Q8_0> {
     __device__ __forceinline__ void decode(const uint8_t* row, int k0, int t, int i, int h, E& o) const {
       const uint8_t* b = row + (size_t)k0 * 34;
       const uint32_t sb = sh_of(b);  // the q bytes at b + 2 + 16h sit at bit offset sb ^ 16
-      const float dv = h2f((d[i] >> sb) & 0xffffu);
+      const float dv = o.scale(h2f((d[i] >> sb) & 0xffffu));
       uint32_t w[4];
       q[i].get(sb ^ 16u, w);
       // d*q as fma(d, q + 128, -128d): q + 128 is the byte with its top bit flipped
@@ -331,7 +327,7 @@ struct Unit<QT_Q5_0> {
       // the block as if 4-aligned: S[j] = bytes 4j .. 4j + 3
       const uint32_t S0 = abit(a[1], a[0], sh), S1 = abit(a[2], a[1], sh), S2 = abit(a[3], a[2], sh),
                      S3 = abit(b[0], a[3], sh), S4 = abit(b[1], b[0], sh), S5 = abit(0u, b[1], sh);
-      const float dv = h2f(S0 & 0xffffu);
+      const float dv = o.scale(h2f(S0 & 0xffffu));
       const uint32_t qh = abit(S1, S0, 16);
       const uint32_t qs[4] = {abit(S2, S1, 16), abit(S3, S2, 16), abit(S4, S3, 16), abit(S5, S4, 16)};
 #pragma unroll
@@ -374,7 +370,7 @@ struct Unit<QT_Q5_K> {
       const int s = (k0 & 7) + t;
       int sc, mn;
       kq_scale_min(s, hd[1], hd[2], hd[3], sc, mn);
-      const float dsc = h2f(hd[0] & 0xffffu) * (float)sc, dm = h2f(hd[0] >> 16) * (float)mn;
+      const float dsc = o.scale(h2f(hd[0] & 0xffffu) * (float)sc), dm = o.scale(h2f(hd[0] >> 16) * (float)mn);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         uint32_t v = ((qs[i][k] >> (4 * t)) & 0x0f0f0f0fu) | (((qh[i][k] >> s) & 0x01010101u) << 4);
@@ -425,7 +421,7 @@ struct Unit<QT_Q6_K> {
                      T3 = abit(se, sw[3], sh), T4 = abit(0u, se, sh);
       const uint32_t Tw = t < 2 ? (a ? T2 : T0) : (a ? T3 : T1);
       const int sc = (int)(int8_t)(uint8_t)(Tw >> (16 * (t & 1) + 8 * h));
-      const float ds = h2f(T4 & 0xffffu) * (float)sc;
+      const float ds = o.scale(h2f(T4 & 0xffffu) * (float)sc);
       uint32_t wl[4], wh[4];
       (t & 1 ? l1[i] : l0[i]).get(sh, wl);
       qh[i].get(sh, wh);
@@ -589,8 +585,7 @@ __global__ __launch_bounds__(512) void qgemm_fused_x3ref(const QArgs p) {
           for (int t = 0; t < 2; ++t) {
             int sc, mn;
             kq_scale_min(((kq0 + q) & 7) + t, H[1], H[2], H[3], sc, mn);
-            // F32: 2^e folded into both scales
-            const float dsc = d * (float)sc * (F32 ? em.sc : 1.f), dm = dmin * (float)mn * (F32 ? em.sc : 1.f);
+            const float dsc = em.scale(d * (float)sc), dm = em.scale(dmin * (float)mn);
             uint8_t* bt = lds + ((q + t) % NBR) * BSLOT;
 #pragma unroll
             for (int i = 0; i < HPL; ++i) {
@@ -605,8 +600,7 @@ __global__ __launch_bounds__(512) void qgemm_fused_x3ref(const QArgs p) {
                 float f[4];
 #pragma unroll
                 for (int b = 0; b < 4; ++b) f[b] = fmaf(dsc, (float)((v >> (8 * b)) & 0xffu), -dm);
-                if constexpr (F32) em.put_scaled(w, f[0], f[1], f[2], f[3]);
-                else em.put(w, f[0], f[1], f[2], f[3]);
+                em.put(w, f[0], f[1], f[2], f[3]);
               }
               const uint32_t* o = em.o;
               *(u32x4*)(bt + swz(r, 2 * (h0 + i))) = u32x4{o[0], o[1], o[2], o[3]};
