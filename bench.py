@@ -145,15 +145,16 @@ def time_launches(hip, stream, launch, steps: int, warmup: int) -> float:
     return per
 
 
-def settle(hip, stream, launch, ms: float = 30.0) -> None:
-    """Untimed launches for `ms` milliseconds before a decode line's warm-up steps.  The
-    host-side input preparation (quantizing the weight) leaves the GPU idle for seconds,
-    and the clock controller then needs a few milliseconds of work to return to its
-    working clock: the 13824x5120 GEMV measured 9.05 us per step over the first 20 steps
-    after idle and 8.6-8.7 us once settled, same box."""
-    est = time_launches(hip, stream, launch, 4, 1)
-    for i in range(max(1, int(ms / max(est, 1e-3)))):
-        launch(i)
+def settle(hip, stream, tier_amd, case: GemvCase, ms: float = 30.0) -> None:
+    """Untimed back-to-back calls (issued from the C loop) for `ms` milliseconds before a
+    decode line's warm-up steps.  The host-side input preparation (quantizing the weight)
+    leaves the GPU idle for seconds, and the clock controller then needs milliseconds of
+    back-to-back work to return to its working clock: the 13824x5120 GEMV measured 9.05 us
+    per step over the first 20 steps after idle and 8.6-8.7 us once settled, and the
+    5120x5120 line 7.2 us over 50 steps after launches issued one by one from Python (which
+    leave the GPU idle between them) against 5.7-5.9 us after 3000 back-to-back calls."""
+    est = time_gemv(hip, stream, tier_amd, case, 4, 1)
+    case.launches(tier_amd, 0, max(1, int(ms / max(est, 1e-3))), stream)
     stream.synchronize()
 
 
@@ -520,7 +521,7 @@ def main() -> int:
     # ---------------------------------------------------------------- headline
     log("bench: preparing q4_K 13824x5120 GEMV inputs")
     head = GemvCase(tier_amd, hip, tier_amd.Q4_K, 13824, 5120, seed=3)
-    settle(hip, stream, lambda i: head.launch(tier_amd, i, stream))
+    settle(hip, stream, tier_amd, head)
     per = time_gemv(hip, stream, tier_amd, head, args.steps, args.warmup)
     wall = per * args.steps
     value = head.bytes * args.steps / (wall * 1e-3) / 1e9
@@ -531,7 +532,7 @@ def main() -> int:
     only = {n for n in args.secondary.split(",") if n}
     want = lambda name: not args.no_secondary and (not only or name in only)  # noqa: E731
     if not args.no_secondary:
-        reps, warm = max(20, args.steps // 4), 5
+        reps, warm = max(200, args.steps), 20
         for name, qt, N, K in (("q4_K_5120x5120_m1", tier_amd.Q4_K, 5120, 5120),
                                ("q4_K_14336x5120_m1", tier_amd.Q4_K, 14336, 5120),
                                ("q4_K_5120x14336_m1", tier_amd.Q4_K, 5120, 14336),
@@ -546,7 +547,7 @@ def main() -> int:
                 continue
             log(f"bench: {name}")
             c = GemvCase(tier_amd, hip, qt, N, K, seed=N + K)
-            settle(hip, stream, lambda i: c.launch(tier_amd, i, stream))
+            settle(hip, stream, tier_amd, c)
             km = time_gemv(hip, stream, tier_amd, c, reps, warm)
             secondary[name] = {"GB/s": round(c.bytes / (km * 1e-3) / 1e9, 1),
                                "frac_hbm": round(c.bytes / (km * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),

@@ -180,8 +180,7 @@ __global__ __launch_bounds__(64 * RT * KS) void qgemv_q4k_mfma(const uint8_t* __
   }
 
   // ---- reduce over the four lane groups of a row, then over the KS waves
-  acc += __shfl_xor(acc, 16, 64);
-  acc += __shfl_xor(acc, 32, 64);
+  acc = row_sum4(acc);
   if (KS > 1) {
     if (g == 0) red[wave * 16 + n] = acc;
     __syncthreads();

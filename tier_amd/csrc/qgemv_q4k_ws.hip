@@ -281,8 +281,7 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
           if (lane == 0) lds_rel(&done[slot * NCP + c], q);
         }
       }
-      acc += __shfl_xor(acc, 16, 64);
-      acc += __shfl_xor(acc, 32, 64);
+      acc = row_sum4(acc);
       if constexpr (OWN) {
         if (g == 0) red[(r * NC + c) * 16 + n] = acc;
       } else {

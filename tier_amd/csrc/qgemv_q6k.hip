@@ -242,8 +242,7 @@ __global__ __launch_bounds__(64 * RT * KS) void qgemv_q6k_mfma(const uint8_t* __
     return;
   }
 
-  acc += __shfl_xor(acc, 16, 64);
-  acc += __shfl_xor(acc, 32, 64);
+  acc = row_sum4(acc);
   if (KS > 1) {
     if (g == 0) red[wave * 16 + n] = acc;
     __syncthreads();

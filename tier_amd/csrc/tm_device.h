@@ -124,6 +124,17 @@ __device__ __forceinline__ void dma16_nt(const void* p, uint32_t lds_addr) {
                "s"(__builtin_amdgcn_readfirstlane(lds_addr))
                : "memory");
 }
+// Sum over the four 16-lane rows of a wave (lanes l, l ^ 16, l ^ 32, l ^ 48), as
+// (row0 + row1) + (row2 + row3) in every lane -- the sums two xor shuffles by 16 and
+// 32 give -- through gfx950's row-swap moves instead of two LDS-routed permutes:
+// with both operands a, permlane16_swap leaves rows (0,0,2,2) in one result and
+// (1,1,3,3) in the other, permlane32_swap the halves (lo,lo) and (hi,hi).
+__device__ __forceinline__ float row_sum4(float a) {
+  const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(a), false, false);
+  const float s = __uint_as_float(t[0]) + __uint_as_float(t[1]);
+  const auto u = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+  return __uint_as_float(u[0]) + __uint_as_float(u[1]);
+}
 template <int N>
 __device__ __forceinline__ void vm_wait() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
