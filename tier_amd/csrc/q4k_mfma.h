@@ -178,6 +178,61 @@ __device__ __forceinline__ float q4k_sb(const uint8_t* hp, int g, const i32x4 (&
   acc = fmaf(d, u, acc);
   return fmaf(-dmin, m, acc);
 }
+// The same with the high nibbles taken as 16 (q - 8) = (byte ^ 0x80) & 0xf0, one
+// v_bitop3 per word instead of a shift and a mask: the MFMAs of the high-nibble
+// sub-blocks (rows 4 sigma + digit, sigma odd) then give 16 q.x - 128 S(digit), so Ca and
+// Cb start from ca / cb = 128 S(digit) on those rows (q4k_hi_init) and the lanes that
+// read them (g odd) take 2^-e / 16 in mt (q4k_hi_scale).  Every intermediate is an exact
+// power-of-two multiple of q4k_sb's, so the result is the same to the bit.
+__device__ __forceinline__ float q4k_sb_hb(const uint8_t* hp, int g, const i32x4 (&A)[4], const float4 mt,
+                                           const i32x4 ca, const i32x4 cb, float acc) {
+  const u32x4 H = *(const u32x4*)hp;
+  const u32x4 cA = *(const u32x4*)(hp + 16 + 16 * g);
+  const u32x4 cB = *(const u32x4*)(hp + 80 + 16 * g);
+  i32x4 B0, B1, B2, B3;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    B0[w] = (int)(cA[w] & 0x0f0f0f0fu);
+    B1[w] = (int)((cA[w] ^ 0x80808080u) & 0xf0f0f0f0u);
+    B2[w] = (int)(cB[w] & 0x0f0f0f0fu);
+    B3[w] = (int)((cB[w] ^ 0x80808080u) & 0xf0f0f0f0u);
+  }
+  i32x4 Ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], B0, ca, 0, 0, 0);
+  Ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[1], B1, Ca, 0, 0, 0);
+  i32x4 Cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[2], B2, cb, 0, 0, 0);
+  Cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[3], B3, Cb, 0, 0, 0);
+  // |C| <= 16*32*15*128: 16 times q4k_sb's halves, still exact through the conversions
+  const float Da = fmaf((float)(Ca[3] * 256 + Ca[2]), 65536.f, (float)(Ca[1] * 256 + Ca[0]));
+  const float Db = fmaf((float)(Cb[3] * 256 + Cb[2]), 65536.f, (float)(Cb[1] * 256 + Cb[0]));
+  const int sh = 8 * g;
+  const uint32_t hy = H[1], hz = H[2], hw = H[3];
+  const int sca = (hy >> sh) & 63, mna = (hz >> sh) & 63;
+  const int scb = ((hw >> sh) & 15) | (((hy >> (sh + 6)) & 3) << 4);
+  const int mnb = ((hw >> (sh + 4)) & 15) | (((hz >> (sh + 6)) & 3) << 4);
+  const float d = h2f(H[0] & 0xffffu), dmin = h2f(H[0] >> 16);
+  const float u = fmaf((float)scb * mt.y, Db, (float)sca * mt.x * Da);
+  const float m = fmaf((float)mnb, mt.w, (float)mna * mt.z);
+  acc = fmaf(d, u, acc);
+  return fmaf(-dmin, m, acc);
+}
+// Accumulator starts of q4k_sb_hb for one super-block column: 128 times the digit sums
+// of the high-nibble A operands (A[1], A[3]) on their rows, zero on the others --
+// minus an MFMA against a B of -128 everywhere.
+__device__ __forceinline__ void q4k_hi_init(const i32x4 (&A)[4], i32x4& ca, i32x4& cb) {
+  const i32x4 neg = {(int)0x80808080u, (int)0x80808080u, (int)0x80808080u, (int)0x80808080u};
+  const i32x4 z = {0, 0, 0, 0};
+  ca = -__builtin_amdgcn_mfma_i32_16x16x64_i8(A[1], neg, z, 0, 0, 0);
+  cb = -__builtin_amdgcn_mfma_i32_16x16x64_i8(A[3], neg, z, 0, 0, 0);
+}
+// mt of q4k_sb_hb: the lanes whose accumulator rows are high-nibble sub-blocks (g odd)
+// take 2^-e / 16.
+__device__ __forceinline__ float4 q4k_hi_scale(float4 mt, int g) {
+  if (g & 1) {
+    mt.x *= 0.0625f;
+    mt.y *= 0.0625f;
+  }
+  return mt;
+}
 // The same with the A operands and metadata read from LDS: a0p / a1p = this
 // lane's A-operand rows for MFMA parities 0 / 1, mtp = the metadata.
 __device__ __forceinline__ float q4k_superblock(const uint8_t* hp, int g, const uint8_t* a0p, const uint8_t* a1p,

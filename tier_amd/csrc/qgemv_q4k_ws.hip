@@ -35,7 +35,10 @@
 // workgroup adds the NC partials of each row in a fixed order (13824x5120 8.51
 // against 8.57-8.64 us, 16384x8192 13.74-13.81 against 13.85-13.93); otherwise
 // the sums stay in registers until every stage is consumed and then go to the
-// ring, behind a second barrier.
+// ring, behind a second barrier.  Up to K = 8192 the q4_K consumers take the high
+// nibbles as 16 (q - 8) through one v_bitop3 per word (q4k_sb_hb), the offset folded
+// into each column's accumulator start: 8 fewer VALU instructions per column of ~59,
+// bit-identical (13824x5120 8.31-8.32 against 8.22-8.24 us; 16384x8192 within noise).
 //
 // Hand-off through LDS flags holding stage numbers, which only grow:
 //   full[slot][p] = q  -- producer p's rows of stage q have landed (its own
@@ -169,6 +172,10 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
   uint8_t* xq = xlds;
   float* meta = (float*)(xq + nsb * XQ_SB);
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // x holds NaN or +-Inf: read once the x preparation is published where registers allow
+  // (up to K = 8192), at the end otherwise
+  constexpr bool XEARLY = MS <= 4;
+  bool xbad = false;
 
   if (wave >= NC) {
     // ------------------------------------------------------------ producer
@@ -203,6 +210,7 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
     const int pro = min(D, total);
     for (int q = 0; q < pro; ++q) issue(q);
     __syncthreads();  // flags initialised; consumers have prepared x
+    if constexpr (XEARLY) xbad = flags_any(nf, NC);
     int marked = 0;   // stages marked full so far
     for (int q = D; q < total; ++q) {
       if (q >= NS) poll_ge<NCP>(done + (q % NS) * NCP, q - NS);
@@ -244,6 +252,7 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
     }
     publish_nonfinite(bad, nf, c, lane);
     __syncthreads();
+    if constexpr (XEARLY) xbad = flags_any(nf, NC);
     // this lane's A operands of its columns GS*gi + c + NC*i, m = gi*CPS + i
     // (zeros where it carries no digit)
     i32x4 A[MS][4];
@@ -260,6 +269,16 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
       A[m][3] = live1 ? *(const i32x4*)(ap + 3 * XQ_T) : z4;
       mt[m] = *(const float4*)(meta + sb * 16 + g * 4);
     }
+    // q4_K up to K = 8192: high nibbles through q4k_sb_hb (its accumulator starts per column)
+    constexpr bool HB = QT == QT_Q4_K && MS <= 4;
+    i32x4 hi0[HB ? MS : 1][2];
+    if constexpr (HB) {
+#pragma unroll
+      for (int m = 0; m < MS; ++m) {
+        q4k_hi_init(A[m], hi0[m][0], hi0[m][1]);
+        mt[m] = q4k_hi_scale(mt[m], g);
+      }
+    }
     // row n of a stage: producer n / 4's slot, row n % 4 of it; column c
     const uint8_t* rowbase = ring + (n / PROWS) * L::REGION + (n % PROWS) * PITCH + c * SBB;
     float part[OWN ? 1 : R];  // (!OWN) this consumer's sum of row n of each tile (lanes g == 0)
@@ -275,8 +294,12 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
 #pragma unroll
             for (int i = 0; i < CPS; ++i)
               if (c + NC * i < GS && GS * gi + c + NC * i < nsb)
-                acc = MfmaFmt<QT>::step_reg(rowbase + slot * SLOT + NC * i * SBB, g, A[gi * CPS + i],
-                                            mt[gi * CPS + i], acc);
+                if constexpr (HB)
+                  acc = q4k_sb_hb(rowbase + slot * SLOT + NC * i * SBB, g, A[gi * CPS + i], mt[gi * CPS + i],
+                                  hi0[gi * CPS + i][0], hi0[gi * CPS + i][1], acc);
+                else
+                  acc = MfmaFmt<QT>::step_reg(rowbase + slot * SLOT + NC * i * SBB, g, A[gi * CPS + i],
+                                              mt[gi * CPS + i], acc);
           }
           if (lane == 0) lds_rel(&done[slot * NCP + c], q);
         }
@@ -296,7 +319,7 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
     }
     __syncthreads();  // partial sums are in red[]
   }
-  if (flags_any(nf, NC)) {  // NaN or +-Inf in x: the rows take gemv_q's non-finite sums
+  if (XEARLY ? xbad : flags_any(nf, NC)) {  // NaN or +-Inf in x: the rows take gemv_q's non-finite sums
     for (int i = wave; i < R * 16; i += NC + NP) {
       const int r = i >> 4, n = i & 15;
       const int tile = (int)blockIdx.x + r * (int)gridDim.x;
