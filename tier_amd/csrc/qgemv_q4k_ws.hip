@@ -146,7 +146,9 @@ struct WsLayout {
 template <int QT, int R, int GS_, int NC, int NS, int D, int XP, int XK>
 __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __restrict__ W, size_t rb,
                                                             const float* __restrict__ x, float* __restrict__ y,
-                                                            int N, int K) {
+                                                            int N, int K, int G) {
+  // G = gridDim.x, passed as an argument: without a read of the grid size the kernel
+  // needs none of the implicit arguments, so its argument segment is 44 bytes, not 296
   using L = WsLayout<QT, GS_, NC, NS, R>;
   constexpr int SBB = MfmaFmt<QT>::SBB;
   constexpr int GS = L::GS, CPS = L::CPS, GRP = L::GRP, PITCH = L::PITCH, SLOT = L::SLOT, NLD = L::NLD,
@@ -196,7 +198,7 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
     auto issue = [&](int q) __attribute__((always_inline)) {
       const int r = q / ngrp, gi = q - r * ngrp;
       // a tile past the last one (its workgroup has fewer) re-reads the last tile
-      const int tile = min((int)blockIdx.x + r * (int)gridDim.x, tiles - 1);
+      const int tile = min((int)blockIdx.x + r * G, tiles - 1);
       const int rbase = min(tile * 16 + PROWS * p, N - 1), rmax = min(PROWS - 1, N - 1 - rbase);
       // bytes past the row's last super-block re-read the last valid 16 bytes
       const int lastb = min(GS, nsb - GS * gi) * SBB - 16;
@@ -322,7 +324,7 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
   if (XEARLY ? xbad : flags_any(nf, NC)) {  // NaN or +-Inf in x: the rows take gemv_q's non-finite sums
     for (int i = wave; i < R * 16; i += NC + NP) {
       const int r = i >> 4, n = i & 15;
-      const int tile = (int)blockIdx.x + r * (int)gridDim.x;
+      const int tile = (int)blockIdx.x + r * G;
       if (tile < tiles && tile * 16 + n < N) {
         const float s = nonfinite_terms<QT>(W + (size_t)(tile * 16 + n) * rb, x, 0, K, lane);
         if (lane == 0) y[tile * 16 + n] = s;
@@ -332,7 +334,7 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
   }
   for (int i = tid; i < R * 16; i += 64 * (NC + NP)) {
     const int r = i >> 4, n = i & 15;
-    const int tile = (int)blockIdx.x + r * (int)gridDim.x;
+    const int tile = (int)blockIdx.x + r * G;
     if (tile < tiles && tile * 16 + n < N) {
       float s = 0.f;
 #pragma unroll
@@ -353,7 +355,7 @@ int launch_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, 
   int st = lds_attr_once(attr, (const void*)qgemv_q4k_ws<QT, R, GS, NC, NS, D, XP, XK>, (int)L::LDS,
                          "tiermm_qgemv: q4_K LDS attribute");
   if (st) return st;
-  qgemv_q4k_ws<QT, R, GS, NC, NS, D, XP, XK><<<grid, 64 * (NC + NP), L::LDS, s>>>((const uint8_t*)W, rb, x, y, N, K);
+  qgemv_q4k_ws<QT, R, GS, NC, NS, D, XP, XK><<<grid, 64 * (NC + NP), L::LDS, s>>>((const uint8_t*)W, rb, x, y, N, K, (int)grid);
   TM_LAUNCH_CHECK("tiermm_qgemv: q4_K launch");
   return TIERMM_OK;
 }
