@@ -226,6 +226,67 @@ def bench_decoder_layer(tier_amd, hip, stream, T=4096, mode=None):
             "TFLOPS": round(tf, 1), "frac_x3_peak": round(tf / X3_PEAK_TFLOPS, 4), "per_matrix": out}
 
 
+def bench_decode_layer(tier_amd, hip, stream):
+    """Chat decode (M=1) over one config-4 layer, q4_K_S recipe (q/k/o/gate/up q4_K, v/down
+    q5_K): the 7 gemv_q calls chat_lin makes per layer (tier.cpp:2357), and the same with
+    q + k and gate + up each as one tiermm_qgemv_batch call (5 calls).  Two copies of the
+    layer's weights alternate (2 x 166 MiB > the 256 MiB MALL); x of each projection
+    ~N(0,1) (5120, 4096 for o, 14336 for down)."""
+    H, Q, KV, F = 5120, 4096, 1024, 14336
+    mats = (("q", tier_amd.Q4_K, Q, H), ("k", tier_amd.Q4_K, KV, H), ("v", tier_amd.Q5_K, KV, H),
+            ("o", tier_amd.Q4_K, H, Q), ("gate", tier_amd.Q4_K, F, H), ("up", tier_amd.Q4_K, F, H),
+            ("down", tier_amd.Q5_K, H, F))
+    rng = np.random.default_rng(21)
+    xs = {k: hip.to_device(rng.standard_normal(k).astype(np.float32)) for k in (H, Q, F)}
+    copies = []
+    nbytes = 0
+    for c in range(2):
+        d = {}
+        for name, qt, N, K in mats:
+            blocks = _quantized(tier_amd, qt, N, K, 300 + len(d))
+            d[name] = (hip.to_device(blocks), qt, N, K, tier_amd.q_row_bytes(qt, K), hip.DeviceBuffer(N * 4))
+            if c == 0:
+                nbytes += blocks.nbytes + K * 4 + N * 4
+        copies.append(d)
+    L = tier_amd.lib()
+    vp, ip = ctypes.c_void_p, ctypes.c_int
+
+    def single(j):
+        d = copies[j % 2]
+        for name, qt, N, K in mats:
+            W, _, _, _, rb, Y = d[name]
+            st = L.tiermm_qgemv(W.ptr, qt, rb, xs[K].ptr, Y.ptr, N, K, stream.handle)
+            if st:
+                raise RuntimeError(f"tiermm_qgemv {name}: {st}")
+
+    # the batched calls' argument arrays, built once per copy
+    plans = []
+    for d in copies:
+        calls = []
+        for group in (("q", "k"), ("v",), ("o",), ("gate", "up"), ("down",)):
+            qt, K, rb = d[group[0]][1], d[group[0]][3], d[group[0]][4]
+            n = len(group)
+            calls.append(((vp * n)(*[d[g][0].ptr for g in group]), qt, rb, xs[K].ptr,
+                          (vp * n)(*[d[g][5].ptr for g in group]), (ip * n)(*[d[g][2] for g in group]), n, K))
+        plans.append(calls)
+
+    def batched(j):
+        for w, qt, rb, x, y, ns, n, K in plans[j % 2]:
+            st = L.tiermm_qgemv_batch(w, qt, rb, x, y, ns, n, K, stream.handle)
+            if st:
+                raise RuntimeError(f"tiermm_qgemv_batch: {st}")
+
+    out = {"recipe": "q4_K_S (v, down q5_K)", "bytes_per_layer": nbytes}
+    for name, fn in (("single_calls", single), ("batched_qk_gateup", batched)):
+        est = time_launches(hip, stream, fn, 2, 1)
+        for i in range(max(1, int(30.0 / max(est, 1e-3)))):  # settle the clock
+            fn(i)
+        per = float(np.median([time_launches(hip, stream, fn, 200, 10) for _ in range(3)]))
+        out[name] = {"us": round(per * 1e3, 2), "GB/s": round(nbytes / (per * 1e-3) / 1e9, 1),
+                     "frac_hbm": round(nbytes / (per * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    return out
+
+
 def bench_decoder_layer_shared(tier_amd, hip, stream, T=4096):
     """Config 4's layer as the engine would issue it with x split once per activation
     (tiermm_split3_f16_ktiled, then tiermm_qgemm_x3parts on the K-tiled planes): one split
@@ -647,6 +708,9 @@ def main() -> int:
                            "us_per_call": round(km * 1e3, 1), "beta": beta,
                            "includes": "both operands' two-part splits (dX: column maxima + transposed split) + GEMM"}
         del Wf, Bm, C, WS
+    if want("decode_layer_m1"):
+        log("bench: decode layer M=1")
+        secondary["decode_layer_m1"] = bench_decode_layer(tier_amd, hip, stream)
     if want("decoder_layer_t4096"):
         secondary["decoder_layer_t4096"] = bench_decoder_layer(tier_amd, hip, stream)
     if want("decoder_layer_t4096_shared_splits"):

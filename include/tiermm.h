@@ -134,6 +134,18 @@ int tiermm_dequant(const void* W, int qtype, size_t rb, int cols, size_t r0, siz
  * from the signs (and zeros) of q_val(W_r, k). */
 int tiermm_qgemv(const void* W, int qtype, size_t rb, const float* x, float* y, int N, int K,
                  tiermm_stream_t stream);
+/* No counterpart in the reference as an entry point (chat_lin calls gemv_q once per
+ * matrix, tier.cpp:2357): gemv_q of count (1..TIERMM_QGEMV_BATCH) matrices that share
+ * x, K and the block type, e.g. the q and k projections of a layer, or gate and up.
+ * W, y and N are HOST arrays (W[i], y[i] device pointers; rows N[i] >= 0, y[i] may be
+ * null where N[i] == 0); rb, alignment and errors as tiermm_qgemv.  Where the whole-tile
+ * kernel takes the concatenated rows (q4_K / q5_K, K <= 5120) the matrices run as one
+ * launch, which saves a launch and a kernel tail per extra matrix (q4_K 4096x5120 +
+ * 1024x5120: 5.4 against 8.5 us); otherwise one tiermm_qgemv each.  Every y[i] is the
+ * same, bit for bit, as tiermm_qgemv on W[i]. */
+#define TIERMM_QGEMV_BATCH 4
+int tiermm_qgemv_batch(const void* const* W, int qtype, size_t rb, const float* x, float* const* y,
+                       const int* N, int count, int K, tiermm_stream_t stream);
 
 /* --------------------------------------------------------------- x3 splits */
 /* split3_fp_k (tier.cpp:869-870) / split3s_fp16 (tier.cpp:2192-2194):

@@ -66,6 +66,7 @@ EXPORTS = (
     "tiermm_qgemm_x3parts",
     "tiermm_qgemm_x3parts_ws_bytes",
     "tiermm_split3_f16_ktiled",
+    "tiermm_qgemv_batch",
 )
 
 
@@ -101,6 +102,7 @@ _sig("tiermm_q_info", [_i, ctypes.POINTER(_i), ctypes.POINTER(_i)])
 _sig("tiermm_q_row_bytes", [_i, _i, ctypes.POINTER(_sz)])
 _sig("tiermm_dequant", [_vp, _i, _sz, _i, _sz, _sz, _vp, _i, _vp])
 _sig("tiermm_qgemv", [_vp, _i, _sz, _vp, _vp, _i, _i, _vp])
+_sig("tiermm_qgemv_batch", [_vp, _i, _sz, _vp, _vp, _vp, _i, _i, _vp])
 _sig("tiermm_split3_f16", [_vp, _vp, _sz, _sz, _i, _vp])
 _sig("tiermm_x3_gemm", [_i, _i, _i, _i, _vp, _i, _vp, _f, _vp, _i, _vp, _sz, _vp])
 _sig("tiermm_x3_gemm_ws_bytes", [_i, _i, _i], _sz)
@@ -240,6 +242,22 @@ def dq_launch(W: int, qtype: int, rb: int, cols: int, r0: int, nrows: int, out: 
 def gemv_q(W: int, qtype: int, rb: int, x: int, y: int, N: int, K: int, stream=None) -> None:
     """gemv_q (tier.cpp:300): y[N] = dequant(W)[N][K] * x[K]."""
     _check(_L.tiermm_qgemv(W, qtype, rb, x, y, N, K, _s(stream)))
+
+
+QGEMV_BATCH = 4
+
+
+def gemv_q_batch(Ws, qtype: int, rb: int, x: int, ys, Ns, K: int, stream=None) -> None:
+    """gemv_q (tier.cpp:300) of up to QGEMV_BATCH matrices sharing x, K and the block type,
+    in one launch where the whole-tile kernel takes them (tiermm_qgemv_batch): ys[i][Ns[i]]
+    = dequant(Ws[i])[Ns[i]][K] * x[K], bit for bit as gemv_q on each."""
+    n = len(Ws)
+    if not (len(ys) == len(Ns) == n):
+        raise ValueError("gemv_q_batch: Ws, ys and Ns differ in length")
+    w = (ctypes.c_void_p * max(n, 1))(*Ws)
+    y = (ctypes.c_void_p * max(n, 1))(*ys)
+    ns = (ctypes.c_int * max(n, 1))(*Ns)
+    _check(_L.tiermm_qgemv_batch(w, qtype, rb, x, y, ns, n, K, _s(stream)))
 
 
 def split3(x: int, parts: int, n: int, stride: int | None = None, order: int = HML, stream=None) -> None:

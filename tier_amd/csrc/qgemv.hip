@@ -377,6 +377,9 @@ int qgemv_q4k(const void* W, size_t rb, const float* x, float* y, int N, int K, 
 int qgemv_q4k_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s);
 int qgemv_q5k_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s);
 bool qgemv_ws_takes(int qtype, int N, int K);
+bool qgemv_ws_batch_takes(int qtype, const int* N, int count, int K);
+int qgemv_ws_batch(const void* const* W, int qtype, size_t rb, const float* x, float* const* y, const int* N,
+                   int count, int K, hipStream_t s);
 bool qgemv_mfma_fits(const void* W, int qtype, size_t rb, int K);
 bool qgemv_q6k_fits(const void* W, size_t rb, int N, int K);
 int qgemv_q6k(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s);
@@ -434,6 +437,44 @@ extern "C" int tiermm_qgemv(const void* W, int qtype, size_t rb, const float* x,
   if ((qtype == QT_F32 || qtype == QT_F16 || qtype == QT_BF16) && ((uintptr_t)W % 16))
     return set_error(TIERMM_EINVAL, "tiermm_qgemv: dense rows must start 16-byte aligned");
   return qgemv_dispatch(W, qtype, rb, x, y, N, K, (hipStream_t)stream);
+}
+
+// gemv_q of up to TIERMM_QGEMV_BATCH matrices that share x, K and the block type.  Where
+// the whole-tile kernel takes their concatenated rows (q4_K / q5_K, K <= 5120, its tile
+// rule on the total) they run as one launch; otherwise one tiermm_qgemv each.  Either
+// way every y[i] is the same, bit for bit, as tiermm_qgemv on W[i].
+extern "C" int tiermm_qgemv_batch(const void* const* W, int qtype, size_t rb, const float* x, float* const* y,
+                                  const int* N, int count, int K, tiermm_stream_t stream) {
+  if (!W || !y || !N || count < 1 || count > TIERMM_QGEMV_BATCH)
+    return set_error(TIERMM_EINVAL, "tiermm_qgemv_batch: 1..%d matrices with weight, output and row arrays",
+                     TIERMM_QGEMV_BATCH);
+  const void* w[TIERMM_QGEMV_BATCH];
+  float* yy[TIERMM_QGEMV_BATCH];
+  int n[TIERMM_QGEMV_BATCH], live = 0;
+  for (int i = 0; i < count; ++i) {
+    if (N[i] < 0) return set_error(TIERMM_EINVAL, "tiermm_qgemv_batch: N[%d] < 0", i);
+    if (N[i] > 0) {  // matrices without rows take no part (their pointers are not read)
+      int st = check_qweight("tiermm_qgemv_batch", W[i], qtype, rb, K, 1);
+      if (st) return st;
+      if (!y[i]) return set_error(TIERMM_EINVAL, "tiermm_qgemv_batch: y[%d] is null", i);
+      w[live] = W[i];
+      yy[live] = y[i];
+      n[live++] = N[i];
+    }
+  }
+  if (!live) return TIERMM_OK;
+  if (!x || ((uintptr_t)x % 16)) return set_error(TIERMM_EINVAL, "tiermm_qgemv_batch: x must be 16-byte aligned");
+  hipStream_t s = (hipStream_t)stream;
+  bool fits = qgemv_ws_batch_takes(qtype, n, live, K);
+  for (int i = 0; fits && i < live && qtype == QT_Q5_K; ++i) fits = qgemv_mfma_fits(w[i], qtype, rb, K);
+  if (fits) return qgemv_ws_batch(w, qtype, rb, x, yy, n, live, K, s);
+  for (int i = 0; i < live; ++i) {
+    if ((qtype == QT_F32 || qtype == QT_F16 || qtype == QT_BF16) && ((uintptr_t)w[i] % 16))
+      return set_error(TIERMM_EINVAL, "tiermm_qgemv_batch: dense rows must start 16-byte aligned");
+    int st = qgemv_dispatch(w[i], qtype, rb, x, yy[i], n[i], K, s);
+    if (st) return st;
+  }
+  return TIERMM_OK;
 }
 
 extern "C" int tiermm_gemv(const void* W, int wtype, const float* x, float* y, int N, int K, tiermm_stream_t stream) {

@@ -143,10 +143,25 @@ struct WsLayout {
   static_assert((size_t)R * NC * 16 * 4 <= RING, "partial sums fit in the ring");
 };
 
-template <int QT, int R, int GS_, int NC, int NS, int D, int XP, int XK>
+// Several matrices with the same K and block type in one launch (tiermm_qgemv_batch):
+// matrix i owns tiles [t0[i], t0[i+1]) of the concatenated tile sequence, with rows
+// N[i], weight W[i] and output y[i]; entries past the batch have t0 = the tile count.
+// NB = 0: one matrix, given by the kernel's own arguments.
+constexpr int WS_BATCH = 4;
+template <int NB>
+struct WsMats {
+  const uint8_t* W[NB];
+  float* y[NB];
+  int t0[NB + 1];
+  int N[NB];
+};
+template <>
+struct WsMats<0> {};
+
+template <int QT, int R, int GS_, int NC, int NS, int D, int XP, int XK, int NB>
 __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __restrict__ W, size_t rb,
                                                             const float* __restrict__ x, float* __restrict__ y,
-                                                            int N, int K, int G) {
+                                                            int N, int K, int G, const WsMats<NB> mats) {
   // G = gridDim.x, passed as an argument: without a read of the grid size the kernel
   // needs none of the implicit arguments, so its argument segment is 44 bytes, not 296
   using L = WsLayout<QT, GS_, NC, NS, R>;
@@ -170,7 +185,27 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
   __shared__ float red_own[OWN ? R * NC * 16 : 1];
   float* red = OWN ? red_own : (float*)ring;
   const int nsb = K >> 8, ngrp = (nsb + GS - 1) / GS, total = R * ngrp;
-  const int tiles = (N + 15) >> 4;
+  int tiles;
+  if constexpr (NB == 0)
+    tiles = (N + 15) >> 4;
+  else
+    tiles = mats.t0[NB];
+  // tile t of the sequence: its matrix's weight, output, rows and tile index there
+  struct TileRef {
+    const uint8_t* W;
+    float* y;
+    int N, tile;
+  };
+  auto locate = [&](int t) __attribute__((always_inline)) {
+    if constexpr (NB == 0) {
+      return TileRef{W, y, N, t};
+    } else {
+      int m = 0;
+#pragma unroll
+      for (int i = 1; i < NB; ++i) m += t >= mats.t0[i] ? 1 : 0;
+      return TileRef{mats.W[m], mats.y[m], mats.N[m], t - mats.t0[m]};
+    }
+  };
   uint8_t* xq = xlds;
   float* meta = (float*)(xq + nsb * XQ_SB);
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -198,11 +233,11 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
     auto issue = [&](int q) __attribute__((always_inline)) {
       const int r = q / ngrp, gi = q - r * ngrp;
       // a tile past the last one (its workgroup has fewer) re-reads the last tile
-      const int tile = min((int)blockIdx.x + r * G, tiles - 1);
-      const int rbase = min(tile * 16 + PROWS * p, N - 1), rmax = min(PROWS - 1, N - 1 - rbase);
+      const TileRef tr = locate(min((int)blockIdx.x + r * G, tiles - 1));
+      const int rbase = min(tr.tile * 16 + PROWS * p, tr.N - 1), rmax = min(PROWS - 1, tr.N - 1 - rbase);
       // bytes past the row's last super-block re-read the last valid 16 bytes
       const int lastb = min(GS, nsb - GS * gi) * SBB - 16;
-      const uint8_t* b = W + (size_t)rbase * rb + (size_t)gi * GRP;
+      const uint8_t* b = tr.W + (size_t)rbase * rb + (size_t)gi * GRP;
       const uint32_t dst = ring_lds + (q % NS) * SLOT;
 #pragma unroll
       for (int j = 0; j < NLD; ++j)
@@ -295,13 +330,14 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
             poll_ge<NP>(full + NP * slot, q);
 #pragma unroll
             for (int i = 0; i < CPS; ++i)
-              if (c + NC * i < GS && GS * gi + c + NC * i < nsb)
+              if (c + NC * i < GS && GS * gi + c + NC * i < nsb) {
                 if constexpr (HB)
                   acc = q4k_sb_hb(rowbase + slot * SLOT + NC * i * SBB, g, A[gi * CPS + i], mt[gi * CPS + i],
                                   hi0[gi * CPS + i][0], hi0[gi * CPS + i][1], acc);
                 else
                   acc = MfmaFmt<QT>::step_reg(rowbase + slot * SLOT + NC * i * SBB, g, A[gi * CPS + i],
                                               mt[gi * CPS + i], acc);
+              }
           }
           if (lane == 0) lds_rel(&done[slot * NCP + c], q);
         }
@@ -324,54 +360,68 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
   if (XEARLY ? xbad : flags_any(nf, NC)) {  // NaN or +-Inf in x: the rows take gemv_q's non-finite sums
     for (int i = wave; i < R * 16; i += NC + NP) {
       const int r = i >> 4, n = i & 15;
-      const int tile = (int)blockIdx.x + r * G;
-      if (tile < tiles && tile * 16 + n < N) {
-        const float s = nonfinite_terms<QT>(W + (size_t)(tile * 16 + n) * rb, x, 0, K, lane);
-        if (lane == 0) y[tile * 16 + n] = s;
+      const int t = (int)blockIdx.x + r * G;
+      if (t < tiles) {
+        const TileRef tr = locate(t);
+        if (tr.tile * 16 + n < tr.N) {
+          const float s = nonfinite_terms<QT>(tr.W + (size_t)(tr.tile * 16 + n) * rb, x, 0, K, lane);
+          if (lane == 0) tr.y[tr.tile * 16 + n] = s;
+        }
       }
     }
     return;
   }
   for (int i = tid; i < R * 16; i += 64 * (NC + NP)) {
     const int r = i >> 4, n = i & 15;
-    const int tile = (int)blockIdx.x + r * G;
-    if (tile < tiles && tile * 16 + n < N) {
-      float s = 0.f;
+    const int t = (int)blockIdx.x + r * G;
+    if (t < tiles) {
+      const TileRef tr = locate(t);
+      if (tr.tile * 16 + n < tr.N) {
+        float s = 0.f;
 #pragma unroll
-      for (int c = 0; c < NC; ++c) s += red[(r * NC + c) * 16 + n];
-      y[tile * 16 + n] = s;
+        for (int c = 0; c < NC; ++c) s += red[(r * NC + c) * 16 + n];
+        tr.y[tr.tile * 16 + n] = s;
+      }
     }
   }
 }
 
-template <int QT, int R, int GS, int NC, int NS, int D, int XP, int XK>
-int launch_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
-  const unsigned grid = (unsigned)((N + 15) / 16 + R - 1) / R;
+template <int QT, int R, int GS, int NC, int NS, int D, int XP, int XK, int NB>
+int launch_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, const WsMats<NB>& mats, int tiles,
+              hipStream_t s) {
+  const unsigned grid = (unsigned)(tiles + R - 1) / R;
   using L = WsLayout<QT, GS, NC, NS, R>;
   static_assert(xq_bytes(XK) - ZERO_BYTES + 4 * NC + (R == 3 || R == 4 ? R * NC * 64 : 0) + L::LDS <= 160 * 1024,
                 "LDS budget (x digits, flags, partial sums, ring)");
   static_assert(XK / 16 <= 64 * NC * XP, "x preparation: one thread per 16 elements");
   static std::atomic<uint64_t> attr{0};
-  int st = lds_attr_once(attr, (const void*)qgemv_q4k_ws<QT, R, GS, NC, NS, D, XP, XK>, (int)L::LDS,
+  int st = lds_attr_once(attr, (const void*)qgemv_q4k_ws<QT, R, GS, NC, NS, D, XP, XK, NB>, (int)L::LDS,
                          "tiermm_qgemv: q4_K LDS attribute");
   if (st) return st;
-  qgemv_q4k_ws<QT, R, GS, NC, NS, D, XP, XK><<<grid, 64 * (NC + NP), L::LDS, s>>>((const uint8_t*)W, rb, x, y, N, K, (int)grid);
+  qgemv_q4k_ws<QT, R, GS, NC, NS, D, XP, XK, NB>
+      <<<grid, 64 * (NC + NP), L::LDS, s>>>((const uint8_t*)W, rb, x, y, N, K, (int)grid, mats);
   TM_LAUNCH_CHECK("tiermm_qgemv: q4_K launch");
   return TIERMM_OK;
 }
 
 // R = ceil(tiles / GTILE) tiles per workgroup (instantiated for 1-4, 6 and 8), so
 // the grid, ceil(tiles / R), stays at or below 256 workgroups up to 2048 tiles.
-template <int QT, int GS, int NC, int NS, int D, int XP, int XK>
-int launch_ws_r(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
-  const int tiles = (N + 15) / 16, r = (tiles + GTILE - 1) / GTILE;
+template <int QT, int GS, int NC, int NS, int D, int XP, int XK, int NB = 0>
+int launch_ws_r(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s,
+                const WsMats<NB>& mats = {}) {
+  int tiles;
+  if constexpr (NB == 0)
+    tiles = (N + 15) / 16;
+  else
+    tiles = mats.t0[NB];
+  const int r = (tiles + GTILE - 1) / GTILE;
   switch (r <= 4 ? r : r <= 6 ? 6 : 8) {
-    case 1: return launch_ws<QT, 1, GS, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
-    case 2: return launch_ws<QT, 2, GS, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
-    case 3: return launch_ws<QT, 3, GS, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
-    case 4: return launch_ws<QT, 4, GS, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
-    case 6: return launch_ws<QT, 6, GS, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
-    default: return launch_ws<QT, 8, GS, NC, NS, D, XP, XK>(W, rb, x, y, N, K, s);
+    case 1: return launch_ws<QT, 1, GS, NC, NS, D, XP, XK, NB>(W, rb, x, y, N, K, mats, tiles, s);
+    case 2: return launch_ws<QT, 2, GS, NC, NS, D, XP, XK, NB>(W, rb, x, y, N, K, mats, tiles, s);
+    case 3: return launch_ws<QT, 3, GS, NC, NS, D, XP, XK, NB>(W, rb, x, y, N, K, mats, tiles, s);
+    case 4: return launch_ws<QT, 4, GS, NC, NS, D, XP, XK, NB>(W, rb, x, y, N, K, mats, tiles, s);
+    case 6: return launch_ws<QT, 6, GS, NC, NS, D, XP, XK, NB>(W, rb, x, y, N, K, mats, tiles, s);
+    default: return launch_ws<QT, 8, GS, NC, NS, D, XP, XK, NB>(W, rb, x, y, N, K, mats, tiles, s);
   }
 }
 
@@ -414,6 +464,42 @@ int qgemv_q5k_ws(const void* W, size_t rb, const float* x, float* y, int N, int 
   if (K <= 5120) return launch_ws_r<QT_Q5_K, 10, 10, 4, 2, 1, 5120>(W, rb, x, y, N, K, s);
   if (K <= 8192) return launch_ws_r<QT_Q5_K, 8, 8, 4, 2, 1, 8192>(W, rb, x, y, N, K, s);
   return set_error(TIERMM_UNSUPPORTED, "tiermm_qgemv: q5_K K=%d above %d", K, 8192);
+}
+
+// Whether the whole-tile kernel takes a batch of `count` (2..WS_BATCH) q4_K or q5_K
+// matrices of K <= 5120 columns in one launch: it must take each matrix on its own, so
+// that each gets the arithmetic of its own call (a tile's sums do not depend on how
+// many tiles a workgroup streams).
+bool qgemv_ws_batch_takes(int qtype, const int* N, int count, int K) {
+  if ((qtype != QT_Q4_K && qtype != QT_Q5_K) || count < 2 || count > WS_BATCH || K > 5120) return false;
+  for (int i = 0; i < count; ++i)
+    if (!qgemv_ws_takes(qtype, N[i], K)) return false;
+  return true;
+}
+
+// The matrices of a batch (N[i] > 0, count <= WS_BATCH, qgemv_ws_batch_takes) in one
+// launch: each tile, its rows and its sums are those of a launch on its matrix alone,
+// so every y[i] is the same, bit for bit, as qgemv_q4k_ws / qgemv_q5k_ws on W[i].
+int qgemv_ws_batch(const void* const* W, int qtype, size_t rb, const float* x, float* const* y, const int* N,
+                   int count, int K, hipStream_t s) {
+  WsMats<WS_BATCH> m{};
+  int t = 0;
+  for (int i = 0; i < WS_BATCH; ++i) {
+    m.t0[i] = t;
+    if (i < count) {
+      m.W[i] = (const uint8_t*)W[i];
+      m.y[i] = y[i];
+      m.N[i] = N[i];
+      t += (N[i] + 15) / 16;
+    } else {
+      m.W[i] = (const uint8_t*)W[0];
+      m.y[i] = y[0];
+      m.N[i] = N[0];
+    }
+  }
+  m.t0[WS_BATCH] = t;
+  if (qtype == QT_Q4_K) return launch_ws_r<QT_Q4_K, 20, 8, 3, 1, 1, 5120, WS_BATCH>(W[0], rb, x, y[0], N[0], K, s, m);
+  return launch_ws_r<QT_Q5_K, 10, 10, 4, 2, 1, 5120, WS_BATCH>(W[0], rb, x, y[0], N[0], K, s, m);
 }
 
 }  // namespace tiermm
