@@ -131,6 +131,18 @@ def test_argument_checks_return_before_device_work():
     assert L.tiermm_dequant(16, tier_amd.F16, 24, 12, 0, 1, 17, tier_amd.OUT_F16, None) == tier_amd.EINVAL
     assert "2-byte aligned" in tier_amd.last_error()
     assert L.tiermm_qgemv(18, tier_amd.F16, 128, 16, 16, 1, 64, None) == tier_amd.EINVAL  # dense rows 16-aligned
+    # batched GEMV: batch size, negative rows, a misaligned weight of a live matrix, a null
+    # output of a live matrix, misaligned x; matrices without rows are not read
+    VP4, I4 = ctypes.c_void_p * 5, ctypes.c_int * 5
+    bq = lambda w, y, n, cnt, x=16: L.tiermm_qgemv_batch(VP4(*w), tier_amd.Q4_K, 144, x, VP4(*y), I4(*n), cnt, 256,
+                                                          None)
+    assert bq([16] * 5, [16] * 5, [16] * 5, 5) == tier_amd.EINVAL
+    assert bq([16] * 5, [16] * 5, [16] * 5, 0) == tier_amd.EINVAL
+    assert bq([16, 16, 0, 0, 0], [16, 16, 0, 0, 0], [16, -1, 0, 0, 0], 2) == tier_amd.EINVAL
+    assert bq([16, 18, 0, 0, 0], [16, 16, 0, 0, 0], [16, 16, 0, 0, 0], 2) == tier_amd.EINVAL
+    assert bq([16, 16, 0, 0, 0], [16, 0, 0, 0, 0], [16, 16, 0, 0, 0], 2) == tier_amd.EINVAL
+    assert bq([16, 16, 0, 0, 0], [16, 16, 0, 0, 0], [16, 16, 0, 0, 0], 2, x=20) == tier_amd.EINVAL
+    assert bq([0, 0, 0, 0, 0], [0, 0, 0, 0, 0], [0, 0, 0, 0, 0], 3) == tier_amd.OK  # no rows: nothing to do
     # chat set: slot count, null handles, registration checks (no HIP call on these paths)
     out = ctypes.c_void_p()
     assert L.tiermm_chat_create(1, None, ctypes.byref(out)) == tier_amd.EINVAL and not out.value
