@@ -459,26 +459,46 @@ def bench_moe(tier_amd, hip, stream):
                         "(64 experts each); no activation between"}
 
 
-def bench_floors(hip, stream, head: GemvCase, head_ms: float):
-    """What the hardware gives the two roofs on this box, from libtiermm_probe.so
-    (tier_amd/csrc/probe.hip): one read of the headline's bytes with nothing else to
-    do (non-temporal 16-byte loads, 2048 workgroups, over the same number of rotated
-    copies as the headline), and a register-only v_mfma_f32_32x32x16_f16 loop on
-    random-like operands (1024 workgroups x 4 waves x 8 independent accumulators)."""
-    lib = probe_lib()
-    nbytes = head.N * head.rb // 16 * 16
-    bufs = [hip.DeviceBuffer(nbytes) for _ in range(head.copies)]
+def _read_floor(hip, stream, lib, nbytes: int) -> float:
+    """Milliseconds per launch of one non-temporal read of `nbytes` (probe.hip read_once,
+    2048 workgroups), rotated over enough copies to exceed the MALL, as a GemvCase is."""
+    nbytes = nbytes // 16 * 16
+    copies = max(2, -(-(MALL_BYTES * 5 // 4) // nbytes))
+    bufs = [hip.DeviceBuffer(nbytes) for _ in range(copies)]
     for b in bufs:
         b.fill_bytes(1)
     out = hip.DeviceBuffer(1 << 16)
 
     def read(i):
-        if lib.tiermm_probe_read(bufs[i % head.copies].ptr, nbytes, 2048, 1, out.ptr, stream.handle):
+        if lib.tiermm_probe_read(bufs[i % copies].ptr, nbytes, 2048, 1, out.ptr, stream.handle):
             raise RuntimeError("tiermm_probe_read")
-    log("bench: read floor")
     rd = min(time_launches(hip, stream, read, 200, 20) for _ in range(3))
     for b in bufs:
         b.free()
+    return rd
+
+
+def bench_floors(hip, stream, head: GemvCase, head_ms: float, secondary=None):
+    """What the hardware gives the two roofs on this box, from libtiermm_probe.so
+    (tier_amd/csrc/probe.hip): one read of the headline's bytes with nothing else to
+    do (non-temporal 16-byte loads, 2048 workgroups, over the same number of rotated
+    copies as the headline) -- and of the weight bytes of the short decode lines, whose
+    time is mostly the fixed cost of a launch --, and a register-only
+    v_mfma_f32_32x32x16_f16 loop on random-like operands (1024 workgroups x 4 waves x 8
+    independent accumulators)."""
+    lib = probe_lib()
+    nbytes = head.N * head.rb // 16 * 16
+    log("bench: read floor")
+    rd = _read_floor(hip, stream, lib, nbytes)
+    short = {}
+    for name, wbytes in (("q4_K_5120x5120_m1", 5120 * 2880), ("q8_0_4096x4096_m1", 4096 * 4352),
+                         ("q4_K_5120x14336_m1", 5120 * 8064)):
+        r = _read_floor(hip, stream, lib, wbytes)
+        short[name] = {"bytes": wbytes, "us_per_launch": round(r * 1e3, 3),
+                       "frac_hbm": round(wbytes / (r * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        line = (secondary or {}).get(name)
+        if line:
+            short[name]["line_over_read"] = round(line["us_per_step"] / (r * 1e3), 3)
     seed = hip.to_device((np.arange(1024, dtype=np.uint64) * 2654435761 % (1 << 32)).astype(np.uint32))
     mo = hip.DeviceBuffer(1024 * 256 * 4)
 
@@ -492,6 +512,7 @@ def bench_floors(hip, stream, head: GemvCase, head_ms: float):
                           "GB/s": round(nbytes / (rd * 1e-3) / 1e9, 1),
                           "frac_hbm": round(nbytes / (rd * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                           "headline_over_read": round(head_ms / rd, 3)},
+            "read_once_short_lines": short,
             "mfma_f16": {"TFLOPS": round(tf, 1), "frac_dense_peak": round(tf / FP16_PEAK_TFLOPS, 4),
                          "x3_target_over_this": round(0.6 * FP16_PEAK_TFLOPS / tf, 4)}}
 
@@ -724,7 +745,7 @@ def main() -> int:
         secondary["chat_streamed_4_layers"] = bench_chat_stream(tier_amd, hip, stream)
 
     if want("floors"):
-        secondary["floors"] = bench_floors(hip, stream, head, per)
+        secondary["floors"] = bench_floors(hip, stream, head, per, secondary)
 
     traffic, traffic_src = measured_traffic()
     cpu = None

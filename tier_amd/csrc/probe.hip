@@ -15,10 +15,13 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // Every 16-byte word of [src, src + n16 * 16) is loaded once (non-temporal), U loads
 // in flight per thread; the XOR of all words decides whether one word is written, so
-// no load can be dropped.
+// no load can be dropped.  grid = gridDim.x, as an argument: like the decode GEMVs the
+// kernel then reads no implicit argument (a 28-byte argument segment, without the 256
+// bytes of implicit arguments a read of gridDim brings).
 template <int U>
-__global__ __launch_bounds__(256) void read_once(const u32x4* __restrict__ src, size_t n16, uint32_t* __restrict__ out) {
-  const size_t stride = (size_t)gridDim.x * 256 * U;
+__global__ __launch_bounds__(256) void read_once(const u32x4* __restrict__ src, size_t n16, uint32_t* __restrict__ out,
+                                                 int grid) {
+  const size_t stride = (size_t)grid * 256 * U;
   uint32_t acc = 0;
   for (size_t i = (size_t)blockIdx.x * 256 * U + threadIdx.x; i < n16; i += stride) {
     u32x4 v[U];
@@ -113,10 +116,10 @@ int tiermm_probe_read(const void* src, size_t bytes, int grid, int unroll, void*
   const size_t n16 = bytes / 16;
   const dim3 g((unsigned)grid), b(256);
   switch (unroll) {
-    case 1: read_once<1><<<g, b, 0, s>>>((const u32x4*)src, n16, (uint32_t*)out); break;
-    case 2: read_once<2><<<g, b, 0, s>>>((const u32x4*)src, n16, (uint32_t*)out); break;
-    case 4: read_once<4><<<g, b, 0, s>>>((const u32x4*)src, n16, (uint32_t*)out); break;
-    case 8: read_once<8><<<g, b, 0, s>>>((const u32x4*)src, n16, (uint32_t*)out); break;
+    case 1: read_once<1><<<g, b, 0, s>>>((const u32x4*)src, n16, (uint32_t*)out, grid); break;
+    case 2: read_once<2><<<g, b, 0, s>>>((const u32x4*)src, n16, (uint32_t*)out, grid); break;
+    case 4: read_once<4><<<g, b, 0, s>>>((const u32x4*)src, n16, (uint32_t*)out, grid); break;
+    case 8: read_once<8><<<g, b, 0, s>>>((const u32x4*)src, n16, (uint32_t*)out, grid); break;
     default: return 1;
   }
   return hipGetLastError() == hipSuccess ? 0 : -1;
