@@ -446,11 +446,16 @@ bool qgemv_ws_takes(int qtype, int N, int K) {
 // super-blocks (shorter rows re-read their last 16 bytes to fill the fixed load
 // count; still the fastest at K = 4096), 8 consumers with up to 3 columns each; up
 // to 8192 and up to 14336 stages of 8 super-blocks (whole-tile and 16-super-block
-// stages measured slower at 10240x8192: 10.8 against 10.1 us).
+// stages measured slower at 10240x8192: 10.8 against 10.1 us).  Up to 14336, where the
+// kernel takes 64..256 tiles, a ring of 5 slots with 3 stages in flight (the LDS the
+// 60 KB of x digits leave): 4096x14336 8.39 against 8.66 us for 4 slots and 2 in
+// flight, 1024 and 2048 rows within 1 %; 4 in flight lost (8.13 against 7.62 us at
+// 1024 rows).  At 320 tiles (5120x14336) the per-wave kernel stays faster (12.1 against
+// 12.3-14.5 us for these rings, two tiles a workgroup).
 int qgemv_q4k_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
   if (K <= 5120) return launch_ws_r<QT_Q4_K, 20, 8, 3, 1, 1, 5120>(W, rb, x, y, N, K, s);
   if (K <= 8192) return launch_ws_r<QT_Q4_K, 8, 8, 4, 2, 1, 8192>(W, rb, x, y, N, K, s);
-  if (K <= 14336) return launch_ws_r<QT_Q4_K, 8, 8, 4, 2, 2, 14336>(W, rb, x, y, N, K, s);
+  if (K <= 14336) return launch_ws_r<QT_Q4_K, 8, 8, 5, 3, 2, 14336>(W, rb, x, y, N, K, s);
   return set_error(TIERMM_UNSUPPORTED, "tiermm_qgemv: q4_K K=%d above %d", K, 14336);
 }
 
