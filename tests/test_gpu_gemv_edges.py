@@ -50,7 +50,9 @@ KERNELS = [
     (tier_amd.Q4_K, 1024, 14336, "q4K-whole-tile-k14336"),
     (tier_amd.Q4_K, 10240, 8192, "q4K-whole-tile-k8192"),
     (tier_amd.Q4_K, 512, 5120, "q4K-per-wave-1x4"),
-    (tier_amd.Q4_K, 5120, 14336, "q4K-per-wave-2x4"),
+    (tier_amd.Q4_K, 5120, 14336, "q4K-whole-tile-split-stages"),
+    (tier_amd.Q4_K, 8192, 14336, "q4K-whole-tile-k14336-2-tiles"),
+    (tier_amd.Q4_K, 9000, 14336, "q4K-per-wave-2x4"),
     (tier_amd.Q4_K, 512, 14336, "q4K-per-wave-1x8"),
     (tier_amd.Q5_K, 13824, 5120, "q5K-whole-tile"),
     (tier_amd.Q5_K, 1024, 5120, "q5K-whole-tile-1-tile"),

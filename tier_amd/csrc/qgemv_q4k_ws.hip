@@ -51,6 +51,7 @@
 // for stages <= q - NS < q - D, which all consumers can finish; consumers wait
 // only for stages that are issued and are marked full in order.
 #include <climits>
+#include <utility>
 
 #include "q4k_mfma.h"
 
@@ -125,6 +126,23 @@ constexpr WsPad ws_pad(int grp, int ns) {
   return best;
 }
 
+// Stages issued before the x barrier (at most the ring's NS slots).  At K = 14336 the x
+// preparation takes ~2.7 us, and with 3 stages (D) requested the loads ran dry before it
+// ended: 4 stages measured 4096x14336 8.04 against 8.41 us (5 stages: 8.37).  At K = 5120
+// a second whole tile up front lost (13824x5120 8.43 against 8.24 us).
+constexpr int ws_pre(int XK, int NS, int D) { return XK == 14336 ? 4 : D; }
+
+// Marks stages 0 .. PRE - D - 1 full as they land, after PRE stages of NLD loads each went out.
+template <int NLD, int PRE, int D, int... M>
+__device__ __forceinline__ void ws_mark_pre(std::integer_sequence<int, M...>, int* full, int p, int lane) {
+  (
+      [&] {
+        vm_wait<NLD * (PRE - 1 - M)>();
+        if (lane == 0) lds_rel(&full[NP * M + p], M);
+      }(),
+      ...);
+}
+
 template <int QT, int GS_, int NC, int NS, int R>
 struct WsLayout {
   static constexpr int GS = GS_;                                // super-blocks per stage
@@ -158,12 +176,58 @@ struct WsMats {
 template <>
 struct WsMats<0> {};
 
-template <int QT, int R, int GS_, int NC, int NS, int D, int XP, int XK, int NB>
+// Split stages (SK): with more row tiles than workgroups but fewer than two per
+// workgroup, whole tiles per workgroup leave CUs idle or load some workgroups with one
+// tile more than others.  Instead workgroup b takes the stages [T b / G, T (b + 1) / G)
+// of the tile-major stage sequence (T = tiles x stages per tile), so every workgroup
+// streams the same bytes to within one stage.  G <= tiles makes every range at least a
+// tile long, so a tile is shared by at most two workgroups, split at the boundary
+// between them.  Each of the two adds its part of the tile's rows; per row they meet in
+// one 64-bit slot of ws_pair (boundary b's 16 rows): each swaps its part in, and the one
+// that gets the other's part back writes y = lower part + upper part (a fixed order) and
+// empties the slot.  Nobody waits for anybody.  A slot carries the launch's epoch (a host
+// counter) beside the part's bits; an entry of another epoch (left by a call that
+// overlapped this one on the device) counts as empty.  Overlapping calls on one device
+// that take this path race (rows left unwritten, no hang); calls that do not overlap
+// always leave the slots empty.
+constexpr int WS_SK_GRID = GTILE;
+// How a workgroup's work is cut: R whole tiles (WS_TILES) or a range of stages (WS_STAGES).
+constexpr int WS_TILES = 0, WS_STAGES = 1;
+__device__ unsigned long long ws_pair[(WS_SK_GRID + 1) * 16];
+// a stored part is its bits ^ WS_SENT, never 0: a computed float is never the
+// signalling NaN 0x7fbadbad (arithmetic yields quiet NaNs)
+constexpr uint32_t WS_SENT = 0x7fbadbadu;
+template <bool SK>
+struct WsSplit {
+  unsigned epoch;
+};
+template <>
+struct WsSplit<false> {};
+
+// Leaves `part` (row n of boundary b's tile) in the slot or, when the other workgroup's
+// part was there, returns true with the row's sum in *sum: lower + upper.  One swap (a
+// compare-and-swap and then a take cost a second round trip to memory: 5120x14336
+// 11.69 against 11.35 us).
+__device__ __forceinline__ bool ws_pair_meet(int b, int n, unsigned epoch, bool upper, float part, float* sum) {
+  unsigned long long* p = ws_pair + b * 16 + n;
+  const unsigned long long mine = ((unsigned long long)epoch << 32) | (__float_as_uint(part) ^ WS_SENT);
+  const unsigned long long old = __hip_atomic_exchange(p, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (old == 0 || (unsigned)(old >> 32) != epoch) return false;  // the first here: the other takes it
+  __hip_atomic_store(p, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const float o = __uint_as_float((uint32_t)old ^ WS_SENT);
+  *sum = upper ? o + part : part + o;
+  return true;
+}
+
+template <int QT, int R, int GS_, int NC, int NS, int D, int XP, int XK, int NB, int SPLIT = WS_TILES>
 __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __restrict__ W, size_t rb,
                                                             const float* __restrict__ x, float* __restrict__ y,
-                                                            int N, int K, int G, const WsMats<NB> mats) {
+                                                            int N, int K, int G, const WsMats<NB> mats,
+                                                            const WsSplit<SPLIT == WS_STAGES> sk) {
   // G = gridDim.x, passed as an argument: without a read of the grid size the kernel
   // needs none of the implicit arguments, so its argument segment is 44 bytes, not 296
+  constexpr bool SK = SPLIT == WS_STAGES;
+  static_assert(!SK || NB == 0, "split stages serve one matrix");
   using L = WsLayout<QT, GS_, NC, NS, R>;
   constexpr int SBB = MfmaFmt<QT>::SBB;
   constexpr int GS = L::GS, CPS = L::CPS, GRP = L::GRP, PITCH = L::PITCH, SLOT = L::SLOT, NLD = L::NLD,
@@ -184,12 +248,23 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
   constexpr bool OWN = R == 3 || R == 4;
   __shared__ float red_own[OWN ? R * NC * 16 : 1];
   float* red = OWN ? red_own : (float*)ring;
-  const int nsb = K >> 8, ngrp = (nsb + GS - 1) / GS, total = R * ngrp;
+  const int nsb = K >> 8, ngrp = (nsb + GS - 1) / GS;
   int tiles;
   if constexpr (NB == 0)
     tiles = (N + 15) >> 4;
   else
     tiles = mats.t0[NB];
+  // this workgroup's stages: R whole tiles blockIdx.x, blockIdx.x + G, ...; or (SK) the
+  // range [s0, s1) of the stage sequence, whose first stage lies in tile t0
+  int total = R * ngrp, s0 = 0, s1 = 0, t0 = 0;
+  if constexpr (SK) {
+    // 32-bit: T * G <= 512 tiles x 56 stages x 256 workgroups
+    const unsigned T = (unsigned)(tiles * ngrp);
+    s0 = (int)(T * blockIdx.x / (unsigned)G);
+    s1 = (int)(T * (blockIdx.x + 1) / (unsigned)G);
+    t0 = s0 / ngrp;
+    total = s1 - s0;
+  }
   // tile t of the sequence: its matrix's weight, output, rows and tile index there
   struct TileRef {
     const uint8_t* W;
@@ -231,9 +306,17 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
     }
     const uint32_t ring_lds = lds_addr(ring + p * L::REGION);
     auto issue = [&](int q) __attribute__((always_inline)) {
-      const int r = q / ngrp, gi = q - r * ngrp;
-      // a tile past the last one (its workgroup has fewer) re-reads the last tile
-      const TileRef tr = locate(min((int)blockIdx.x + r * G, tiles - 1));
+      int tile, gi;
+      if constexpr (SK) {
+        tile = (s0 + q) / ngrp;
+        gi = s0 + q - tile * ngrp;
+      } else {
+        const int r = q / ngrp;
+        gi = q - r * ngrp;
+        // a tile past the last one (its workgroup has fewer) re-reads the last tile
+        tile = min((int)blockIdx.x + r * G, tiles - 1);
+      }
+      const TileRef tr = locate(tile);
       const int rbase = min(tr.tile * 16 + PROWS * p, tr.N - 1), rmax = min(PROWS - 1, tr.N - 1 - rbase);
       // bytes past the row's last super-block re-read the last valid 16 bytes
       const int lastb = min(GS, nsb - GS * gi) * SBB - 16;
@@ -244,12 +327,22 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
         if (j < NLD - 1 || L::LAST == 64 || lane < L::LAST)
           dma16_nt(b + (size_t)min(roff[j], rmax) * rb + min(coff[j], lastb), dst + j * 1024);
     };
-    const int pro = min(D, total);
+    // PRE stages go out before the x barrier when the workgroup has that many (the ring
+    // is empty), D otherwise; the steady loop keeps D in flight
+    constexpr int PRE = ws_pre(XK, NS, D);
+    const bool deep = PRE > D && total >= PRE;
+    const int pro = deep ? PRE : min(D, total);
     for (int q = 0; q < pro; ++q) issue(q);
     __syncthreads();  // flags initialised; consumers have prepared x
     if constexpr (XEARLY) xbad = flags_any(nf, NC);
     int marked = 0;   // stages marked full so far
-    for (int q = D; q < total; ++q) {
+    if constexpr (PRE > D) {
+      if (deep) {  // stage m has landed once at most PRE - 1 - m stages' loads are pending
+        ws_mark_pre<NLD, PRE, D>(std::make_integer_sequence<int, PRE - D>{}, full, p, lane);
+        marked = PRE - D;
+      }
+    }
+    for (int q = deep ? PRE : D; q < total; ++q) {
       if (q >= NS) poll_ge<NCP>(done + (q % NS) * NCP, q - NS);
       issue(q);
       vm_wait<NLD * D>();  // stage q - D has landed
@@ -324,8 +417,10 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
       float acc = 0.f;
 #pragma unroll
       for (int gi = 0; gi < MG; ++gi) {
-        if (gi < ngrp) {
-          const int q = r * ngrp + gi, slot = q % NS;
+        // q: this stage's place in the workgroup's sequence
+        const int q = SK ? (t0 + r) * ngrp + gi - s0 : r * ngrp + gi;
+        if (gi < ngrp && (!SK || (q >= 0 && q < total))) {
+          const int slot = q % NS;
           if (GS * gi + c < nsb) {
             poll_ge<NP>(full + NP * slot, q);
 #pragma unroll
@@ -357,49 +452,71 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
     }
     __syncthreads();  // partial sums are in red[]
   }
+  // the output row of row n of this workgroup's tile r (false: none), its tile in t
+  auto out_row = [&](int r, int n, int& t, TileRef& tr, int& row) __attribute__((always_inline)) {
+    t = SK ? t0 + r : (int)blockIdx.x + r * G;
+    if (SK ? t * ngrp >= s1 : t >= tiles) return false;  // (SK: the tile holds a stage of the range)
+    tr = locate(t);
+    row = tr.tile * 16 + n;
+    return row < tr.N;
+  };
   if (XEARLY ? xbad : flags_any(nf, NC)) {  // NaN or +-Inf in x: the rows take gemv_q's non-finite sums
+    // (a tile two workgroups share gets the same whole-row value from both)
     for (int i = wave; i < R * 16; i += NC + NP) {
       const int r = i >> 4, n = i & 15;
-      const int t = (int)blockIdx.x + r * G;
-      if (t < tiles) {
-        const TileRef tr = locate(t);
-        if (tr.tile * 16 + n < tr.N) {
-          const float s = nonfinite_terms<QT>(tr.W + (size_t)(tr.tile * 16 + n) * rb, x, 0, K, lane);
-          if (lane == 0) tr.y[tr.tile * 16 + n] = s;
-        }
+      int t, row;
+      TileRef tr;
+      if (out_row(r, n, t, tr, row)) {
+        const float s = nonfinite_terms<QT>(tr.W + (size_t)row * rb, x, 0, K, lane);
+        if (lane == 0) tr.y[row] = s;
       }
     }
     return;
   }
   for (int i = tid; i < R * 16; i += 64 * (NC + NP)) {
     const int r = i >> 4, n = i & 15;
-    const int t = (int)blockIdx.x + r * G;
-    if (t < tiles) {
-      const TileRef tr = locate(t);
-      if (tr.tile * 16 + n < tr.N) {
-        float s = 0.f;
+    int t, row;
+    TileRef tr;
+    if (out_row(r, n, t, tr, row)) {
+      float s = 0.f;
 #pragma unroll
-        for (int c = 0; c < NC; ++c) s += red[(r * NC + c) * 16 + n];
-        tr.y[tr.tile * 16 + n] = s;
+      for (int c = 0; c < NC; ++c) s += red[(r * NC + c) * 16 + n];
+      if constexpr (SK) {
+        // the tile began in the previous workgroup (this one holds its upper part), or
+        // goes on into the next one (this one holds its lower part)
+        const bool upper = t * ngrp < s0, lower = (t + 1) * ngrp > s1;
+        if (upper || lower) {
+          float sum;
+          if (ws_pair_meet((int)blockIdx.x + (upper ? 0 : 1), n, sk.epoch, upper, s, &sum)) tr.y[row] = sum;
+          continue;
+        }
       }
+      tr.y[row] = s;
     }
   }
 }
 
-template <int QT, int R, int GS, int NC, int NS, int D, int XP, int XK, int NB>
+template <int QT, int R, int GS, int NC, int NS, int D, int XP, int XK, int NB, int SPLIT = WS_TILES>
 int launch_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, const WsMats<NB>& mats, int tiles,
               hipStream_t s) {
-  const unsigned grid = (unsigned)(tiles + R - 1) / R;
+  // WS_STAGES: WS_SK_GRID workgroups (no more than the tiles)
+  constexpr bool SK = SPLIT == WS_STAGES;
+  const unsigned grid = SK ? (unsigned)min(tiles, WS_SK_GRID) : (unsigned)(tiles + R - 1) / R;
+  WsSplit<SK> sk;
+  if constexpr (SK) {
+    static std::atomic<unsigned> epoch{0};
+    sk.epoch = epoch.fetch_add(1, std::memory_order_relaxed);
+  }
   using L = WsLayout<QT, GS, NC, NS, R>;
   static_assert(xq_bytes(XK) - ZERO_BYTES + 4 * NC + (R == 3 || R == 4 ? R * NC * 64 : 0) + L::LDS <= 160 * 1024,
                 "LDS budget (x digits, flags, partial sums, ring)");
   static_assert(XK / 16 <= 64 * NC * XP, "x preparation: one thread per 16 elements");
   static std::atomic<uint64_t> attr{0};
-  int st = lds_attr_once(attr, (const void*)qgemv_q4k_ws<QT, R, GS, NC, NS, D, XP, XK, NB>, (int)L::LDS,
+  int st = lds_attr_once(attr, (const void*)qgemv_q4k_ws<QT, R, GS, NC, NS, D, XP, XK, NB, SPLIT>, (int)L::LDS,
                          "tiermm_qgemv: q4_K LDS attribute");
   if (st) return st;
-  qgemv_q4k_ws<QT, R, GS, NC, NS, D, XP, XK, NB>
-      <<<grid, 64 * (NC + NP), L::LDS, s>>>((const uint8_t*)W, rb, x, y, N, K, (int)grid, mats);
+  qgemv_q4k_ws<QT, R, GS, NC, NS, D, XP, XK, NB, SPLIT>
+      <<<grid, 64 * (NC + NP), L::LDS, s>>>((const uint8_t*)W, rb, x, y, N, K, (int)grid, mats, sk);
   TM_LAUNCH_CHECK("tiermm_qgemv: q4_K launch");
   return TIERMM_OK;
 }
@@ -428,14 +545,16 @@ int launch_ws_r(const void* W, size_t rb, const float* x, float* y, int N, int K
 }  // namespace
 
 // Which GEMVs take this kernel.  q4_K: from 64 row tiles up to K = 5120, from 640
-// up to 8192, and 64..256 tiles up to 14336 (one tile per workgroup; at 320 tiles
-// 160 workgroups of two lose to the per-wave kernel: 5120x14336 14.7 against
-// 12.9 us).  q5_K: from 64 row tiles up to K = 5120, from 640 up to 8192 (at
-// 5120x14336 the per-wave kernel is faster: 14.9 against 15.5 us).
+// up to 8192, 64..256 tiles up to 14336, and 257..512 tiles above 8192 (per-wave
+// kernel against this one: 5120x14336 12.1 against 11.1 us in split stages, 8192x14336
+// 14.4 against 13.7 us in two tiles a workgroup).  q5_K: from 64 row tiles up to
+// K = 5120, from 640 up to 8192 (at 5120x14336 the per-wave kernel is faster: 14.9
+// against 15.5 us).
 bool qgemv_ws_takes(int qtype, int N, int K) {
   const int tiles = (N + 15) / 16;
   if (qtype == QT_Q4_K)
-    return (K <= 5120 && tiles >= 64) || (K <= 8192 && tiles >= 640) || (K <= 14336 && tiles >= 64 && tiles <= 256);
+    return (K <= 5120 && tiles >= 64) || (K <= 8192 && tiles >= 640) || (K <= 14336 && tiles >= 64 && tiles <= 256) ||
+           (K > 8192 && K <= 14336 && tiles > 256 && tiles <= 512);
   if (qtype == QT_Q5_K) return (K <= 5120 && tiles >= 64) || (K <= 8192 && tiles >= 640);
   return false;
 }
@@ -450,11 +569,17 @@ bool qgemv_ws_takes(int qtype, int N, int K) {
 // kernel takes 64..256 tiles, a ring of 5 slots with 3 stages in flight (the LDS the
 // 60 KB of x digits leave): 4096x14336 8.39 against 8.66 us for 4 slots and 2 in
 // flight, 1024 and 2048 rows within 1 %; 4 in flight lost (8.13 against 7.62 us at
-// 1024 rows).  At 320 tiles (5120x14336) the per-wave kernel stays faster (12.1 against
-// 12.3-14.5 us for these rings, two tiles a workgroup).
+// 1024 rows).  Four of the stages go out before the x barrier (ws_pre).  From 257 to 384
+// tiles split stages (WS_STAGES): 5120x14336 11.1 us against 12.1 on the per-wave
+// kernel, 14.7 for 160 workgroups of two tiles; above that two tiles a workgroup.  At
+// K <= 5120 split stages need shorter stages and lost (5120x5120: 6.0-6.5 against
+// 5.4 us for 160 workgroups of two whole tiles).
 int qgemv_q4k_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
+  const int tiles = (N + 15) / 16;
   if (K <= 5120) return launch_ws_r<QT_Q4_K, 20, 8, 3, 1, 1, 5120>(W, rb, x, y, N, K, s);
   if (K <= 8192) return launch_ws_r<QT_Q4_K, 8, 8, 4, 2, 1, 8192>(W, rb, x, y, N, K, s);
+  if (K <= 14336 && tiles > WS_SK_GRID && tiles <= 384)  // ranges of 1-1.5 tiles' stages: at most 3 tiles each
+    return launch_ws<QT_Q4_K, 3, 8, 8, 5, 3, 2, 14336, 0, WS_STAGES>(W, rb, x, y, N, K, {}, tiles, s);
   if (K <= 14336) return launch_ws_r<QT_Q4_K, 8, 8, 5, 3, 2, 14336>(W, rb, x, y, N, K, s);
   return set_error(TIERMM_UNSUPPORTED, "tiermm_qgemv: q4_K K=%d above %d", K, 14336);
 }
