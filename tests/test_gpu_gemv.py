@@ -190,8 +190,8 @@ def test_gemv_long_k_launch_shapes(gpu, t, N):
     """K = 14336 around the launch-shape boundaries: q4_K takes the whole-tile kernel from
     64 to 256 row tiles (1024 and 4096 rows), in split stages from 257 to 384 (4100,
     6144), two tiles a workgroup from 385 to 512 (6160, 8192), and the per-wave kernel
-    outside (1000, 8200); q5_K and q8_0 switch at 256 tiles between one tile x eight K
-    parts and two tiles x four K parts per workgroup."""
+    outside (1000, 8200); q5_K the same from 64 tiles; q8_0 switches at 256 tiles between
+    one tile x eight K parts and two tiles x four K parts per workgroup."""
     K = 14336
     rng = np.random.default_rng(N + t)
     blocks = oracle.random_blocks(rng, t, N * (K // oracle.block(t)[0])).reshape(N, -1)
@@ -297,9 +297,10 @@ def test_gemv_from_a_tq_base(gpu, tmp_path):
 SPLIT = [(4100, 14336), (5120, 14336), (6000, 14336), (6144, 14336), (5000, 9216), (4500, 12800)]
 
 
+@pytest.mark.parametrize("t", [tier_amd.Q4_K, tier_amd.Q5_K])
 @pytest.mark.parametrize("N,K", SPLIT)
-def test_gemv_q4k_split_stages(gpu, N, K):
-    """q4_K with 257..384 row tiles above K = 8192: each workgroup streams an equal range of
+def test_gemv_split_stages(gpu, t, N, K):
+    """q4_K and q5_K with 257..384 row tiles above K = 8192: each workgroup streams an equal range of
     stages, and a tile split between two workgroups gets its rows from the two parts
     (lower + upper) through the pairing slots.  Partial last tiles (4100, 6000, 5000, 4500
     rows), a last stage shorter than the others (K = 9216: 36 super-blocks in stages of 8;
@@ -307,13 +308,12 @@ def test_gemv_q4k_split_stages(gpu, N, K):
     its other part is off by about half its value), every row written (NaN fill), and the
     same bits on repeated calls, also with another split shape in between (the slots are
     left empty by every call)."""
-    t = tier_amd.Q4_K
     blocks = quantized_weight(t, N, K, seed=N + K)
     x = activations(1, K, seed=N)[0]
     want = oracle.gemv_f64(blocks, t, x, N, K)
     rb = tier_amd.q_row_bytes(t, K)
     W, X, Y = hip.to_device(blocks), hip.to_device(x), hip.DeviceBuffer(N * 4)
-    o_blocks = quantized_weight(t, 5120, 14336, seed=3)
+    o_blocks = quantized_weight(tier_amd.Q4_K, 5120, 14336, seed=3)
     o_x = activations(1, 14336, seed=4)[0]
     OW, OX, OY = hip.to_device(o_blocks), hip.to_device(o_x), hip.DeviceBuffer(5120 * 4)
     runs = []
@@ -321,7 +321,8 @@ def test_gemv_q4k_split_stages(gpu, N, K):
         Y.fill_bytes(0xff)
         tier_amd.gemv_q(W.ptr, t, rb, X.ptr, Y.ptr, N, K)
         if i == 1:  # another split shape between the second and third call
-            tier_amd.gemv_q(OW.ptr, t, tier_amd.q_row_bytes(t, 14336), OX.ptr, OY.ptr, 5120, 14336)
+            tier_amd.gemv_q(OW.ptr, tier_amd.Q4_K, tier_amd.q_row_bytes(tier_amd.Q4_K, 14336), OX.ptr, OY.ptr, 5120,
+                            14336)
         hip.synchronize()
         runs.append(Y.download(np.float32, N))
     y = runs[0]
@@ -332,4 +333,4 @@ def test_gemv_q4k_split_stages(gpu, N, K):
     for r in runs[1:]:
         assert np.array_equal(r.view(np.uint32), y.view(np.uint32))
     oy = OY.download(np.float32, 5120)
-    assert oracle.rel_fro(oy, oracle.gemv_f64(o_blocks, t, o_x, 5120, 14336)) <= TOL
+    assert oracle.rel_fro(oy, oracle.gemv_f64(o_blocks, tier_amd.Q4_K, o_x, 5120, 14336)) <= TOL

@@ -57,6 +57,8 @@ KERNELS = [
     (tier_amd.Q5_K, 13824, 5120, "q5K-whole-tile"),
     (tier_amd.Q5_K, 1024, 5120, "q5K-whole-tile-1-tile"),
     (tier_amd.Q5_K, 512, 5120, "q5K-per-wave"),
+    (tier_amd.Q5_K, 5120, 14336, "q5K-whole-tile-split-stages"),
+    (tier_amd.Q5_K, 4096, 14336, "q5K-whole-tile-k14336"),
     (tier_amd.Q8_0, 4096, 4096, "q8_0-per-wave"),
     (tier_amd.Q8_0, 10240, 8192, "q8_0-per-wave-tall"),
     (tier_amd.Q6_K, 1024, 5120, "q6K"),

@@ -197,6 +197,7 @@ __device__ unsigned long long ws_pair[(WS_SK_GRID + 1) * 16];
 // a stored part is its bits ^ WS_SENT, never 0: a computed float is never the
 // signalling NaN 0x7fbadbad (arithmetic yields quiet NaNs)
 constexpr uint32_t WS_SENT = 0x7fbadbadu;
+std::atomic<unsigned> ws_epoch{0};  // one count for every launch in split stages
 template <bool SK>
 struct WsSplit {
   unsigned epoch;
@@ -503,10 +504,7 @@ int launch_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, 
   constexpr bool SK = SPLIT == WS_STAGES;
   const unsigned grid = SK ? (unsigned)min(tiles, WS_SK_GRID) : (unsigned)(tiles + R - 1) / R;
   WsSplit<SK> sk;
-  if constexpr (SK) {
-    static std::atomic<unsigned> epoch{0};
-    sk.epoch = epoch.fetch_add(1, std::memory_order_relaxed);
-  }
+  if constexpr (SK) sk.epoch = ws_epoch.fetch_add(1, std::memory_order_relaxed);
   using L = WsLayout<QT, GS, NC, NS, R>;
   static_assert(xq_bytes(XK) - ZERO_BYTES + 4 * NC + (R == 3 || R == 4 ? R * NC * 64 : 0) + L::LDS <= 160 * 1024,
                 "LDS budget (x digits, flags, partial sums, ring)");
@@ -548,14 +546,14 @@ int launch_ws_r(const void* W, size_t rb, const float* x, float* y, int N, int K
 // up to 8192, 64..256 tiles up to 14336, and 257..512 tiles above 8192 (per-wave
 // kernel against this one: 5120x14336 12.1 against 11.1 us in split stages, 8192x14336
 // 14.4 against 13.7 us in two tiles a workgroup).  q5_K: from 64 row tiles up to
-// K = 5120, from 640 up to 8192 (at 5120x14336 the per-wave kernel is faster: 14.9
-// against 15.5 us).
+// K = 5120, from 640 up to 8192, and 64..512 tiles above 8192 up to 14336.
 bool qgemv_ws_takes(int qtype, int N, int K) {
   const int tiles = (N + 15) / 16;
   if (qtype == QT_Q4_K)
     return (K <= 5120 && tiles >= 64) || (K <= 8192 && tiles >= 640) || (K <= 14336 && tiles >= 64 && tiles <= 256) ||
            (K > 8192 && K <= 14336 && tiles > 256 && tiles <= 512);
-  if (qtype == QT_Q5_K) return (K <= 5120 && tiles >= 64) || (K <= 8192 && tiles >= 640);
+  if (qtype == QT_Q5_K)
+    return (K <= 5120 && tiles >= 64) || (K <= 8192 && tiles >= 640) || (K > 8192 && K <= 14336 && tiles >= 64 && tiles <= 512);
   return false;
 }
 
@@ -587,13 +585,20 @@ int qgemv_q4k_ws(const void* W, size_t rb, const float* x, float* y, int N, int 
 // The same kernel on Q5_K (176-byte super-blocks; stages of 10 super-blocks up
 // to K = 5120 keep the ring within the LDS).  Against the per-wave kernel:
 // 13824x5120 10.8 against 12.5 us, 10240x8192 12.0 against 15.4 us, 5120x5120
-// 7.2 against 7.8 us.  Q8_0 (272-byte groups) gained nothing this way (a 3-slot
+// 7.2 against 7.8 us.  Above K = 8192 a 4-slot ring of 8-super-block stages, 2 in flight
+// (60 KB of x digits leave room for 4 slots; stages of 6 super-blocks spilled): 5120x14336
+// 12.7 against 14.0 us (split stages), 4096x14336 9.8 against 10.8, 8192x14336 15.7
+// against 17.0, 1024x14336 8.9 against 9.0.  Q8_0 (272-byte groups) gained nothing this way (a 3-slot
 // ring: 17.5 against 17.1 us at 13824x5120, 36.6 against 22.2 us at 10240x8192;
 // 4096x4096 whole-tile stages: 8.4 against 5.9 us) and keeps the per-wave kernel.
 int qgemv_q5k_ws(const void* W, size_t rb, const float* x, float* y, int N, int K, hipStream_t s) {
+  const int tiles = (N + 15) / 16;
   if (K <= 5120) return launch_ws_r<QT_Q5_K, 10, 10, 4, 2, 1, 5120>(W, rb, x, y, N, K, s);
   if (K <= 8192) return launch_ws_r<QT_Q5_K, 8, 8, 4, 2, 1, 8192>(W, rb, x, y, N, K, s);
-  return set_error(TIERMM_UNSUPPORTED, "tiermm_qgemv: q5_K K=%d above %d", K, 8192);
+  if (K <= 14336 && tiles > WS_SK_GRID && tiles <= 384)
+    return launch_ws<QT_Q5_K, 3, 8, 8, 4, 2, 2, 14336, 0, WS_STAGES>(W, rb, x, y, N, K, {}, tiles, s);
+  if (K <= 14336) return launch_ws_r<QT_Q5_K, 8, 8, 4, 2, 2, 14336>(W, rb, x, y, N, K, s);
+  return set_error(TIERMM_UNSUPPORTED, "tiermm_qgemv: q5_K K=%d above %d", K, 14336);
 }
 
 // Whether the whole-tile kernel takes a batch of `count` (2..WS_BATCH) q4_K or q5_K
