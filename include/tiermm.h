@@ -131,7 +131,10 @@ int tiermm_dequant(const void* W, int qtype, size_t rb, int cols, size_t r0, siz
  * rows (F32/F16/BF16) go to tiermm_gemv's kernel and must start 16-byte
  * aligned.  Non-finite x: y takes gemv_q's fp32 result classes exactly -- NaN
  * everywhere for a NaN in x, and for +-Inf at column k, +-Inf or NaN per row
- * from the signs (and zeros) of q_val(W_r, k). */
+ * from the signs (and zeros) of q_val(W_r, k).  q4_K / q5_K with 257..384 row tiles
+ * above K = 8192 pair workgroups through a small device-global table that every
+ * call leaves empty: such calls on one GPU must not overlap (order them on one
+ * stream), or rows of theirs may go unwritten. */
 int tiermm_qgemv(const void* W, int qtype, size_t rb, const float* x, float* y, int N, int K,
                  tiermm_stream_t stream);
 /* No counterpart in the reference as an entry point (chat_lin calls gemv_q once per
