@@ -1104,6 +1104,59 @@ __global__ __launch_bounds__(256) void qrow_exp_kernel(const uint8_t* __restrict
   if (lane == 0) wexp[n] = x3s_exp(b);
 }
 
+// The two passes of the fp32-semantics GEMM in one launch: blocks [0, M) split x's rows
+// (x3s_split_row), the rest take four weight rows each for their exponents, as
+// qrow_exp_kernel does.  Small products (the chat prefill's chunks of 256 rows) save a
+// launch and the gap behind it.
+template <int XR, int QT>
+__global__ __launch_bounds__(256) void f32_prep_kernel(const float* __restrict__ X, uint16_t* __restrict__ xhi,
+                                                      uint16_t* __restrict__ xlo, int32_t* __restrict__ xexp, int M,
+                                                      int K, const uint8_t* __restrict__ W, size_t rb, int N,
+                                                      int nblk, int32_t* __restrict__ wexp) {
+  if ((int)blockIdx.x < M) {
+    x3s_split_row<XR>(X, xhi, xlo, xexp, K, blockIdx.x);
+    return;
+  }
+  const int lane = threadIdx.x & 63;
+  const int n = ((int)blockIdx.x - M) * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const uint8_t* row = W + (size_t)n * rb;
+  float b = 0.f;
+  for (int i = lane; i < nblk; i += 64) b = fmaxf(b, blk_bound<QT>(row, i));
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) b = fmaxf(b, __shfl_xor(b, o, 64));
+  if (lane == 0) wexp[n] = x3s_exp(b);
+}
+
+template <int XR>
+int f32_prep_xr(const float* X, uint16_t* xhi, uint16_t* xlo, int32_t* xexp, int M, int K, const void* W, int qtype,
+                size_t rb, int N, int32_t* wexp, hipStream_t s) {
+  const unsigned grid = (unsigned)(M + (N + 3) / 4);
+  const uint8_t* w = (const uint8_t*)W;
+  switch (qtype) {
+    case QT_Q4_K: f32_prep_kernel<XR, QT_Q4_K><<<grid, 256, 0, s>>>(X, xhi, xlo, xexp, M, K, w, rb, N, K / 256, wexp); break;
+    case QT_Q5_K: f32_prep_kernel<XR, QT_Q5_K><<<grid, 256, 0, s>>>(X, xhi, xlo, xexp, M, K, w, rb, N, K / 256, wexp); break;
+    case QT_Q6_K: f32_prep_kernel<XR, QT_Q6_K><<<grid, 256, 0, s>>>(X, xhi, xlo, xexp, M, K, w, rb, N, K / 256, wexp); break;
+    case QT_Q8_0: f32_prep_kernel<XR, QT_Q8_0><<<grid, 256, 0, s>>>(X, xhi, xlo, xexp, M, K, w, rb, N, K / 32, wexp); break;
+    case QT_Q5_0: f32_prep_kernel<XR, QT_Q5_0><<<grid, 256, 0, s>>>(X, xhi, xlo, xexp, M, K, w, rb, N, K / 32, wexp); break;
+    default: return set_error(TIERMM_UNSUPPORTED, "f32_prep: type %d", qtype);
+  }
+  TM_LAUNCH_CHECK("tiermm_qgemm: split x, weight row exponents");
+  return TIERMM_OK;
+}
+
+// x's two-part split and W's row exponents in one launch where x takes the register
+// split (rows of a multiple of 4 up to 16384, 16-byte aligned; parts 8-byte aligned);
+// TIERMM_UNSUPPORTED (nothing launched, no error recorded) otherwise.
+int f32_prep(const float* X, uint16_t* xhi, uint16_t* xlo, int32_t* xexp, int M, int K, const void* W, int qtype,
+             size_t rb, int N, int32_t* wexp, hipStream_t s) {
+  if (K % 4 || ((uintptr_t)X & 15) || ((uintptr_t)xhi & 7) || ((uintptr_t)xlo & 7) || K > 16384)
+    return TIERMM_UNSUPPORTED;
+  if (K <= 4096) return f32_prep_xr<4>(X, xhi, xlo, xexp, M, K, W, qtype, rb, N, wexp, s);
+  if (K <= 8192) return f32_prep_xr<8>(X, xhi, xlo, xexp, M, K, W, qtype, rb, N, wexp, s);
+  return f32_prep_xr<16>(X, xhi, xlo, xexp, M, K, W, qtype, rb, N, wexp, s);
+}
+
 int qrow_exps(const void* W, int qtype, size_t rb, int N, int K, int32_t* wexp, hipStream_t s) {
   const unsigned grid = (unsigned)((N + 3) / 4);
   const uint8_t* w = (const uint8_t*)W;

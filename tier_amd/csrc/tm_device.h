@@ -71,6 +71,56 @@ __device__ __forceinline__ int x3s_exp(float amax) {
   return min(100, max(-100, 15 - ex));
 }
 
+__device__ __forceinline__ float block_max_256(float v, float* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  v = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  return v;
+}
+
+// The two-part split of row `row` of src (cols fp32, a multiple of 4, at most 1024 * XR;
+// rows 16-byte aligned) by a block of 256 threads, the row held in registers: hi, lo =
+// the fp16 parts of x * 2^e, exps[row] = e (x3s_exp of the row's max |x|).
+template <int XR>
+__device__ __forceinline__ void x3s_split_row(const float* __restrict__ src, uint16_t* __restrict__ hi,
+                                              uint16_t* __restrict__ lo, int32_t* __restrict__ exps, int cols,
+                                              int row) {
+  __shared__ float red[4];
+  const size_t base = (size_t)row * cols;
+  const int c4 = cols >> 2;
+  float4 v[XR];
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < XR; ++j) {
+    const int k = threadIdx.x + 256 * j;
+    v[j] = k < c4 ? ((const float4*)(src + base))[k] : make_float4(0.f, 0.f, 0.f, 0.f);
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+  }
+  amax = block_max_256(amax, red);
+  const int e = x3s_exp(amax);
+  const float sc = ldexpf(1.f, e);
+#pragma unroll
+  for (int j = 0; j < XR; ++j) {
+    const int k = threadIdx.x + 256 * j;
+    if (k >= c4) break;
+    const float f[4] = {v[j].x * sc, v[j].y * sc, v[j].z * sc, v[j].w * sc};
+    uint32_t h[2], l[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint16_t h0 = f2h(f[2 * q]), h1 = f2h(f[2 * q + 1]);
+      const uint16_t l0 = f2h(f[2 * q] - h2f(h0)), l1 = f2h(f[2 * q + 1] - h2f(h1));
+      h[q] = h0 | ((uint32_t)h1 << 16);
+      l[q] = l0 | ((uint32_t)l1 << 16);
+    }
+    ((uint2*)(hi + base))[k] = make_uint2(h[0], h[1]);
+    ((uint2*)(lo + base))[k] = make_uint2(l[0], l[1]);
+  }
+  if (threadIdx.x == 0) exps[row] = e;
+}
+
 // Hand-issued vector memory for the kernels that stream through LDS: the
 // compiler's wait insertion cannot follow global->LDS loads (it falls back to
 // waiting for everything before LDS reads), which would serialise the stream.

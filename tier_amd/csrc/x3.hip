@@ -46,6 +46,8 @@ bool qgemm_fusable(int qtype, const int* rows, int n, int N, int K, bool split, 
 // wexp[n] = the x3s exponent of a bound of weight row n's |q_val| (from the block
 // scales), rows [0, N) of K columns, for the fused fp32 kernels.
 int qrow_exps(const void* W, int qtype, size_t rb, int N, int K, int32_t* wexp, hipStream_t s);
+int f32_prep(const float* X, uint16_t* xhi, uint16_t* xlo, int32_t* xexp, int M, int K, const void* W, int qtype,
+             size_t rb, int N, int32_t* wexp, hipStream_t s);
 int device_cus(int* cus);
 
 namespace {
@@ -128,53 +130,13 @@ __global__ __launch_bounds__(256) void split3_vec8_kernel(const float* __restric
   }
 }
 
-__device__ __forceinline__ float block_max_256(float v, float* red) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  v = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  __syncthreads();
-  return v;
-}
-
 // One pass over a row held in registers: 4 consecutive elements per thread and
 // step (cols a multiple of 4, at most 1024 * XR; rows 16-byte aligned).
 template <int XR>
 __global__ __launch_bounds__(256) void x3s_split_reg_kernel(const float* __restrict__ src, uint16_t* __restrict__ hi,
                                                             uint16_t* __restrict__ lo, int32_t* __restrict__ exps,
                                                             int cols) {
-  __shared__ float red[4];
-  const size_t base = (size_t)blockIdx.x * cols;
-  const int c4 = cols >> 2;
-  float4 v[XR];
-  float amax = 0.f;
-#pragma unroll
-  for (int j = 0; j < XR; ++j) {
-    const int k = threadIdx.x + 256 * j;
-    v[j] = k < c4 ? ((const float4*)(src + base))[k] : make_float4(0.f, 0.f, 0.f, 0.f);
-    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
-  }
-  amax = block_max_256(amax, red);
-  const int e = x3s_exp(amax);
-  const float sc = ldexpf(1.f, e);
-#pragma unroll
-  for (int j = 0; j < XR; ++j) {
-    const int k = threadIdx.x + 256 * j;
-    if (k >= c4) break;
-    const float f[4] = {v[j].x * sc, v[j].y * sc, v[j].z * sc, v[j].w * sc};
-    uint32_t h[2], l[2];
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const uint16_t h0 = f2h(f[2 * q]), h1 = f2h(f[2 * q + 1]);
-      const uint16_t l0 = f2h(f[2 * q] - h2f(h0)), l1 = f2h(f[2 * q + 1] - h2f(h1));
-      h[q] = h0 | ((uint32_t)h1 << 16);
-      l[q] = l0 | ((uint32_t)l1 << 16);
-    }
-    ((uint2*)(hi + base))[k] = make_uint2(h[0], h[1]);
-    ((uint2*)(lo + base))[k] = make_uint2(l[0], l[1]);
-  }
-  if (threadIdx.x == 0) exps[blockIdx.x] = e;
+  x3s_split_row<XR>(src, hi, lo, exps, cols, blockIdx.x);
 }
 
 __global__ __launch_bounds__(256) void x3s_split_kernel(const float* __restrict__ src, uint16_t* __restrict__ hi,
@@ -1537,9 +1499,12 @@ int tiermm_qgemm(const void* W, int qtype, size_t rb, const float* X, float* Y, 
     int32_t* wexp = (int32_t*)b;              b += al256((size_t)N * 4);
     float* partials = (float*)b;
     const size_t xs = al256(mk * 2) / 2;
-    x3s_split_launch(X, xhi, xhi + xs, xexp, M, K, s);
-    TM_LAUNCH_CHECK("tiermm_qgemm: split x");
-    st = qrow_exps(W, qtype, rb, N, K, wexp, s);
+    st = f32_prep(X, xhi, xhi + xs, xexp, M, K, W, qtype, rb, N, wexp, s);  // both passes in one launch
+    if (st == TIERMM_UNSUPPORTED) {
+      x3s_split_launch(X, xhi, xhi + xs, xexp, M, K, s);
+      TM_LAUNCH_CHECK("tiermm_qgemm: split x");
+      st = qrow_exps(W, qtype, rb, N, K, wexp, s);
+    }
     if (st) return st;
     int cus = 0;
     st = device_cus(&cus);
