@@ -129,6 +129,38 @@ class Stream:
             self.handle = None
 
 
+class Graph:
+    """The work ``record(stream)`` issues on ``stream``, captured once (relaxed mode) and
+    instantiated; ``launch`` replays it on a stream."""
+
+    def __init__(self, stream: Stream, record):
+        h = lib()
+        s = ctypes.c_void_p(stream.handle)
+        check(h.hipStreamBeginCapture(s, 2), "hipStreamBeginCapture")  # hipStreamCaptureModeRelaxed
+        g = ctypes.c_void_p()
+        try:
+            record(stream)
+        finally:
+            err = h.hipStreamEndCapture(s, ctypes.byref(g))
+        check(err, "hipStreamEndCapture")
+        self.graph = g.value
+        ex = ctypes.c_void_p()
+        check(h.hipGraphInstantiate(ctypes.byref(ex), ctypes.c_void_p(self.graph), None, None, ctypes.c_size_t(0)),
+              "hipGraphInstantiate")
+        self.exec = ex.value
+
+    def launch(self, stream: Stream) -> None:
+        check(lib().hipGraphLaunch(ctypes.c_void_p(self.exec), ctypes.c_void_p(stream.handle)), "hipGraphLaunch")
+
+    def destroy(self) -> None:
+        if self.exec:
+            check(lib().hipGraphExecDestroy(ctypes.c_void_p(self.exec)), "hipGraphExecDestroy")
+            self.exec = None
+        if self.graph:
+            check(lib().hipGraphDestroy(ctypes.c_void_p(self.graph)), "hipGraphDestroy")
+            self.graph = None
+
+
 class Event:
     def __init__(self):
         e = ctypes.c_void_p()
