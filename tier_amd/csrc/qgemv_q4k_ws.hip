@@ -229,6 +229,11 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
   // needs none of the implicit arguments, so its argument segment is 44 bytes, not 296
   constexpr bool SK = SPLIT == WS_STAGES;
   static_assert(!SK || NB == 0, "split stages serve one matrix");
+  // q4_K in split stages: the split tiles' parts meet early (the first tile's part is left
+  // as soon as it is summed, the last tile's partner part taken while the consumers finish):
+  // 5120x14336 11.12 -> 10.90 us.  q5_K keeps both meetings at the end (the early ones
+  // spilled 4 more registers there: 12.97 -> 13.79 us).
+  constexpr bool EARLY = SK && QT == QT_Q4_K;
   using L = WsLayout<QT, GS_, NC, NS, R>;
   constexpr int SBB = MfmaFmt<QT>::SBB;
   constexpr int GS = L::GS, CPS = L::CPS, GRP = L::GRP, PITCH = L::PITCH, SLOT = L::SLOT, NLD = L::NLD,
@@ -249,6 +254,10 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
   constexpr bool OWN = R == 3 || R == 4;
   __shared__ float red_own[OWN ? R * NC * 16 : 1];
   float* red = OWN ? red_own : (float*)ring;
+  // SK: consumers past the first tile's partial sums; what the early swaps of the split
+  // tiles got back ([0, 16): the last tile's take, [16, 32): the first tile's deposit)
+  __shared__ int first_in[1];
+  __shared__ unsigned long long met[SK ? 32 : 1];
   const int nsb = K >> 8, ngrp = (nsb + GS - 1) / GS;
   int tiles;
   if constexpr (NB == 0)
@@ -294,6 +303,7 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
     // ------------------------------------------------------------ producer
     const int p = wave - NC;
     if (lane < NS) full[NP * lane + p] = -1;
+    if (p == 0 && lane == 0) first_in[0] = 0;
     if (p == 0)  // consumer flags; padding entries never hold a wait back
       for (int i = lane; i < NS * NCP; i += 64) done[i] = (i % NCP) < NC ? -1 : INT_MAX;
     // byte f of a slot: row f / PITCH of the producer's 4, byte f % PITCH of its
@@ -353,6 +363,15 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
     vm_wait<0>();
     for (; marked < total; ++marked)
       if (lane == 0) lds_rel(&full[NP * (marked % NS) + p], marked);
+    if constexpr (EARLY) {
+      // the last tile goes on into the next workgroup, which left its part of it early
+      // (its first tile): take it now, while the consumers finish, so that the round trip
+      // is not at the end
+      const int tl = (s1 - 1) / ngrp;
+      if (p == 0 && (tl + 1) * ngrp > s1 && lane < 16 && tl * 16 + lane < N)
+        met[lane] = __hip_atomic_exchange(ws_pair + ((int)blockIdx.x + 1) * 16 + lane, 0ull, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+    }
     if constexpr (!OWN) __syncthreads();  // every stage consumed: the ring is free
     __syncthreads();                         // partial sums are in red[]
   } else {
@@ -413,6 +432,8 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
     // row n of a stage: producer n / 4's slot, row n % 4 of it; column c
     const uint8_t* rowbase = ring + (n / PROWS) * L::REGION + (n % PROWS) * PITCH + c * SBB;
     float part[OWN ? 1 : R];  // (!OWN) this consumer's sum of row n of each tile (lanes g == 0)
+    unsigned long long upswap = 0;  // SK: what the deposit of the first tile's part got back
+    bool upmine = false;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       float acc = 0.f;
@@ -444,7 +465,28 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
       } else {
         part[r] = acc;
       }
+      if constexpr (EARLY) {
+        if (r == 0 && t0 * ngrp < s0) {
+          // the first tile began in the previous workgroup: the last consumer done with it
+          // leaves its part (the sum of the consumers' partials, in the final loop's order)
+          // for that workgroup now, long before the end
+          int old = 0;
+          if (lane == 0) old = __hip_atomic_fetch_add(first_in, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+          old = __shfl(old, 0, 64);
+          if (old == NC - 1 && lane < 16 && t0 * 16 + lane < N) {
+            float sp = 0.f;
+#pragma unroll
+            for (int cc = 0; cc < NC; ++cc) sp += red[cc * 16 + lane];
+            const unsigned long long mine = ((unsigned long long)sk.epoch << 32) | (__float_as_uint(sp) ^ WS_SENT);
+            upswap = __hip_atomic_exchange(ws_pair + (int)blockIdx.x * 16 + lane, mine, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+            upmine = true;
+          }
+        }
+      }
     }
+    if constexpr (EARLY)
+      if (upmine) met[16 + lane] = upswap;
     if constexpr (!OWN) {
       __syncthreads();  // every stage consumed: the ring is free
       if (g == 0)
@@ -461,6 +503,46 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
     row = tr.tile * 16 + n;
     return row < tr.N;
   };
+  // SK: the split tiles' meetings end here, before both branches below, so that every call
+  // leaves the table empty.  EARLY: the first tile's part was deposited already (a part
+  // the other workgroup had left first means this one sums the row), and the last tile's
+  // partner part taken (met[n]), else it is deposited now (ws_pair_meet).  Otherwise
+  // both parts meet here (ws_pair_meet).
+  float ssum = 0.f;
+  bool split = false, swrite = false;
+  if constexpr (SK) {
+    if (tid < R * 16) {
+      const int r = tid >> 4, n = tid & 15;
+      int t, row;
+      TileRef tr;
+      if (out_row(r, n, t, tr, row)) {
+        const bool upper = t * ngrp < s0, lower = (t + 1) * ngrp > s1;
+        if (upper || lower) {
+          split = true;
+          float sp = 0.f;
+#pragma unroll
+          for (int c = 0; c < NC; ++c) sp += red[(r * NC + c) * 16 + n];
+          const unsigned long long o = EARLY ? met[upper ? 16 + n : n] : 0ull;
+          const bool theirs = o != 0 && (unsigned)(o >> 32) == sk.epoch;
+          const float other = __uint_as_float((uint32_t)o ^ WS_SENT);
+          if (!EARLY) {
+            swrite = ws_pair_meet((int)blockIdx.x + (upper ? 0 : 1), n, sk.epoch, upper, sp, &ssum);
+          } else if (upper) {
+            if (theirs) {  // the other part was there before this one: take it off the table
+              __hip_atomic_store(ws_pair + (int)blockIdx.x * 16 + n, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              ssum = other + sp;  // lower + upper
+              swrite = true;
+            }
+          } else if (theirs) {
+            ssum = sp + other;
+            swrite = true;
+          } else {
+            swrite = ws_pair_meet((int)blockIdx.x + 1, n, sk.epoch, false, sp, &ssum);
+          }
+        }
+      }
+    }
+  }
   if (XEARLY ? xbad : flags_any(nf, NC)) {  // NaN or +-Inf in x: the rows take gemv_q's non-finite sums
     // (a tile two workgroups share gets the same whole-row value from both)
     for (int i = wave; i < R * 16; i += NC + NP) {
@@ -479,19 +561,13 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
     int t, row;
     TileRef tr;
     if (out_row(r, n, t, tr, row)) {
+      if (SK && split) {  // a split tile's row: written by the workgroup that met the other part
+        if (swrite) tr.y[row] = ssum;
+        continue;
+      }
       float s = 0.f;
 #pragma unroll
       for (int c = 0; c < NC; ++c) s += red[(r * NC + c) * 16 + n];
-      if constexpr (SK) {
-        // the tile began in the previous workgroup (this one holds its upper part), or
-        // goes on into the next one (this one holds its lower part)
-        const bool upper = t * ngrp < s0, lower = (t + 1) * ngrp > s1;
-        if (upper || lower) {
-          float sum;
-          if (ws_pair_meet((int)blockIdx.x + (upper ? 0 : 1), n, sk.epoch, upper, s, &sum)) tr.y[row] = sum;
-          continue;
-        }
-      }
       tr.y[row] = s;
     }
   }
