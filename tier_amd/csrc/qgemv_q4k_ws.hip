@@ -302,6 +302,10 @@ __global__ __launch_bounds__(64 * (NC + NP)) void qgemv_q4k_ws(const uint8_t* __
   if (wave >= NC) {
     // ------------------------------------------------------------ producer
     const int p = wave - NC;
+    // up to K = 5120 the producers issue ahead of the consumers' VALU work on their SIMD
+    // (13824x5120 8.20 -> 8.15 us, 5120x5120 5.36 -> 5.28); above it this lost 6-8 %
+    // (4096x14336 8.01 -> 8.66 us)
+    if constexpr (XK <= 5120) __builtin_amdgcn_s_setprio(1);
     if (lane < NS) full[NP * lane + p] = -1;
     if (p == 0 && lane == 0) first_in[0] = 0;
     if (p == 0)  // consumer flags; padding entries never hold a wait back
